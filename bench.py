@@ -1,0 +1,234 @@
+"""Benchmark of the MI355X fp32 matmul path (BASELINE.json metric: fp32 GEMM/BMM TFLOP/s and %
+of the MI355X FP32 matrix peak at 4096^3).
+
+One step = the three GEMMs of BASELINE config 4 on synthetic N(0, 1/64) data resident in HBM:
+  NN  C  = A  * B      (forward)
+  NT  dA = dC * B^T    (autograd gradient of A)
+  TN  dB = A^T * dC    (autograd gradient of B)
+each M = N = K = 4096, 2*4096^3 FLOP. `value` is the whole step's FLOP / wall time.
+
+Prints ONE JSON line on stdout. Extra per-configuration measurements (--configs all) go to
+stderr. The CPU baseline is the oracle's restatement of the reference matmul_tiled arithmetic
+(oracle/oracle.c, kind "port") timed on the host cores on a bounded row sample.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense FP32 matrix peak (AMD public specification)
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--configs", default="main", choices=["main", "all"],
+                   help="'all' also measures every BASELINE config (reported on stderr)")
+    p.add_argument("--cpu-seconds", type=float, default=12.0,
+                   help="target duration of the bounded CPU-baseline sample")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args()
+
+
+def cpu_baseline(target_s):
+    """Oracle restatement of matmul_tiled (fp32 fma chains, ascending k) on host cores, on
+    a growing row sample of the 4096^3 NN GEMM until ~target_s of CPU work."""
+    import oracle
+    n = 4096
+    threads = min(16, os.cpu_count() or 1)
+    A = oracle.uniform((n, n), 3, 0)
+    B = oracle.uniform((n, n), 3, 1)
+    rows = max(threads, 16)
+    elapsed = 0.0
+    while True:
+        t0 = time.perf_counter()
+        oracle.matmul_rows(A, B, 0, rows, threads=threads)
+        elapsed = time.perf_counter() - t0
+        if elapsed >= target_s / 4 or rows >= n:
+            break
+        rows = min(n, int(rows * max(2.0, (target_s / 4) / max(elapsed, 1e-3))))
+    # final timed sample sized to about target_s
+    rows = min(n, max(rows, int(rows * target_s / max(elapsed, 1e-3))))
+    t0 = time.perf_counter()
+    oracle.matmul_rows(A, B, 0, rows, threads=threads)
+    elapsed = time.perf_counter() - t0
+    flop = 2.0 * rows * n * n
+    return {"value": flop / elapsed / 1e12, "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"rows 0..{rows} of the 4096^3 NN GEMM ({flop / 1e9:.1f} GFLOP) with the "
+                      f"oracle's matmul_tiled restatement (fp32 fma chains, ascending k), "
+                      f"{threads} threads, {elapsed:.1f} s",
+            "openmp": bool(oracle.lib().oracle_openmp_enabled())}
+
+
+class Timer:
+    """HIP events on torch's current stream -- the stream every migemm launch uses."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs = []
+
+    def around(self, fn):
+        s = self.torch.cuda.Event(enable_timing=True)
+        e = self.torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        self.pairs.append((s, e))
+
+    def mean_ms(self):
+        self.torch.cuda.synchronize()
+        return float(np.mean([s.elapsed_time(e) for s, e in self.pairs]))
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: every GPU box here has one "
+                                   "MI355X, and the matmul path shards without collectives "
+                                   "(see the sharding paragraph of the design notes); run "
+                                   "with --gpus 1"}))
+        sys.exit(2)
+
+    import torch
+    from my_pytchon_opencl_lib_amd import NnClGlob, _native
+
+    nncl = NnClGlob("cuda:0")
+    dev = torch.device("cuda:0")
+    n = 4096
+    flop = 2.0 * n * n * n
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    std = 1.0 / 64.0
+    A = torch.randn(n, n, device=dev, generator=gen) * std
+    B = torch.randn(n, n, device=dev, generator=gen) * std
+    dC = torch.randn(n, n, device=dev, generator=gen) * std
+    C = torch.empty(n, n, device=dev)
+    dA = torch.empty(n, n, device=dev)
+    dB = torch.empty(n, n, device=dev)
+
+    forms = {
+        "NN": lambda: nncl.gemm(A, B, out=C),
+        "NT": lambda: nncl.gemm(dC, B, transB=True, out=dA),
+        "TN": lambda: nncl.gemm(A, dC, transA=True, out=dB),
+    }
+    timers = {k: Timer(torch) for k in forms}
+
+    for _ in range(args.warmup):
+        for f in forms.values():
+            f()
+    torch.cuda.synchronize()
+
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        for k, f in forms.items():
+            timers[k].around(f)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+
+    per_form = {}
+    for k, t in timers.items():
+        ms = t.mean_ms()
+        per_form[k] = {"ms": round(ms, 4), "tflops": round(flop / (ms * 1e-3) / 1e12, 2)}
+    dominant = max(per_form, key=lambda k: per_form[k]["ms"])
+    dom_ms = per_form[dominant]["ms"]
+    achieved = flop / (dom_ms * 1e-3) / 1e12
+    value = 3 * flop / (ms_per_step * 1e-3) / 1e12
+
+    extra = {}
+    if args.configs == "all":
+        extra = measure_all_configs(torch, nncl, _native)
+        print(json.dumps({"configs": extra}, indent=1), file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(args.cpu_seconds)
+
+    line = {
+        "metric": "fp32 GEMM/BMM TFLOP/s and % of MI355X FP32 matrix peak at 4096^3",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: A, B, dC ~ N(0, 1/64) fp32 in HBM (torch generator, seed 3)",
+        "config": {"workload": "BASELINE config 4: fp32 4096x4096x4096 NN forward + NT "
+                               "(dA = dC*B^T) + TN (dB = A^T*dC), one step = all three",
+                   "M": n, "N": n, "K": n, "forms": per_form,
+                   "pct_of_fp32_matrix_peak": round(100 * value / PEAK_FP32_MFMA_TFLOPS, 2),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": f"gemm_mfma_kernel ({dominant} form)",
+                     "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def measure_all_configs(torch, nncl, _native, reps=50):
+    """Per-config kernel time (mean of HIP-event timed launches) for DESIGN.md."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    out = {}
+
+    def timed(fn, reps=reps):
+        for _ in range(5):
+            fn()
+        t = Timer(torch)
+        for _ in range(reps):
+            t.around(fn)
+        return t.mean_ms()
+
+    def rec(name, ms, flop, byts):
+        out[name] = {"us": round(ms * 1e3, 2), "tflops": round(flop / (ms * 1e-3) / 1e12, 3),
+                     "pct_mfma_peak": round(100 * flop / (ms * 1e-3) / 1e12 /
+                                            PEAK_FP32_MFMA_TFLOPS, 2),
+                     "GBps": round(byts / (ms * 1e-3) / 1e9, 1),
+                     "pct_hbm_peak": round(100 * byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2)}
+
+    r = lambda *s: torch.rand(*s, device=dev, generator=g) * 2 - 1
+    A = r(256, 256)
+    B = r(256, 256)
+    rec("1_nn_256", timed(lambda: nncl.gemm(A, B)), 2 * 256 ** 3, 4 * 3 * 256 * 256)
+    Q, Kt, P, V = r(32, 128, 64), r(32, 64, 128), r(32, 128, 128), r(32, 128, 64)
+    rec("2a_bmm_qk", timed(lambda: nncl.BmmPermute(Q, Kt)), 2 * 32 * 128 * 128 * 64,
+        4 * 32 * (128 * 64 * 2 + 128 * 128))
+    rec("2b_bmm_pv", timed(lambda: nncl.BmmPermute(P, V)), 2 * 32 * 128 * 128 * 64,
+        4 * 32 * (128 * 128 + 128 * 64 * 2))
+    X = r(100, 64, 1536)
+    W = r(1, 1536, 4096) / 32
+    bias = r(4096) / 32
+    steps = iter(range(10 ** 9))
+    rec("3_lstm_gate_step", timed(lambda: nncl.LinearForward(X[next(steps) % 100][None], W, bias)),
+        2 * 64 * 1536 * 4096, 4 * (64 * 1536 + 1536 * 4096 + 64 * 4096 + 4096))
+    A5, B5 = r(1000, 777), r(777, 3000)
+    rec("5a_ragged", timed(lambda: nncl.gemm(A5, B5)), 2 * 1000 * 3000 * 777,
+        4 * (1000 * 777 + 777 * 3000 + 1000 * 3000))
+    x = r(1, 4096)
+    copies = [r(4096, 11008) for _ in range(3)]  # 541 MB > the 256 MB MALL
+    it = iter(range(10 ** 9))
+    rec("5b_gemv", timed(lambda: nncl.gemm(x, copies[next(it) % 3])), 2 * 4096 * 11008,
+        4 * (4096 + 4096 * 11008 + 11008))
+    return out
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,180 @@
+/*
+ * migemm.h -- C ABI of the MI355X (gfx950) fp32 matrix-multiplication library.
+ *
+ * This is the drop-in boundary for the matmul path of Dima3108/my_pytchon_opencl_lib.
+ * Every entry point below replaces one OpenCL enqueue of the reference; the comment
+ * above each declaration names the reference interface it replaces (file:line, paths
+ * relative to the reference repository root; "cs/" abbreviates csharp/cstorchcl/cstorchcl/).
+ *
+ * Conventions (shared by every compute entry point):
+ *   - All matrices are row-major fp32 in device memory (HIP device pointers).
+ *   - Sizes are element counts; strides ("batch strides") are element offsets between
+ *     consecutive matrices of a batch, exactly as the reference kernels take them.
+ *     A batch stride of 0 broadcasts that operand over the batch
+ *     (cs/compiler/NnClGlob.cs:467 and :1719-1720).
+ *   - `stream` is a hipStream_t passed as void*; NULL means the null stream.
+ *     Compute entry points are asynchronous on that stream (like BmmPermute /
+ *     LinearForward in the reference); the host wrappers add the blocking
+ *     synchronisation where the reference has one (cs/compiler/NnClGlob.cs:498).
+ *   - The library never allocates or frees caller tensors. Outputs are written only
+ *     inside [M x N] of each batch entry; memory around them (pooled buffers larger
+ *     than M*N, cs/compiler/OpenCLBufferManager.cs:29-40) is left untouched.
+ *   - An output range that overlaps an input range is rejected (MIGEMM_ERR_ALIAS):
+ *     the reference kernels read inputs while other work-groups write C, so an
+ *     aliased call has no defined result there either.
+ *   - Every argument is validated before any HIP call is made, so argument errors are
+ *     reported identically on machines with and without a GPU.
+ *   - Arithmetic: each output element is an fp32 sum over k of fp32 products,
+ *     accumulated by fp32 MFMA (v_mfma_f32_32x32x2_f32) or by fp32 FMA chains in the
+ *     skinny kernels, plus an optional bias added after the k loop
+ *     (cs/cl_kernels/linear.cl:119-122). Results match the reference kernels within a
+ *     relative error of 1e-5*sqrt(K) against an fp64 evaluation.
+ */
+#ifndef MIGEMM_H
+#define MIGEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. 0 = success. The C# / Python wrappers map INVALID_ARG, ALIAS and
+ * UNSUPPORTED to ArgumentException / ValueError (cs/compiler/NnClGlob.cs:443-452),
+ * and HIP / NO_DEVICE / WORKSPACE to InvalidOperationException / RuntimeError
+ * (cs/compiler/JITProgramCache.cs:40-43). */
+enum {
+    MIGEMM_OK = 0,
+    MIGEMM_ERR_INVALID_ARG = 1, /* bad size, stride, pointer, flag or overflow        */
+    MIGEMM_ERR_ALIAS = 2,       /* output range overlaps an input range              */
+    MIGEMM_ERR_HIP = 3,         /* a HIP runtime call failed (message in last error) */
+    MIGEMM_ERR_NO_DEVICE = 4,   /* no usable gfx950 device                           */
+    MIGEMM_ERR_WORKSPACE = 5,   /* internal workspace could not be allocated         */
+    MIGEMM_ERR_UNSUPPORTED = 6  /* valid request outside what this build implements  */
+};
+
+/* ------------------------------------------------------------------------------- */
+/* (1) General strided-batched GEMM: the one entry point every form below reduces to.
+ *
+ *   C_b[m, n] = sum_k opA(A_b)[m, k] * opB(B_b)[k, n]  (+ bias[n] if bias != NULL)
+ *   A_b = A + b*strideA, B_b = B + b*strideB, C_b = C + b*strideC, b in [0, batch)
+ *   transA == 0: A_b element (m,k) at A_b[m*lda + k]   (A stored [M,K])
+ *   transA != 0: A_b element (m,k) at A_b[k*lda + m]   (A stored [K,M])
+ *   transB == 0: B_b element (k,n) at B_b[k*ldb + n]   (B stored [K,N])
+ *   transB != 0: B_b element (k,n) at B_b[n*ldb + k]   (B stored [N,K])
+ *   C_b element (m,n) at C_b[m*ldc + n].
+ * Requirements: M,N,K,batch >= 1; lda/ldb/ldc at least the stored row length;
+ * strideA, strideB >= 0 (0 = broadcast); when batch > 1, strideC >= (M-1)*ldc + N
+ * so that no two batch entries write the same element.
+ * Covers NN / NT / TN (TT too), stride-0 broadcast and the bias epilogue of
+ * cs/cl_kernels/linear.cl:107-143 and cs/cl_kernels/lstm.cl:340-366.
+ */
+int migemm_gemm_strided_batched(void *stream, int transA, int transB,
+                                int M, int N, int K,
+                                const float *A, int64_t lda, int64_t strideA,
+                                const float *B, int64_t ldb, int64_t strideB,
+                                const float *bias,
+                                float *C, int64_t ldc, int64_t strideC,
+                                int batch);
+
+/* ------------------------------------------------------------------------------- */
+/* (2) Reference-shaped entry points: same argument lists and meaning as the OpenCL
+ *     kernels (plus the stream, and the batch count that the reference passes as the
+ *     third global-size dimension), so every reference call site maps 1:1.          */
+
+/* Replaces kernel matmul_tiled, cl_kernels/matmul.cl:8-14
+ * (launched as in tests/test_matrix_ops.py:109-121): C[M,N] = A[M,K] * B[K,N]. */
+int migemm_matmul_tiled(void *stream, const float *A, const float *B, float *C,
+                        int M, int K, int N);
+
+/* Replaces kernel bmm_tiled, cl_kernels/matmul.cl:78-87, enqueued by
+ * NnClGlob.Bmm (cs/compiler/NnClGlob.cs:441-506) and nncl_glob.py:110-147.
+ * batch_stride_B == 0 broadcasts B (NnClGlob.cs:467). */
+int migemm_bmm_tiled(void *stream, const float *A, const float *B, float *C,
+                     int M, int K, int N,
+                     int batch_stride_A, int batch_stride_B, int batch_stride_C,
+                     int batch);
+
+/* Replaces kernel bmm_permute_tiled, cs/cl_kernels/bmm_permute_tiled.cl:7-19,
+ * enqueued by NnClGlob.BmmPermute (cs/compiler/NnClGlob.cs:1702-1751).
+ * transA: A stored [K,M] (element (r,k) = A[k*M + r], bmm_permute_tiled.cl:59);
+ * transB: B stored [N,K] (element (k,c) = B[c*K + k], bmm_permute_tiled.cl:74). */
+int migemm_bmm_permute_tiled(void *stream, const float *A, const float *B, float *C,
+                             int M, int K, int N,
+                             int batch_stride_A, int batch_stride_B, int batch_stride_C,
+                             int transA, int transB, int batch);
+
+/* Replaces kernel linear_forward_tiled, cs/cl_kernels/linear.cl:14-24, enqueued by
+ * NnClGlob.LinearForward (cs/compiler/NnClGlob.cs:1493-1551):
+ * Y_b = X_b * W + bias, W [K,N] shared by every batch entry, bias [N] (never NULL). */
+int migemm_linear_forward(void *stream, const float *X, const float *W,
+                          const float *bias, float *Y,
+                          int M, int K, int N,
+                          int batch_stride_X, int batch_stride_Y, int batch);
+
+/* Replaces kernel lstm_gemm_xw, cs/cl_kernels/lstm.cl:273-279, enqueued by
+ * NnClGlob.Lstm (cs/compiler/NnClGlob.cs:877-899):
+ * XW_out[T,G] = X[T,F] * W[F,G] + bias[G]. */
+int migemm_lstm_gemm_xw(void *stream, const float *X, const float *W,
+                        const float *bias, float *XW_out,
+                        int total_tokens, int in_features, int total_gates);
+
+/* Replaces kernel tensor_permute, cl_kernels/permute.cl:11-18, enqueued by
+ * NnClGlob.Permute (cs/compiler/NnClGlob.cs:382-424) and nncl_glob.py:148-174.
+ * dst = src.permute(axes); src_dims and axes are HOST int arrays of length num_dims
+ * (1..10) -- the reference builds three device buffers from them on every call
+ * (NnClGlob.cs:402-405); here they travel in the kernel arguments. */
+int migemm_tensor_permute(void *stream, const float *src, float *dst,
+                          const int *src_dims, const int *axes, int num_dims);
+
+/* Replaces kernel linear_bias_backward, cs/cl_kernels/linear.cl:149-153, enqueued by
+ * NnClGlob.LinearBiasBackward (cs/compiler/NnClGlob.cs:1557-1584):
+ * grad_bias[n] = sum over r < total_rows of grad_output[r*N + n], r ascending. */
+int migemm_linear_bias_backward(void *stream, const float *grad_output, float *grad_bias,
+                                int total_rows, int N);
+
+/* Replaces kernel reduce_sum_axis, cs/cl_kernels/reduce_sum_axis.cl:3-8, enqueued by
+ * NnClGlob.Sum (cs/compiler/NnClGlob.cs:1595-1664):
+ * Y[o, i] = sum over a < axis_size of X[(o*axis_size + a)*inner_size + i], a ascending. */
+int migemm_reduce_sum_axis(void *stream, const float *X, float *Y,
+                           int outer_size, int axis_size, int inner_size);
+
+/* Weight gradient of LinearOp.Backward (cs/core/LinearOp.cs:35-39):
+ * dW[K,N] = sum_b X_b^T * dY_b for X [batch,M,K], dY [batch,M,N] contiguous.
+ * The reference materialises BmmPermute(x, dY, transA) [batch,K,N] and then
+ * Sum(axis 0); this runs one TN GEMM whose contraction runs over batch*M rows. */
+int migemm_linear_weight_grad(void *stream, const float *X, const float *dY, float *dW,
+                              int M, int K, int N, int batch);
+
+/* ------------------------------------------------------------------------------- */
+/* (3) Device, memory and stream services that replace the OpenCL context, queue
+ *     registry, buffer manager and host read-back used by the reference host
+ *     (cs/core/ComputeContext.cs:35-155, cs/core/DeviceQueueRegistry.cs:14-37,
+ *     cs/compiler/OpenCLBufferManager.cs:22-88, cs/compiler/HostReturner.cs:17-74). */
+
+/* Number of visible HIP devices (0 when there is none). */
+int migemm_device_count(int *count);
+/* Select the device used by later calls on this host thread. */
+int migemm_set_device(int device);
+/* Name (e.g. "gfx950"), compute-unit count and global memory of a device. */
+int migemm_device_info(int device, char *arch_name, size_t arch_name_len,
+                       int *compute_units, size_t *global_mem_bytes);
+int migemm_malloc(void **ptr, size_t bytes);
+int migemm_free(void *ptr);
+int migemm_memcpy_h2d(void *stream, void *dst, const void *src, size_t bytes);
+int migemm_memcpy_d2h(void *stream, void *dst, const void *src, size_t bytes);
+int migemm_memset(void *stream, void *dst, int value, size_t bytes);
+int migemm_stream_create(void **stream);
+int migemm_stream_destroy(void *stream);
+int migemm_stream_synchronize(void *stream);
+/* Message of the last failing call on this host thread ("" if none). */
+const char *migemm_last_error(void);
+/* Library version, e.g. "0.1.0". */
+const char *migemm_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIGEMM_H */

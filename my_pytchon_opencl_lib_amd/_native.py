@@ -1,0 +1,126 @@
+"""ctypes binding of libmigemm.so, the HIP/gfx950 C ABI declared in include/migemm.h.
+
+The shared library is built in-tree by build_native.py. There is no fallback: if the
+library is missing or cannot be loaded, every operator raises, so a silent CPU or
+PyTorch path can never stand in for the HIP kernels.
+"""
+import ctypes
+import os
+import threading
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "libmigemm.so")
+
+MIGEMM_OK = 0
+MIGEMM_ERR_INVALID_ARG = 1
+MIGEMM_ERR_ALIAS = 2
+MIGEMM_ERR_HIP = 3
+MIGEMM_ERR_NO_DEVICE = 4
+MIGEMM_ERR_WORKSPACE = 5
+MIGEMM_ERR_UNSUPPORTED = 6
+
+STATUS_NAMES = {
+    MIGEMM_OK: "MIGEMM_OK",
+    MIGEMM_ERR_INVALID_ARG: "MIGEMM_ERR_INVALID_ARG",
+    MIGEMM_ERR_ALIAS: "MIGEMM_ERR_ALIAS",
+    MIGEMM_ERR_HIP: "MIGEMM_ERR_HIP",
+    MIGEMM_ERR_NO_DEVICE: "MIGEMM_ERR_NO_DEVICE",
+    MIGEMM_ERR_WORKSPACE: "MIGEMM_ERR_WORKSPACE",
+    MIGEMM_ERR_UNSUPPORTED: "MIGEMM_ERR_UNSUPPORTED",
+}
+
+
+class MigemmArgumentError(ValueError):
+    """Argument / shape error (the reference throws ArgumentException,
+    csharp/cstorchcl/cstorchcl/compiler/NnClGlob.cs:443-452)."""
+
+    def __init__(self, status, message):
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+
+
+class MigemmRuntimeError(RuntimeError):
+    """Device / runtime error (the reference throws InvalidOperationException,
+    csharp/cstorchcl/cstorchcl/compiler/JITProgramCache.cs:40-43)."""
+
+    def __init__(self, status, message):
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+
+
+# Every exported symbol with its C signature (argument types, return type). The CPU test
+# suite checks this table against include/migemm.h.
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int
+_i64 = ctypes.c_int64
+_sz = ctypes.c_size_t
+_ip = ctypes.POINTER(ctypes.c_int)
+SIGNATURES = {
+    "migemm_gemm_strided_batched": ([_vp, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _vp,
+                                     _i64, _i64, _vp, _vp, _i64, _i64, _i32], _i32),
+    "migemm_matmul_tiled": ([_vp, _vp, _vp, _vp, _i32, _i32, _i32], _i32),
+    "migemm_bmm_tiled": ([_vp, _vp, _vp, _vp] + [_i32] * 7, _i32),
+    "migemm_bmm_permute_tiled": ([_vp, _vp, _vp, _vp] + [_i32] * 9, _i32),
+    "migemm_linear_forward": ([_vp, _vp, _vp, _vp, _vp] + [_i32] * 6, _i32),
+    "migemm_lstm_gemm_xw": ([_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32], _i32),
+    "migemm_tensor_permute": ([_vp, _vp, _vp, _ip, _ip, _i32], _i32),
+    "migemm_linear_bias_backward": ([_vp, _vp, _vp, _i32, _i32], _i32),
+    "migemm_reduce_sum_axis": ([_vp, _vp, _vp, _i32, _i32, _i32], _i32),
+    "migemm_linear_weight_grad": ([_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32], _i32),
+    "migemm_device_count": ([_ip], _i32),
+    "migemm_set_device": ([_i32], _i32),
+    "migemm_device_info": ([_i32, ctypes.c_char_p, _sz, _ip, ctypes.POINTER(_sz)], _i32),
+    "migemm_malloc": ([ctypes.POINTER(_vp), _sz], _i32),
+    "migemm_free": ([_vp], _i32),
+    "migemm_memcpy_h2d": ([_vp, _vp, _vp, _sz], _i32),
+    "migemm_memcpy_d2h": ([_vp, _vp, _vp, _sz], _i32),
+    "migemm_memset": ([_vp, _vp, _i32, _sz], _i32),
+    "migemm_stream_create": ([ctypes.POINTER(_vp)], _i32),
+    "migemm_stream_destroy": ([_vp], _i32),
+    "migemm_stream_synchronize": ([_vp], _i32),
+    "migemm_last_error": ([], ctypes.c_char_p),
+    "migemm_version": ([], ctypes.c_char_p),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load():
+    """Load libmigemm.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"libmigemm.so not found at {LIB_PATH}: build it first "
+                    "(python -c 'import __graft_entry__ as g; g.build()' or "
+                    "python my_pytchon_opencl_lib_amd/build_native.py)")
+            L = ctypes.CDLL(LIB_PATH)
+            for name, (args, res) in SIGNATURES.items():
+                fn = getattr(L, name)
+                fn.argtypes = args
+                fn.restype = res
+            _lib = L
+    return _lib
+
+
+def last_error():
+    return load().migemm_last_error().decode(errors="replace")
+
+
+def check(status):
+    """Raise the exception type that matches a migemm status code."""
+    if status == MIGEMM_OK:
+        return
+    msg = last_error()
+    if status in (MIGEMM_ERR_INVALID_ARG, MIGEMM_ERR_ALIAS, MIGEMM_ERR_UNSUPPORTED):
+        raise MigemmArgumentError(status, msg)
+    raise MigemmRuntimeError(status, msg)
+
+
+def call(name, *args):
+    """Call an exported function and raise on a non-zero status."""
+    check(getattr(load(), name)(*args))

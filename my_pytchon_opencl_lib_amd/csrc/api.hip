@@ -1,0 +1,431 @@
+// C ABI of libmigemm: argument validation, dispatch to the HIP kernels, and the device /
+// memory / stream services the reference host obtains from OpenCL.
+//
+// Every compute entry point validates all of its arguments before the first HIP call, so
+// argument errors behave the same with and without a GPU, mirroring the reference's
+// checks that throw before any enqueue (cs/compiler/NnClGlob.cs:443-452, :1704-1714,
+// cs/core/Tensor.cs:191-192; "cs/" = csharp/cstorchcl/cstorchcl/).
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "migemm_internal.h"
+
+namespace migemm {
+
+namespace {
+thread_local char g_last_error[512] = "";
+constexpr int64_t kMaxElems = (int64_t)1 << 46;  // 256 TiB of fp32: beyond any device
+
+// a*b + c with overflow detection for non-negative operands (bounded by kMaxElems).
+bool mul_add_ok(int64_t a, int64_t b, int64_t c, int64_t *out) {
+    if (a < 0 || b < 0 || c < 0) return false;
+    if (a != 0 && b > kMaxElems / a) return false;
+    const int64_t p = a * b;
+    if (p > kMaxElems - c) return false;
+    *out = p + c;
+    return true;
+}
+
+bool ranges_overlap(const void *p0, int64_t n0, const void *p1, int64_t n1) {
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(p0);
+    const uintptr_t a1 = reinterpret_cast<uintptr_t>(p1);
+    const uintptr_t e0 = a0 + (uintptr_t)n0 * sizeof(float);
+    const uintptr_t e1 = a1 + (uintptr_t)n1 * sizeof(float);
+    return a0 < e1 && a1 < e0;
+}
+
+// Element extent touched by a batched matrix operand: (batch-1)*stride + (rows-1)*ld + cols.
+bool extent(int batch, int64_t stride, int rows, int64_t ld, int cols, int64_t *out) {
+    int64_t inner;
+    if (!mul_add_ok(rows - 1, ld, cols, &inner)) return false;
+    return mul_add_ok(batch - 1, stride, inner, out);
+}
+
+struct DeviceWorkspace {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+std::vector<DeviceWorkspace> g_ws;
+}  // namespace
+
+int set_error(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+void clear_error() { g_last_error[0] = '\0'; }
+
+int hip_check(hipError_t e, const char *what) {
+    if (e == hipSuccess) return MIGEMM_OK;
+    if (e == hipErrorNoDevice || e == hipErrorInvalidDevice)
+        return set_error(MIGEMM_ERR_NO_DEVICE, "%s: %s", what, hipGetErrorString(e));
+    return set_error(MIGEMM_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// One growing buffer per device. The first 1 MiB holds arrival counters that every kernel
+// using them returns to zero; it is cleared once when the buffer is (re)allocated. Calls
+// that use the workspace must be ordered on one stream (they share the buffer).
+void *workspace(size_t bytes, int *status) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        *status = hip_check(e, "hipGetDevice");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
+    DeviceWorkspace &w = g_ws[dev];
+    if (w.bytes < bytes) {
+        if (w.ptr != nullptr) {
+            // Work queued earlier may still read the old buffer.
+            e = hipDeviceSynchronize();
+            if (e == hipSuccess) e = hipFree(w.ptr);
+            w.ptr = nullptr;
+            w.bytes = 0;
+            if (e != hipSuccess) {
+                *status = hip_check(e, "workspace release");
+                return nullptr;
+            }
+        }
+        size_t want = bytes < ((size_t)8 << 20) ? ((size_t)8 << 20) : bytes;
+        e = hipMalloc(&w.ptr, want);
+        if (e == hipSuccess) e = hipMemset(w.ptr, 0, want);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) {
+            w.ptr = nullptr;
+            *status = set_error(MIGEMM_ERR_WORKSPACE, "workspace of %zu bytes: %s", want,
+                                hipGetErrorString(e));
+            return nullptr;
+        }
+        w.bytes = want;
+    }
+    *status = MIGEMM_OK;
+    return w.ptr;
+}
+
+// Validates a general GEMM request and fills `d`. No HIP call is made.
+static int validate_gemm(int transA, int transB, int M, int N, int K, const float *A,
+                         int64_t lda, int64_t strideA, const float *B, int64_t ldb,
+                         int64_t strideB, const float *bias, float *C, int64_t ldc,
+                         int64_t strideC, int batch, GemmDesc *d) {
+    if (M < 1 || N < 1 || K < 1 || batch < 1)
+        return set_error(MIGEMM_ERR_INVALID_ARG,
+                         "gemm: sizes must be >= 1 (M=%d N=%d K=%d batch=%d)", M, N, K, batch);
+    if (A == nullptr || B == nullptr || C == nullptr)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "gemm: A, B and C must be non-null");
+    if (transA != 0 && transA != 1)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "gemm: transA must be 0 or 1 (got %d)", transA);
+    if (transB != 0 && transB != 1)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "gemm: transB must be 0 or 1 (got %d)", transB);
+    const int a_rows = transA ? K : M, a_cols = transA ? M : K;
+    const int b_rows = transB ? N : K, b_cols = transB ? K : N;
+    if (lda < a_cols)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "gemm: lda=%lld < %d", (long long)lda, a_cols);
+    if (ldb < b_cols)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "gemm: ldb=%lld < %d", (long long)ldb, b_cols);
+    if (ldc < N)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "gemm: ldc=%lld < N=%d", (long long)ldc, N);
+    if (strideA < 0 || strideB < 0 || strideC < 0)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "gemm: batch strides must be >= 0");
+    int64_t ea, eb, ec;
+    if (!extent(batch, strideA, a_rows, lda, a_cols, &ea) ||
+        !extent(batch, strideB, b_rows, ldb, b_cols, &eb) ||
+        !extent(batch, strideC, M, ldc, N, &ec))
+        return set_error(MIGEMM_ERR_INVALID_ARG, "gemm: operand extent overflows");
+    if (batch > 1 && strideC < (int64_t)(M - 1) * ldc + N)
+        return set_error(MIGEMM_ERR_INVALID_ARG,
+                         "gemm: strideC=%lld makes batch entries of C overlap",
+                         (long long)strideC);
+    if (ranges_overlap(C, ec, A, ea) || ranges_overlap(C, ec, B, eb) ||
+        (bias != nullptr && ranges_overlap(C, ec, bias, N)))
+        return set_error(MIGEMM_ERR_ALIAS, "gemm: output overlaps an input");
+    d->A = A;
+    d->B = B;
+    d->bias = bias;
+    d->C = C;
+    d->lda = lda;
+    d->ldb = ldb;
+    d->ldc = ldc;
+    d->sA = batch > 1 ? strideA : 0;
+    d->sB = batch > 1 ? strideB : 0;
+    d->sC = batch > 1 ? strideC : 0;
+    d->M = M;
+    d->N = N;
+    d->K = K;
+    d->batch = batch;
+    d->transA = transA != 0;
+    d->transB = transB != 0;
+    return MIGEMM_OK;
+}
+
+static int run_gemm(hipStream_t stream, const GemmDesc &d) {
+    if (skinny_applicable(d)) return launch_gemm_skinny(stream, d);
+    return launch_gemm_tiled(stream, d);
+}
+
+}  // namespace migemm
+
+using namespace migemm;
+
+extern "C" {
+
+int migemm_gemm_strided_batched(void *stream, int transA, int transB, int M, int N, int K,
+                                const float *A, int64_t lda, int64_t strideA, const float *B,
+                                int64_t ldb, int64_t strideB, const float *bias, float *C,
+                                int64_t ldc, int64_t strideC, int batch) {
+    clear_error();
+    GemmDesc d;
+    int rc = validate_gemm(transA, transB, M, N, K, A, lda, strideA, B, ldb, strideB, bias, C,
+                           ldc, strideC, batch, &d);
+    if (rc != MIGEMM_OK) return rc;
+    return run_gemm(static_cast<hipStream_t>(stream), d);
+}
+
+int migemm_matmul_tiled(void *stream, const float *A, const float *B, float *C, int M, int K,
+                        int N) {
+    return migemm_gemm_strided_batched(stream, 0, 0, M, N, K, A, K, 0, B, N, 0, nullptr, C, N,
+                                       0, 1);
+}
+
+static int check_ref_strides(const char *who, int sA, int sB, int sC) {
+    if (sA < 0 || sB < 0 || sC < 0)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "%s: batch strides must be >= 0", who);
+    return MIGEMM_OK;
+}
+
+int migemm_bmm_tiled(void *stream, const float *A, const float *B, float *C, int M, int K, int N,
+                     int batch_stride_A, int batch_stride_B, int batch_stride_C, int batch) {
+    clear_error();
+    int rc = check_ref_strides("bmm_tiled", batch_stride_A, batch_stride_B, batch_stride_C);
+    if (rc != MIGEMM_OK) return rc;
+    return migemm_gemm_strided_batched(stream, 0, 0, M, N, K, A, K, batch_stride_A, B, N,
+                                       batch_stride_B, nullptr, C, N, batch_stride_C, batch);
+}
+
+int migemm_bmm_permute_tiled(void *stream, const float *A, const float *B, float *C, int M,
+                             int K, int N, int batch_stride_A, int batch_stride_B,
+                             int batch_stride_C, int transA, int transB, int batch) {
+    clear_error();
+    int rc = check_ref_strides("bmm_permute_tiled", batch_stride_A, batch_stride_B,
+                               batch_stride_C);
+    if (rc != MIGEMM_OK) return rc;
+    // The reference treats any non-zero flag as "transposed" (bmm_permute_tiled.cl:43-44).
+    const int ta = transA != 0, tb = transB != 0;
+    return migemm_gemm_strided_batched(stream, ta, tb, M, N, K, A, ta ? M : K, batch_stride_A,
+                                       B, tb ? K : N, batch_stride_B, nullptr, C, N,
+                                       batch_stride_C, batch);
+}
+
+int migemm_linear_forward(void *stream, const float *X, const float *W, const float *bias,
+                          float *Y, int M, int K, int N, int batch_stride_X, int batch_stride_Y,
+                          int batch) {
+    clear_error();
+    if (bias == nullptr)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "linear_forward: bias must be non-null");
+    int rc = check_ref_strides("linear_forward", batch_stride_X, 0, batch_stride_Y);
+    if (rc != MIGEMM_OK) return rc;
+    return migemm_gemm_strided_batched(stream, 0, 0, M, N, K, X, K, batch_stride_X, W, N, 0,
+                                       bias, Y, N, batch_stride_Y, batch);
+}
+
+int migemm_lstm_gemm_xw(void *stream, const float *X, const float *W, const float *bias,
+                        float *XW_out, int total_tokens, int in_features, int total_gates) {
+    clear_error();
+    if (bias == nullptr)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "lstm_gemm_xw: bias must be non-null");
+    return migemm_gemm_strided_batched(stream, 0, 0, total_tokens, total_gates, in_features, X,
+                                       in_features, 0, W, total_gates, 0, bias, XW_out,
+                                       total_gates, 0, 1);
+}
+
+int migemm_linear_weight_grad(void *stream, const float *X, const float *dY, float *dW, int M,
+                              int K, int N, int batch) {
+    clear_error();
+    if (M < 1 || K < 1 || N < 1 || batch < 1)
+        return set_error(MIGEMM_ERR_INVALID_ARG,
+                         "linear_weight_grad: sizes must be >= 1 (M=%d K=%d N=%d batch=%d)", M,
+                         K, N, batch);
+    const int64_t rows = (int64_t)batch * M;
+    if (rows > INT32_MAX)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "linear_weight_grad: batch*M exceeds 2^31-1");
+    // dW[K,N] = X'^T dY' with X' = X viewed [batch*M, K] and dY' = dY viewed [batch*M, N].
+    return migemm_gemm_strided_batched(stream, 1, 0, K, N, (int)rows, X, K, 0, dY, N, 0,
+                                       nullptr, dW, N, 0, 1);
+}
+
+int migemm_tensor_permute(void *stream, const float *src, float *dst, const int *src_dims,
+                          const int *axes, int num_dims) {
+    clear_error();
+    if (src == nullptr || dst == nullptr || src_dims == nullptr || axes == nullptr)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "tensor_permute: null pointer argument");
+    if (num_dims < 1 || num_dims > 10)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "tensor_permute: num_dims=%d not in [1,10]",
+                         num_dims);
+    int64_t total = 1;
+    bool seen[10] = {false};
+    for (int i = 0; i < num_dims; ++i) {
+        if (src_dims[i] < 1)
+            return set_error(MIGEMM_ERR_INVALID_ARG, "tensor_permute: dim %d is %d (< 1)", i,
+                             src_dims[i]);
+        if (axes[i] < 0 || axes[i] >= num_dims || seen[axes[i]])
+            return set_error(MIGEMM_ERR_INVALID_ARG,
+                             "tensor_permute: axes is not a permutation of 0..%d", num_dims - 1);
+        seen[axes[i]] = true;
+        if (!mul_add_ok(total, src_dims[i], 0, &total))
+            return set_error(MIGEMM_ERR_INVALID_ARG, "tensor_permute: size overflows");
+    }
+    if (ranges_overlap(src, total, dst, total))
+        return set_error(MIGEMM_ERR_ALIAS, "tensor_permute: dst overlaps src");
+    return launch_permute(static_cast<hipStream_t>(stream), src, dst, src_dims, axes, num_dims,
+                          total);
+}
+
+int migemm_reduce_sum_axis(void *stream, const float *X, float *Y, int outer_size,
+                           int axis_size, int inner_size) {
+    clear_error();
+    if (X == nullptr || Y == nullptr)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "reduce_sum_axis: null pointer argument");
+    if (outer_size < 1 || axis_size < 1 || inner_size < 1)
+        return set_error(MIGEMM_ERR_INVALID_ARG,
+                         "reduce_sum_axis: sizes must be >= 1 (outer=%d axis=%d inner=%d)",
+                         outer_size, axis_size, inner_size);
+    int64_t nin, nout;
+    if (!mul_add_ok((int64_t)outer_size * inner_size, axis_size, 0, &nin) ||
+        !mul_add_ok(outer_size, inner_size, 0, &nout) || nout > INT32_MAX * (int64_t)256)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "reduce_sum_axis: size overflows");
+    if (ranges_overlap(X, nin, Y, nout))
+        return set_error(MIGEMM_ERR_ALIAS, "reduce_sum_axis: output overlaps input");
+    return launch_column_sum(static_cast<hipStream_t>(stream), X, Y, outer_size, axis_size,
+                             inner_size);
+}
+
+int migemm_linear_bias_backward(void *stream, const float *grad_output, float *grad_bias,
+                                int total_rows, int N) {
+    clear_error();
+    if (grad_output == nullptr || grad_bias == nullptr)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "linear_bias_backward: null pointer argument");
+    if (total_rows < 1 || N < 1)
+        return set_error(MIGEMM_ERR_INVALID_ARG,
+                         "linear_bias_backward: sizes must be >= 1 (rows=%d N=%d)", total_rows,
+                         N);
+    return migemm_reduce_sum_axis(stream, grad_output, grad_bias, 1, total_rows, N);
+}
+
+// ---------------------------------------------------------------------------------------
+// Services.
+
+int migemm_device_count(int *count) {
+    clear_error();
+    if (count == nullptr) return set_error(MIGEMM_ERR_INVALID_ARG, "device_count: null pointer");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e == hipErrorNoDevice) {
+        *count = 0;
+        return MIGEMM_OK;
+    }
+    MIGEMM_HIP(e);
+    *count = n;
+    return MIGEMM_OK;
+}
+
+int migemm_set_device(int device) {
+    clear_error();
+    if (device < 0) return set_error(MIGEMM_ERR_INVALID_ARG, "set_device: device %d < 0", device);
+    MIGEMM_HIP(hipSetDevice(device));
+    return MIGEMM_OK;
+}
+
+int migemm_device_info(int device, char *arch_name, size_t arch_name_len, int *compute_units,
+                       size_t *global_mem_bytes) {
+    clear_error();
+    if (device < 0) return set_error(MIGEMM_ERR_INVALID_ARG, "device_info: device %d < 0", device);
+    hipDeviceProp_t prop;
+    MIGEMM_HIP(hipGetDeviceProperties(&prop, device));
+    if (arch_name != nullptr && arch_name_len > 0) {
+        strncpy(arch_name, prop.gcnArchName, arch_name_len - 1);
+        arch_name[arch_name_len - 1] = '\0';
+    }
+    if (compute_units != nullptr) *compute_units = prop.multiProcessorCount;
+    if (global_mem_bytes != nullptr) *global_mem_bytes = prop.totalGlobalMem;
+    return MIGEMM_OK;
+}
+
+int migemm_malloc(void **ptr, size_t bytes) {
+    clear_error();
+    if (ptr == nullptr || bytes == 0)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "malloc: null pointer or zero size");
+    MIGEMM_HIP(hipMalloc(ptr, bytes));
+    return MIGEMM_OK;
+}
+
+int migemm_free(void *ptr) {
+    clear_error();
+    if (ptr == nullptr) return MIGEMM_OK;
+    MIGEMM_HIP(hipFree(ptr));
+    return MIGEMM_OK;
+}
+
+int migemm_memcpy_h2d(void *stream, void *dst, const void *src, size_t bytes) {
+    clear_error();
+    if ((dst == nullptr || src == nullptr) && bytes != 0)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "memcpy_h2d: null pointer");
+    if (bytes == 0) return MIGEMM_OK;
+    MIGEMM_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice,
+                              static_cast<hipStream_t>(stream)));
+    return MIGEMM_OK;
+}
+
+int migemm_memcpy_d2h(void *stream, void *dst, const void *src, size_t bytes) {
+    clear_error();
+    if ((dst == nullptr || src == nullptr) && bytes != 0)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "memcpy_d2h: null pointer");
+    if (bytes == 0) return MIGEMM_OK;
+    MIGEMM_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost,
+                              static_cast<hipStream_t>(stream)));
+    MIGEMM_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    return MIGEMM_OK;
+}
+
+int migemm_memset(void *stream, void *dst, int value, size_t bytes) {
+    clear_error();
+    if (dst == nullptr && bytes != 0) return set_error(MIGEMM_ERR_INVALID_ARG, "memset: null pointer");
+    if (bytes == 0) return MIGEMM_OK;
+    MIGEMM_HIP(hipMemsetAsync(dst, value, bytes, static_cast<hipStream_t>(stream)));
+    return MIGEMM_OK;
+}
+
+int migemm_stream_create(void **stream) {
+    clear_error();
+    if (stream == nullptr) return set_error(MIGEMM_ERR_INVALID_ARG, "stream_create: null pointer");
+    hipStream_t s;
+    MIGEMM_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = s;
+    return MIGEMM_OK;
+}
+
+int migemm_stream_destroy(void *stream) {
+    clear_error();
+    if (stream == nullptr) return MIGEMM_OK;
+    MIGEMM_HIP(hipStreamDestroy(static_cast<hipStream_t>(stream)));
+    return MIGEMM_OK;
+}
+
+int migemm_stream_synchronize(void *stream) {
+    clear_error();
+    MIGEMM_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    return MIGEMM_OK;
+}
+
+const char *migemm_last_error(void) { return g_last_error; }
+
+const char *migemm_version(void) { return "0.1.0"; }
+
+}  // extern "C"

@@ -1,0 +1,142 @@
+// Layout and reduction kernels of the matmul path:
+//  * tensor permute (cl_kernels/permute.cl:11-50): a batched 2-D transpose through LDS
+//    when the permutation swaps the last two axes (the [0,2,1] / [1,0] forms that
+//    BmmOp.Backward and the Python Linear use), else a generic <=10-D gather;
+//  * column sums (cs/cl_kernels/linear.cl:149-168 linear_bias_backward and
+//    cs/cl_kernels/reduce_sum_axis.cl:3-24 reduce_sum_axis): each output is summed over
+//    the reduced axis in ascending order from +0.0f, exactly as the reference kernels do,
+//    so these results are bit-identical to the reference's.
+#include "migemm_internal.h"
+
+namespace migemm {
+namespace {
+
+constexpr int MAXD = 10;
+
+struct PermuteArgs {
+    const float *src;
+    float *dst;
+    int64_t total;
+    int ndim;
+    int64_t dst_dims[MAXD];
+    int64_t src_stride_of_dst_axis[MAXD];  // stride in src of the axis placed at dst axis i
+};
+
+__global__ void __launch_bounds__(256) permute_gather_kernel(PermuteArgs a) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < a.total; t += step) {
+        int64_t rem = t;
+        int64_t off = 0;
+        for (int i = a.ndim - 1; i >= 0; --i) {
+            const int64_t d = a.dst_dims[i];
+            const int64_t c = rem % d;
+            rem /= d;
+            off += c * a.src_stride_of_dst_axis[i];
+        }
+        a.dst[t] = a.src[off];
+    }
+}
+
+// dst[b][c][r] = src[b][r][c] for src [batch][R][Ccols]; 32x32 tiles through LDS with a
+// +1 pad so the column read of the tile is bank-conflict free.
+__global__ void __launch_bounds__(256) transpose_kernel(const float *__restrict__ src,
+                                                          float *__restrict__ dst, int R, int Cc,
+                                                          int tiles_c) {
+    __shared__ float tile[32][33];
+    const int b = blockIdx.y;
+    const int tr = blockIdx.x / tiles_c;
+    const int tc = blockIdx.x % tiles_c;
+    const int tx = threadIdx.x & 31;
+    const int ty = threadIdx.x >> 5;  // 0..7
+    const float *s = src + (int64_t)b * R * Cc;
+    float *d = dst + (int64_t)b * R * Cc;
+#pragma unroll
+    for (int j = 0; j < 32; j += 8) {
+        const int r = tr * 32 + ty + j;
+        const int c = tc * 32 + tx;
+        if (r < R && c < Cc) tile[ty + j][tx] = s[(int64_t)r * Cc + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 32; j += 8) {
+        const int c = tc * 32 + ty + j;
+        const int r = tr * 32 + tx;
+        if (r < R && c < Cc) d[(int64_t)c * R + r] = tile[tx][ty + j];
+    }
+}
+
+// Y[o, i] = sum_{a ascending} X[(o*axis + a)*inner + i], one thread per output.
+__global__ void __launch_bounds__(256) column_sum_kernel(const float *__restrict__ X,
+                                                           float *__restrict__ Y, int outer,
+                                                           int axis, int inner) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (int64_t)outer * inner) return;
+    const int64_t o = t / inner;
+    const int64_t i = t - o * inner;
+    const float *x = X + o * (int64_t)axis * inner + i;
+    float sum = 0.0f;
+    int a = 0;
+    for (; a + 4 <= axis; a += 4) {
+        const float x0 = x[(int64_t)a * inner], x1 = x[(int64_t)(a + 1) * inner];
+        const float x2 = x[(int64_t)(a + 2) * inner], x3 = x[(int64_t)(a + 3) * inner];
+        sum += x0;
+        sum += x1;
+        sum += x2;
+        sum += x3;
+    }
+    for (; a < axis; ++a) sum += x[(int64_t)a * inner];
+    Y[t] = sum;
+}
+
+}  // namespace
+
+int launch_permute(hipStream_t stream, const float *src, float *dst, const int *src_dims,
+                   const int *axes, int num_dims, int64_t total) {
+    // Batched transpose of the last two axes with every leading axis in place.
+    bool last2 = num_dims >= 2 && axes[num_dims - 1] == num_dims - 2 &&
+                 axes[num_dims - 2] == num_dims - 1;
+    for (int i = 0; i + 2 < num_dims && last2; ++i) last2 = axes[i] == i;
+    if (last2) {
+        const int R = src_dims[num_dims - 2];
+        const int Cc = src_dims[num_dims - 1];
+        int64_t batch = 1;
+        for (int i = 0; i + 2 < num_dims; ++i) batch *= src_dims[i];
+        const int tiles_r = (R + 31) / 32;
+        const int tiles_c = (Cc + 31) / 32;
+        if (batch <= 65535 && (int64_t)tiles_r * tiles_c <= INT32_MAX) {
+            hipLaunchKernelGGL(transpose_kernel, dim3(tiles_r * tiles_c, (unsigned)batch),
+                               dim3(256), 0, stream, src, dst, R, Cc, tiles_c);
+            return hip_check(hipGetLastError(), "transpose_kernel launch");
+        }
+    }
+    PermuteArgs a;
+    a.src = src;
+    a.dst = dst;
+    a.total = total;
+    a.ndim = num_dims;
+    int64_t src_strides[MAXD];
+    int64_t st = 1;
+    for (int i = num_dims - 1; i >= 0; --i) {
+        src_strides[i] = st;
+        st *= src_dims[i];
+    }
+    for (int i = 0; i < MAXD; ++i) {
+        a.dst_dims[i] = i < num_dims ? src_dims[axes[i]] : 1;
+        a.src_stride_of_dst_axis[i] = i < num_dims ? src_strides[axes[i]] : 0;
+    }
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(permute_gather_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    return hip_check(hipGetLastError(), "permute_gather_kernel launch");
+}
+
+int launch_column_sum(hipStream_t stream, const float *X, float *Y, int outer, int axis,
+                      int inner) {
+    const int64_t outputs = (int64_t)outer * inner;
+    const int64_t blocks = (outputs + 255) / 256;
+    hipLaunchKernelGGL(column_sum_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, X, Y,
+                       outer, axis, inner);
+    return hip_check(hipGetLastError(), "column_sum_kernel launch");
+}
+
+}  // namespace migemm

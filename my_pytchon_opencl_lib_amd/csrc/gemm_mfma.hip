@@ -1,0 +1,383 @@
+// Tiled fp32 GEMM for gfx950 on the matrix cores (v_mfma_f32_32x32x2_f32).
+//
+// One kernel template covers every form of the reference matmul path:
+//   matmul_tiled / bmm_tiled        (cl_kernels/matmul.cl:8-135)         -> NN
+//   bmm_permute_tiled transA/transB (cs/cl_kernels/bmm_permute_tiled.cl) -> TN / NT
+//   linear_forward_tiled, lstm_gemm_xw bias epilogue (cs/cl_kernels/linear.cl:107-143,
+//   cs/cl_kernels/lstm.cl:340-366)
+// ("cs/" = csharp/cstorchcl/cstorchcl/ in the reference repository.)
+//
+// Design (what differs from the reference's one-output-per-work-item 16x16 tiles):
+//  * A work-group of WM x WN wavefronts computes a BM x BN tile of C; each wavefront owns
+//    a (BM/WM) x (BN/WN) sub-tile made of 32x32 MFMA blocks whose fp32 accumulators stay
+//    in registers for the whole K loop.
+//  * Operands move global -> registers -> LDS with 128-bit loads and stores, double
+//    buffered: tile k+1 is fetched from HBM/L2 while tile k is multiplied out of LDS, with
+//    one barrier per BK step.
+//  * Each operand keeps its global orientation in LDS. A K-contiguous operand (A not
+//    transposed, B transposed) is stored [i][BK+4]; the +4 float pad puts the 8 (or 16)
+//    rows touched by one 128-bit LDS read phase on disjoint banks, and one ds_read_b128
+//    feeds four MFMA steps. An I-contiguous operand (A transposed, B not transposed) is
+//    stored [k][T+8] and read with conflict-free 32-bit reads of 32 consecutive floats.
+//  * The K order inside an MFMA step is permuted consistently for both operands: in step
+//    s of k-group g, lanes 0-31 supply k = 8g+s and lanes 32-63 supply k = 8g+4+s. The
+//    sum over k is unchanged; only the fp32 association order differs from the
+//    reference's ascending chain (covered by the 1e-5*sqrt(K) tolerance).
+//  * Edges: rows beyond M / columns beyond N are clamped on load (they only feed outputs
+//    that are never stored); k >= K is zero-filled in both operands, as the reference's
+//    zero padding does (matmul.cl:39-52). Stores are guarded to [M x N].
+//  * Work-group ids are remapped so that consecutive output tiles land on the same XCD
+//    (the dispatcher deals work-groups round-robin over the 8 XCDs, each with its own
+//    L2), then rastered in groups of 8 tile-rows so concurrently running tiles share
+//    A and B panels in that L2.
+#include "migemm_internal.h"
+
+namespace migemm {
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16 __attribute__((ext_vector_type(16)));
+
+struct TiledArgs {
+    const float *A;
+    const float *B;
+    const float *bias;
+    float *C;
+    int64_t lda, ldb, ldc;
+    int64_t sA, sB, sC;
+    int M, N, K;
+    int tiles_m, tiles_n;  // tiles per batch entry
+    int total;             // tiles_m * tiles_n * batch
+};
+
+constexpr int PAD_K = 4;  // pad of a K-contiguous LDS tile row  [i][BK + 4]
+constexpr int PAD_I = 8;  // pad of an I-contiguous LDS tile row [k][T + 8]
+
+template <int T, int BK, bool KC>
+struct TileFloats {
+    static constexpr int value = KC ? T * (BK + PAD_K) : BK * (T + PAD_I);
+};
+
+// One operand tile (T rows of the M or N dimension by BK of the K dimension).
+//  KC  : element (i, k) lives at base[i*ld + k] (K contiguous) else at base[k*ld + i].
+//  VEC : 128-bit global loads are legal (16-byte aligned base, ld % 4 == 0 and the
+//        contiguous extent % 4 == 0); otherwise four 32-bit loads per register.
+template <int T, int BK, int NT, bool KC, bool VEC>
+struct Operand {
+    static_assert((T * BK) % (4 * NT) == 0, "operand tile does not split over the threads");
+    static constexpr int NLOAD = T * BK / (4 * NT);
+    f4 r[NLOAD];
+
+    // Fetch tile (i0.., k0..) into registers. `rows` is the extent along i (M or N).
+    // With `tail` set, k >= K is zero-filled; every address formed stays inside the
+    // operand's rows [0, rows) and columns [0, K) whether or not it is used.
+    __device__ __forceinline__ void load(const float *__restrict__ base, int64_t ld, int i0,
+                                         int rows, int k0, int K, bool tail, int tid) {
+        if constexpr (KC) {
+            constexpr int TPR = BK / 4;    // threads per tile row
+            constexpr int RPP = NT / TPR;  // tile rows per pass
+            const int c = (tid % TPR) * 4;
+            const int rr = tid / TPR;
+            const int gk = k0 + c;
+#pragma unroll
+            for (int p = 0; p < NLOAD; ++p) {
+                int gi = i0 + rr + p * RPP;
+                gi = gi < rows ? gi : rows - 1;
+                const float *rowp = base + (int64_t)gi * ld;
+                if constexpr (VEC) {
+                    const bool ok = !tail || gk < K;
+                    f4 v = *reinterpret_cast<const f4 *>(rowp + (ok ? gk : 0));
+                    r[p] = ok ? v : f4{0.f, 0.f, 0.f, 0.f};
+                } else {
+                    f4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const bool ok = !tail || gk + e < K;
+                        const float x = rowp[ok ? gk + e : 0];
+                        v[e] = ok ? x : 0.f;
+                    }
+                    r[p] = v;
+                }
+            }
+        } else {
+            constexpr int TPR = T / 4;
+            constexpr int RPP = NT / TPR;
+            const int c = (tid % TPR) * 4;
+            const int kr = tid / TPR;
+#pragma unroll
+            for (int p = 0; p < NLOAD; ++p) {
+                const int gk = k0 + kr + p * RPP;
+                const bool ok = !tail || gk < K;
+                const float *rowp = base + (int64_t)(ok ? gk : 0) * ld;
+                if constexpr (VEC) {
+                    int gi = i0 + c;
+                    gi = gi < rows ? gi : rows - 4;
+                    f4 v = *reinterpret_cast<const f4 *>(rowp + gi);
+                    r[p] = ok ? v : f4{0.f, 0.f, 0.f, 0.f};
+                } else {
+                    f4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        int gi = i0 + c + e;
+                        gi = gi < rows ? gi : rows - 1;
+                        const float x = rowp[gi];
+                        v[e] = ok ? x : 0.f;
+                    }
+                    r[p] = v;
+                }
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(float *lds, int tid) const {
+        if constexpr (KC) {
+            constexpr int TPR = BK / 4;
+            constexpr int RPP = NT / TPR;
+            const int c = (tid % TPR) * 4;
+            const int rr = tid / TPR;
+#pragma unroll
+            for (int p = 0; p < NLOAD; ++p)
+                *reinterpret_cast<f4 *>(lds + (rr + p * RPP) * (BK + PAD_K) + c) = r[p];
+        } else {
+            constexpr int TPR = T / 4;
+            constexpr int RPP = NT / TPR;
+            const int c = (tid % TPR) * 4;
+            const int kr = tid / TPR;
+#pragma unroll
+            for (int p = 0; p < NLOAD; ++p)
+                *reinterpret_cast<f4 *>(lds + (kr + p * RPP) * (T + PAD_I) + c) = r[p];
+        }
+    }
+};
+
+// MFMA operand fragments of k-group g (8 consecutive k of the LDS tile) for F blocks of
+// 32 rows starting at `off`: fr[f][s] is this lane's value for MFMA step s.
+template <int T, int BK, bool KC, int F>
+__device__ __forceinline__ void read_frags(const float *lds, int off, int g, int lane,
+                                           f4 (&fr)[F]) {
+    const int lo = lane & 31;
+    const int hi = lane >> 5;
+    if constexpr (KC) {
+#pragma unroll
+        for (int f = 0; f < F; ++f)
+            fr[f] = *reinterpret_cast<const f4 *>(lds + (off + f * 32 + lo) * (BK + PAD_K) +
+                                                  8 * g + 4 * hi);
+    } else {
+#pragma unroll
+        for (int f = 0; f < F; ++f)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                fr[f][s] = lds[(8 * g + 4 * hi + s) * (T + PAD_I) + off + f * 32 + lo];
+    }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, bool AV, bool BV>
+__global__ void __launch_bounds__(WM *WN * 64)
+gemm_mfma_kernel(TiledArgs p) {
+    constexpr int NT = WM * WN * 64;
+    constexpr int WTM = BM / WM;
+    constexpr int WTN = BN / WN;
+    constexpr int FM = WTM / 32;
+    constexpr int FN = WTN / 32;
+    static_assert(FM >= 1 && FN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "bad wave tile");
+    static_assert(BK % 8 == 0, "BK must be a multiple of 8");
+    constexpr int A_FL = TileFloats<BM, BK, AKC>::value;
+    constexpr int B_FL = TileFloats<BN, BK, BKC>::value;
+    constexpr int STAGE = A_FL + B_FL;
+    __shared__ __attribute__((aligned(16))) float smem[2 * STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / WN;
+    const int wn = wave % WN;
+
+    // ---- work-group -> (batch, tile) with XCD-contiguous chunks and grouped raster ----
+    int pid = blockIdx.x;
+    const int total = p.total;
+    if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
+    const int per_batch = p.tiles_m * p.tiles_n;
+    const int b = pid / per_batch;
+    const int t = pid - b * per_batch;
+    constexpr int GROUP = 8;
+    const int in_group = GROUP * p.tiles_n;
+    const int first_m = (t / in_group) * GROUP;
+    const int gsz = min(p.tiles_m - first_m, GROUP);
+    const int tm = first_m + (t % in_group) % gsz;
+    const int tn = (t % in_group) / gsz;
+    const int m0 = tm * BM;
+    const int n0 = tn * BN;
+
+    const float *Ab = p.A + (int64_t)b * p.sA;
+    const float *Bb = p.B + (int64_t)b * p.sB;
+
+    Operand<BM, BK, NT, AKC, AV> opa;
+    Operand<BN, BK, NT, BKC, BV> opb;
+
+    f16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int K = p.K;
+    const int nk = (K + BK - 1) / BK;
+    const int nfull = K / BK;
+
+    opa.load(Ab, p.lda, m0, p.M, 0, K, nfull == 0, tid);
+    opb.load(Bb, p.ldb, n0, p.N, 0, K, nfull == 0, tid);
+    opa.store(smem, tid);
+    opb.store(smem + A_FL, tid);
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const float *cur = smem + (kt & 1) * STAGE;
+        float *nxt = smem + ((kt + 1) & 1) * STAGE;
+        const bool more = kt + 1 < nk;
+        if (more) {
+            const bool tail = kt + 1 >= nfull;
+            opa.load(Ab, p.lda, m0, p.M, (kt + 1) * BK, K, tail, tid);
+            opb.load(Bb, p.ldb, n0, p.N, (kt + 1) * BK, K, tail, tid);
+        }
+#pragma unroll
+        for (int g = 0; g < BK / 8; ++g) {
+            f4 fa[FM];
+            f4 fb[FN];
+            read_frags<BM, BK, AKC, FM>(cur, wm * WTM, g, lane, fa);
+            read_frags<BN, BK, BKC, FN>(cur + A_FL, wn * WTN, g, lane, fb);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s],
+                                                                         acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            opa.store(nxt, tid);
+            opb.store(nxt + A_FL, tid);
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue: accumulator (i, j) register r holds C row 8*(r/4) + 4*(lane/32) +
+    // r%4, column lane%32 of its 32x32 block; bias is added after the k loop ----
+    const int lo = lane & 31;
+    const int hi = lane >> 5;
+    float *Cb = p.C + (int64_t)b * p.sC;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int col = n0 + wn * WTN + j * 32 + lo;
+        const bool cok = col < p.N;
+        float bv = 0.f;
+        if (p.bias != nullptr && cok) bv = p.bias[col];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+                if (cok && row < p.M) {
+                    float v = acc[i][j][r];
+                    if (p.bias != nullptr) v = v + bv;
+                    Cb[(int64_t)row * p.ldc + col] = v;
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------
+// Host-side selection.
+
+struct TileCfg {
+    int bm, bn;
+};
+
+template <int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, bool AV, bool BV>
+int launch_one(hipStream_t s, const TiledArgs &a) {
+    hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AKC, BKC, AV, BV>),
+                       dim3(a.total), dim3(WM * WN * 64), 0, s, a);
+    return hip_check(hipGetLastError(), "gemm_mfma_kernel launch");
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC>
+int launch_vec(hipStream_t s, const TiledArgs &a, bool av, bool bv) {
+    if (av) {
+        if (bv) return launch_one<BM, BN, BK, WM, WN, AKC, BKC, true, true>(s, a);
+        return launch_one<BM, BN, BK, WM, WN, AKC, BKC, true, false>(s, a);
+    }
+    if (bv) return launch_one<BM, BN, BK, WM, WN, AKC, BKC, false, true>(s, a);
+    return launch_one<BM, BN, BK, WM, WN, AKC, BKC, false, false>(s, a);
+}
+
+template <int BM, int BN, int BK, int WM, int WN>
+int launch_layout(hipStream_t s, const TiledArgs &a, bool akc, bool bkc, bool av, bool bv) {
+    if (akc) {
+        if (bkc) return launch_vec<BM, BN, BK, WM, WN, true, true>(s, a, av, bv);
+        return launch_vec<BM, BN, BK, WM, WN, true, false>(s, a, av, bv);
+    }
+    if (bkc) return launch_vec<BM, BN, BK, WM, WN, false, true>(s, a, av, bv);
+    return launch_vec<BM, BN, BK, WM, WN, false, false>(s, a, av, bv);
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
+    // Operand orientation: A is K-contiguous unless transposed; B is K-contiguous only
+    // when transposed.
+    const bool akc = !d.transA;
+    const bool bkc = d.transB;
+    // 128-bit loads need a 16-byte aligned start for every batch entry, a leading
+    // dimension that keeps rows 16-byte aligned and a contiguous extent that is a
+    // multiple of 4 (so a float4 is entirely inside or entirely outside the matrix).
+    const bool av = aligned16(d.A) && d.lda % 4 == 0 && (d.batch == 1 || d.sA % 4 == 0) &&
+                    (akc ? d.K % 4 == 0 : d.M % 4 == 0);
+    const bool bv = aligned16(d.B) && d.ldb % 4 == 0 && (d.batch == 1 || d.sB % 4 == 0) &&
+                    (bkc ? d.K % 4 == 0 : d.N % 4 == 0);
+
+    TiledArgs a;
+    a.A = d.A;
+    a.B = d.B;
+    a.bias = d.bias;
+    a.C = d.C;
+    a.lda = d.lda;
+    a.ldb = d.ldb;
+    a.ldc = d.ldc;
+    a.sA = d.sA;
+    a.sB = d.sB;
+    a.sC = d.sC;
+    a.M = d.M;
+    a.N = d.N;
+    a.K = d.K;
+
+    auto tiles = [&](int bm, int bn) {
+        return (int64_t)((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn) * d.batch;
+    };
+    // Pick the largest tile that still gives the 256 CUs enough work-groups.
+    int cfg;
+    if (tiles(128, 128) >= 512)
+        cfg = 128;
+    else if (tiles(64, 64) >= 256)
+        cfg = 64;
+    else
+        cfg = 32;
+    a.tiles_m = (d.M + cfg - 1) / cfg;
+    a.tiles_n = (d.N + cfg - 1) / cfg;
+    const int64_t total = tiles(cfg, cfg);
+    if (total > INT32_MAX)
+        return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm: %lld tiles exceed one launch",
+                         (long long)total);
+    a.total = (int)total;
+    switch (cfg) {
+        case 128: return launch_layout<128, 128, 32, 2, 2>(stream, a, akc, bkc, av, bv);
+        case 64: return launch_layout<64, 64, 32, 2, 2>(stream, a, akc, bkc, av, bv);
+        default: return launch_layout<32, 32, 32, 1, 1>(stream, a, akc, bkc, av, bv);
+    }
+}
+
+}  // namespace migemm

@@ -1,0 +1,51 @@
+// Internal declarations shared by the HIP translation units of libmigemm.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/migemm.h"
+
+namespace migemm {
+
+// Thread-local last-error message (returned by migemm_last_error()).
+int set_error(int code, const char *fmt, ...);
+void clear_error();
+
+// Checks a HIP status; on failure records the message and returns MIGEMM_ERR_HIP.
+int hip_check(hipError_t e, const char *what);
+
+#define MIGEMM_HIP(call)                                   \
+    do {                                                   \
+        int _rc = ::migemm::hip_check((call), #call);      \
+        if (_rc != MIGEMM_OK) return _rc;                  \
+    } while (0)
+
+// Description of one (possibly batched, possibly transposed) fp32 GEMM after
+// validation: C_b = opA(A_b) * opB(B_b) (+ bias).
+struct GemmDesc {
+    const float *A;
+    const float *B;
+    const float *bias;
+    float *C;
+    int64_t lda, ldb, ldc;
+    int64_t sA, sB, sC;
+    int M, N, K, batch;
+    bool transA, transB;
+};
+
+// Launchers. They assume a validated descriptor and only enqueue work.
+int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d);
+int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d);
+bool skinny_applicable(const GemmDesc &d);
+
+// Device workspace owned by the library (one growing buffer per device), used by
+// split reductions. Returns nullptr and records MIGEMM_ERR_WORKSPACE on failure.
+void *workspace(size_t bytes, int *status);
+
+int launch_permute(hipStream_t stream, const float *src, float *dst,
+                   const int *src_dims, const int *axes, int num_dims, int64_t total);
+int launch_column_sum(hipStream_t stream, const float *X, float *Y,
+                      int outer, int axis, int inner);
+
+}  // namespace migemm

@@ -1,0 +1,71 @@
+"""Parity helpers shared by the GPU tests: run a GEMM form through the C ABI on the GPU and
+check it against the oracle (fp64 evaluation + the restated reference arithmetic).
+
+Bar (stated by the matmul path's north star): relative error <= 1e-5 * sqrt(K) against fp64,
+both normwise ||C - C64||_F / ||C64||_F and componentwise max |C - C64| / (|A||B|)."""
+import numpy as np
+import torch
+
+import oracle
+
+
+def dev(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0")
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def sample_rows(M, count=24, seed=0):
+    """Rows that cover every tile edge class: first/last rows, 32/64/128 boundaries, random."""
+    rows = {0, M - 1}
+    for b in (31, 32, 63, 64, 127, 128, 255, 256):
+        if b < M:
+            rows.add(b)
+    rng = np.random.default_rng(seed)
+    rows.update(int(r) for r in rng.integers(0, M, size=count))
+    return sorted(rows)
+
+
+def check_gemm(C, A, B, transA, transB, bias=None, M=None, N=None, K=None, lda=None, ldb=None,
+               sA=0, sB=0, batch=1, rows=None, ref=None):
+    """Compare GPU output C (numpy [batch, M, N]) with fp64 on the selected rows.
+    Returns (normwise, componentwise, vs_ref) where vs_ref is the componentwise distance to
+    the restated reference arithmetic `ref` (if given)."""
+    C = np.asarray(C).reshape(batch, M, N)
+    rows = list(range(M)) if rows is None else rows
+    tol = oracle.tolerance(K)
+    worst_nw = worst_cw = 0.0
+    vs_ref = 0.0
+    # contiguous runs of rows keep the fp64 calls few
+    runs = []
+    for r in rows:
+        if runs and runs[-1][1] == r:
+            runs[-1][1] = r + 1
+        else:
+            runs.append([r, r + 1])
+    c64_parts, ap_parts, c_parts, ref_parts = [], [], [], []
+    for r0, r1 in runs:
+        kw = dict(M=M, N=N, K=K, lda=lda, ldb=ldb, sA=sA, sB=sB, batch=batch, rows=(r0, r1))
+        c64_parts.append(oracle.gemm_f64(A, B, transA, transB, bias, **kw))
+        ap_parts.append(oracle.gemm_absprod(A, B, transA, transB, bias, **kw))
+        c_parts.append(C[:, r0:r1, :])
+        if ref is not None:
+            ref_parts.append(np.asarray(ref).reshape(batch, M, N)[:, r0:r1, :])
+    c64 = np.concatenate(c64_parts, axis=1)
+    ap = np.concatenate(ap_parts, axis=1)
+    cg = np.concatenate(c_parts, axis=1)
+    worst_nw, worst_cw = oracle.errors(cg, c64, ap)
+    if ref is not None:
+        rr = np.concatenate(ref_parts, axis=1).astype(np.float64)
+        with np.errstate(divide="ignore", invalid="ignore"):
+            d = np.abs(cg.astype(np.float64) - rr)
+            vs_ref = float(np.max(np.where(ap > 0, d / ap, np.where(d > 0, np.inf, 0.0))))
+    assert np.all(np.isfinite(cg)), "non-finite output"
+    assert worst_nw <= tol, f"normwise error {worst_nw:.3e} > {tol:.3e}"
+    assert worst_cw <= tol, f"componentwise error {worst_cw:.3e} > {tol:.3e}"
+    if ref is not None:
+        assert vs_ref <= 2 * tol, f"distance to the reference arithmetic {vs_ref:.3e}"
+    return worst_nw, worst_cw, vs_ref

@@ -1,0 +1,252 @@
+"""GPU parity of the HIP matmul path against the oracle, through the C ABI.
+
+Each case prints what it runs before the GPU call, so a failure names its shape.
+Exactness: small-integer operands make every partial sum exactly representable, so the
+MFMA result must equal the reference arithmetic bit-for-bit; random operands are held to
+the 1e-5*sqrt(K) relative bar against fp64."""
+import itertools
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from parity import check_gemm, dev, host, sample_rows
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "small_cases.npz")
+
+
+def small_ints(shape, seed, lo=-4, hi=4):
+    rng = np.random.default_rng(seed)
+    return rng.integers(lo, hi + 1, size=shape).astype(np.float32)
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def gemm_gpu(nncl, A, B, transA=False, transB=False, bias=None):
+    out = nncl.gemm(dev(A), dev(B), transA=transA, transB=transB,
+                    bias=dev(bias) if bias is not None else None)
+    return host(out)
+
+
+# ------------------------------------------------------------------------ golden fixtures
+def test_golden_fixtures(nncl):
+    z = np.load(GOLDEN, allow_pickle=False)
+    meta = json.loads(bytes(z["meta"]).decode())
+    for m in meta:
+        name = m["name"]
+        say("golden", name)
+        A, B, C64, Cref = z[f"{name}.A"], z[f"{name}.B"], z[f"{name}.C64"], z[f"{name}.C_ref"]
+        M, K, N, ta, tb, batch = m["M"], m["K"], m["N"], m["transA"], m["transB"], m["batch"]
+        if m["bias"]:
+            bias = z[f"{name}.bias"]
+            got = host(nncl.LinearForward(dev(A), dev(B), dev(bias)))
+        else:
+            bias = None
+            got = host(nncl.BmmPermute(dev(A), dev(B), transA=bool(ta), transB=bool(tb)))
+        ap = oracle.gemm_absprod(A, B, ta, tb, bias, M=M, N=N, K=K, lda=M if ta else K,
+                                 ldb=K if tb else N, sA=A.shape[1] * A.shape[2],
+                                 sB=0 if B.shape[0] == 1 else K * N, batch=batch)
+        nw, cw = oracle.errors(got, C64, ap)
+        assert nw <= oracle.tolerance(K) and cw <= oracle.tolerance(K), (name, nw, cw)
+        nw2, cw2 = oracle.errors(got, Cref.astype(np.float64), ap)
+        assert cw2 <= 2 * oracle.tolerance(K), (name, cw2)
+
+
+# ------------------------------------------------------------------- exact known answers
+SHAPES = [(1, 1, 1), (5, 7, 3), (17, 33, 5), (64, 128, 96), (127, 129, 65), (128, 128, 128),
+          (200, 40, 300), (1000, 777, 3000), (2, 300, 1000), (4, 4096, 600), (300, 9, 257)]
+
+
+@pytest.mark.parametrize("M,K,N", SHAPES)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_small_int_exact_all_layouts(nncl, M, K, N, ta, tb):
+    say("exact", M, K, N, "transA", ta, "transB", tb)
+    A = small_ints((K, M) if ta else (M, K), M * 7 + K)
+    B = small_ints((N, K) if tb else (K, N), N * 3 + K)
+    Aop = A.T if ta else A
+    Bop = B.T if tb else B
+    expect = (Aop.astype(np.int64) @ Bop.astype(np.int64)).astype(np.float32)
+    got = gemm_gpu(nncl, A, B, bool(ta), bool(tb))
+    assert np.array_equal(got, expect)
+
+
+def test_probe_matrices_hit_every_edge(nncl):
+    """Single non-zero probes at tile boundaries of every tile size the dispatcher uses."""
+    for (M, K, N) in [(1000, 777, 3000), (100, 70, 90), (33, 65, 130)]:
+        for ta, tb in [(0, 0), (0, 1), (1, 0)]:
+            say("probe", M, K, N, ta, tb)
+            cases = list(itertools.product(
+                sorted({0, 31, 32, 63, 64, 127, 128, M - 1} & set(range(M))),
+                sorted({0, 7, 8, 31, 32, K - 1} & set(range(K))),
+                sorted({0, 31, 32, 127, 128, N - 1} & set(range(N)))))
+            rng = np.random.default_rng(M + K + N)
+            for idx in rng.choice(len(cases), size=min(12, len(cases)), replace=False):
+                i, k, j = cases[idx]
+                A = np.zeros((M, K), np.float32)
+                B = np.zeros((K, N), np.float32)
+                A[i, k] = 3.0
+                B[k, j] = 5.0
+                An = np.ascontiguousarray(A.T) if ta else A
+                Bn = np.ascontiguousarray(B.T) if tb else B
+                got = gemm_gpu(nncl, An, Bn, bool(ta), bool(tb))
+                nz = np.argwhere(got != 0)
+                assert nz.tolist() == [[i, j]] and got[i, j] == 15.0, ((M, K, N), (i, k, j))
+
+
+# --------------------------------------------------------------- output-boundary canary
+def test_writes_stay_inside_m_by_n(nncl):
+    """Pooled buffers may be larger than M*N (OpenCLBufferManager.cs:29-40): nothing
+    outside C's [M x N] per batch entry may change."""
+    M, K, N, batch = 70, 33, 45, 3
+    A = oracle.uniform((batch, M, K), 5, 0)
+    B = oracle.uniform((batch, K, N), 5, 1)
+    ldc = N + 7
+    strideC = M * ldc + 11
+    buf = torch.full((batch * strideC + 64,), float("nan"), device="cuda:0")
+    from my_pytchon_opencl_lib_amd import _native
+    import ctypes
+    a, b = dev(A), dev(B)
+    _native.call("migemm_gemm_strided_batched",
+                 ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), 0, 0, M, N, K,
+                 ctypes.c_void_p(a.data_ptr()), K, M * K, ctypes.c_void_p(b.data_ptr()), N,
+                 K * N, None, ctypes.c_void_p(buf.data_ptr()), ldc, strideC, batch)
+    out = host(buf)
+    mask = np.zeros(out.shape, bool)
+    for z in range(batch):
+        for r in range(M):
+            s = z * strideC + r * ldc
+            mask[s:s + N] = True
+    assert np.all(np.isnan(out[~mask])), "write outside [M x N]"
+    C = np.stack([out[z * strideC:z * strideC + M * ldc].reshape(M, ldc)[:, :N]
+                  for z in range(batch)])
+    check_gemm(C, A, B, 0, 0, M=M, N=N, K=K, lda=K, ldb=N, sA=M * K, sB=K * N, batch=batch)
+
+
+# -------------------------------------------------------------- properties between forms
+def test_nt_tn_equal_nn_on_materialised_transposes(nncl):
+    M, K, N = 300, 260, 200
+    A = oracle.normal((M, K), 3, 0)
+    B = oracle.normal((K, N), 3, 1)
+    say("forms", M, K, N)
+    nn = gemm_gpu(nncl, A, B)
+    nt = gemm_gpu(nncl, A, np.ascontiguousarray(B.T), transB=True)
+    tn = gemm_gpu(nncl, np.ascontiguousarray(A.T), B, transA=True)
+    # same MFMA operands in the same k order whatever the storage layout: bit-identical
+    assert np.array_equal(nn, nt)
+    assert np.array_equal(nn, tn)
+
+
+def test_broadcast_equals_per_batch_loop(nncl):
+    A = oracle.normal((6, 77, 50), 9, 0)
+    B = oracle.normal((1, 50, 90), 9, 1)
+    say("broadcast")
+    got = host(nncl.Bmm(dev(A), dev(B)))
+    for z in range(6):
+        assert np.array_equal(got[z], gemm_gpu(nncl, A[z], B[0]))
+
+
+def test_bias_epilogue_is_gemm_plus_row_add(nncl):
+    X = oracle.normal((2, 64, 1536), 2, 0)
+    W = oracle.uniform((1, 1536, 4096), 2, 1, -1 / 32, 1 / 32)
+    bias = oracle.uniform((4096,), 2, 2, -1 / 32, 1 / 32)
+    say("bias epilogue")
+    y = host(nncl.LinearForward(dev(X), dev(W), dev(bias)))
+    plain = host(nncl.Bmm(dev(X), dev(W)))
+    assert np.array_equal(y, (plain + bias).astype(np.float32))
+
+
+# ---------------------------------------------------------- BASELINE.json configurations
+def test_config1_nn_256(nncl):
+    A = oracle.uniform((256, 256), 0, 0)
+    B = oracle.uniform((256, 256), 0, 1)
+    say("config1 256^3")
+    C = gemm_gpu(nncl, A, B)
+    check_gemm(C, A, B, 0, 0, M=256, N=256, K=256, lda=256, ldb=256,
+               ref=oracle.matmul_tiled(A, B))
+
+
+def test_config2_attention_bmm(nncl):
+    Q = oracle.normal((32, 128, 64), 1, 0)
+    Kt = oracle.normal((32, 64, 128), 1, 1)
+    say("config2 QK^T")
+    S = host(nncl.Bmm(dev(Q), dev(Kt)))
+    check_gemm(S, Q, Kt, 0, 0, M=128, N=128, K=64, lda=64, ldb=128, sA=128 * 64, sB=64 * 128,
+               batch=32, ref=oracle.bmm(Q, Kt))
+    logits = oracle.normal((32, 128, 128), 1, 2).astype(np.float64)
+    e = np.exp(logits - logits.max(axis=-1, keepdims=True))
+    P = (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
+    V = oracle.normal((32, 128, 64), 1, 3)
+    say("config2 PV")
+    O = host(nncl.Bmm(dev(P), dev(V)))
+    check_gemm(O, P, V, 0, 0, M=128, N=64, K=128, lda=128, ldb=64, sA=128 * 128, sB=128 * 64,
+               batch=32, ref=oracle.bmm(P, V))
+
+
+def test_config3_lstm_gate_gemm(nncl):
+    X = oracle.normal((64, 1536), 2, 0)
+    W = oracle.uniform((1536, 4096), 2, 1, -1 / 32, 1 / 32)
+    bias = oracle.uniform((4096,), 2, 2, -1 / 32, 1 / 32)
+    say("config3 lstm gate")
+    from my_pytchon_opencl_lib_amd import _native
+    import ctypes
+    x, w, b = dev(X), dev(W), dev(bias)
+    out = torch.empty((64, 4096), device="cuda:0")
+    _native.call("migemm_lstm_gemm_xw", ctypes.c_void_p(torch.cuda.current_stream().cuda_stream),
+                 ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(w.data_ptr()),
+                 ctypes.c_void_p(b.data_ptr()), ctypes.c_void_p(out.data_ptr()), 64, 1536, 4096)
+    check_gemm(host(out), X, W, 0, 0, bias=bias, M=64, N=4096, K=1536, lda=1536, ldb=4096,
+               ref=oracle.lstm_gemm_xw(X, W, bias))
+
+
+@pytest.mark.parametrize("form", ["NN", "NT", "TN"])
+def test_config4_4096_cube(nncl, form):
+    n = 4096
+    A = oracle.normal((n, n), 3, 0, 0.0, 1.0 / 64)
+    B = oracle.normal((n, n), 3, 1, 0.0, 1.0 / 64)
+    ta, tb = {"NN": (0, 0), "NT": (0, 1), "TN": (1, 0)}[form]
+    say("config4", form)
+    C = gemm_gpu(nncl, A, B, bool(ta), bool(tb))
+    check_gemm(C, A, B, ta, tb, M=n, N=n, K=n, lda=n, ldb=n, rows=sample_rows(n, 16))
+
+
+def test_config5a_ragged(nncl):
+    A = oracle.uniform((1000, 777), 4, 0)
+    B = oracle.uniform((777, 3000), 4, 1)
+    say("config5a ragged")
+    C = gemm_gpu(nncl, A, B)
+    rows = sample_rows(1000, 40)
+    ref = oracle.matmul_rows(A, B, 0, 1000, threads=8)
+    check_gemm(C, A, B, 0, 0, M=1000, N=3000, K=777, lda=777, ldb=3000, rows=rows, ref=ref)
+
+
+def test_config5b_gemv(nncl):
+    A = oracle.uniform((1, 4096), 4, 2)
+    B = oracle.uniform((4096, 11008), 4, 3)
+    say("config5b gemv")
+    C = gemm_gpu(nncl, A, B)
+    check_gemm(C, A, B, 0, 0, M=1, N=11008, K=4096, lda=4096, ldb=11008,
+               ref=oracle.matmul_rows(A, B, 0, 1, threads=8))
+    # repeated calls reuse the arrival counters: the result must not change
+    C2 = gemm_gpu(nncl, A, B)
+    assert np.array_equal(C, C2)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_skinny_rows_and_bias(nncl, M):
+    K, N = 1000, 1030  # N not a multiple of 4 -> scalar loads; K not a slice multiple
+    A = oracle.uniform((M, K), 6, M)
+    B = oracle.uniform((K, N), 6, 10 + M)
+    bias = oracle.uniform((N,), 6, 20 + M)
+    say("skinny", M)
+    C = gemm_gpu(nncl, A, B, bias=bias)
+    check_gemm(C, A, B, 0, 0, bias=bias, M=M, N=N, K=K, lda=K, ldb=N)
+    At = np.ascontiguousarray(A.T)
+    C2 = gemm_gpu(nncl, At, B, transA=True, bias=bias)
+    assert np.array_equal(C, C2)

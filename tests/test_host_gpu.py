@@ -1,0 +1,169 @@
+"""The reference's own hot-path tests, re-run through the host API (NnClGlob mirror) on the
+HIP kernels. Shapes follow the reference tests; inputs come from this repository's seeded
+generator (the reference's are unseeded numpy draws). Each test also applies the reference
+tests' own bar (np.testing.assert_allclose rtol=atol=1e-4 against PyTorch CPU) next to the
+fp64 bar of the matmul path."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from parity import check_gemm, dev, host
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def test_matmul_tiled_reference_shape(nncl):
+    """tests/test_matrix_ops.py:87-131 (Test 2): M,K,N = 64,128,96."""
+    A = oracle.normal((64, 128), 10, 0)
+    B = oracle.normal((128, 96), 10, 1)
+    say("test_matrix_ops matmul 64x128x96")
+    import ctypes
+    from my_pytchon_opencl_lib_amd import _native
+    a, b = dev(A), dev(B)
+    c = torch.empty((64, 96), device="cuda:0")
+    _native.call("migemm_matmul_tiled", ctypes.c_void_p(torch.cuda.current_stream().cuda_stream),
+                 ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(b.data_ptr()),
+                 ctypes.c_void_p(c.data_ptr()), 64, 128, 96)
+    C = host(c)
+    np.testing.assert_allclose(C, torch.matmul(torch.from_numpy(A), torch.from_numpy(B)).numpy(),
+                               rtol=1e-4, atol=1e-4)
+    check_gemm(C, A, B, 0, 0, M=64, N=96, K=128, lda=128, ldb=96, ref=oracle.matmul_tiled(A, B))
+
+
+def test_bmm_tiled_reference_shape(nncl):
+    """tests/test_bmm.py:6-74: BATCH=4, M,K,N = 32,64,32 (the reference swallows failures
+    there, test_bmm.py:69-74; here they fail)."""
+    A = oracle.normal((4, 32, 64), 11, 0)
+    B = oracle.normal((4, 64, 32), 11, 1)
+    say("test_bmm 4x32x64x32")
+    C = host(nncl.bmm(dev(A), dev(B)))
+    np.testing.assert_allclose(C, torch.bmm(torch.from_numpy(A), torch.from_numpy(B)).numpy(),
+                               rtol=1e-4, atol=1e-4)
+    check_gemm(C, A, B, 0, 0, M=32, N=32, K=64, lda=64, ldb=32, sA=32 * 64, sB=64 * 32,
+               batch=4, ref=oracle.bmm(A, B))
+
+
+def test_bmm_glob_pipeline(nncl):
+    """tests/test_nncl_glob.py:118-177: BATCH,M,K,N = 4,32,64,48; forward, then
+    bmm_backward(grad_output, A, B) checked against PyTorch autograd."""
+    A = oracle.normal((4, 32, 64), 777, 0)
+    B = oracle.normal((4, 64, 48), 777, 1)
+    G = oracle.normal((4, 32, 48), 777, 2)
+    say("test_bmm_glob_pipeline")
+    C = host(nncl.bmm(dev(A), dev(B)))
+    gA, gB = nncl.bmm_backward(dev(G), dev(A), dev(B))
+    gA, gB = host(gA), host(gB)
+    tA = torch.tensor(A, requires_grad=True)
+    tB = torch.tensor(B, requires_grad=True)
+    tC = torch.bmm(tA, tB)
+    tC.backward(torch.tensor(G))
+    np.testing.assert_allclose(C, tC.detach().numpy(), rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(gA, tA.grad.numpy(), rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(gB, tB.grad.numpy(), rtol=1e-4, atol=1e-4)
+    # fp64 bar: dA = dC B^T (NT over N=48), dB = A^T dC (TN over M=32)
+    check_gemm(gA, G, B, 0, 1, M=32, N=64, K=48, lda=48, ldb=48, sA=32 * 48, sB=64 * 48,
+               batch=4)
+    check_gemm(gB, A, G, 1, 0, M=64, N=48, K=32, lda=64, ldb=48, sA=32 * 64, sB=32 * 48,
+               batch=4)
+    # grad_A is a separate tensor: the reference's "bmm_c" aliasing (BmmOp.cs:47,60) is gone
+    assert gA.shape == (4, 32, 64) and gB.shape == (4, 64, 48)
+
+
+def test_linear_via_permute_and_bmm(nncl):
+    """tests/test_layers.py:88-112 with core/layers.py:21-33: Linear(16 -> 8) on 8 tokens,
+    weight [out, in] transposed by permute([1, 0]) then bmm."""
+    x = oracle.normal((2, 4, 16), 42, 0)
+    bound = 1.0 / np.sqrt(16)
+    w = oracle.uniform((8, 16), 42, 1, -bound, bound)
+    say("test_layers Linear")
+    wt = nncl.permute(dev(w), [1, 0])
+    assert np.array_equal(host(wt), w.T)
+    y = host(nncl.bmm(dev(x.reshape(1, 8, 16)), wt.unsqueeze(0).contiguous()))
+    ref = torch.nn.functional.linear(torch.from_numpy(x), torch.from_numpy(w)).numpy()
+    np.testing.assert_allclose(y.reshape(-1, 8), ref.reshape(-1, 8), rtol=1e-4, atol=1e-4)
+
+
+def test_linear_op_backward(nncl):
+    """cs/core/LinearOp.cs:16-49 (dX NT, dW TN + batch sum, db column sum) against
+    PyTorch autograd and fp64, on the TestLSTMRealTrain-style ragged N."""
+    from my_pytchon_opencl_lib_amd.autograd import LinearOp
+    batch, M, K, N = 3, 50, 40, 6565 // 50  # 131 columns: N not a multiple of 4
+    X = oracle.normal((batch, M, K), 12, 0)
+    W = oracle.uniform((1, K, N), 12, 1, -0.1, 0.1)
+    bias = oracle.uniform((N,), 12, 2, -0.1, 0.1)
+    G = oracle.normal((batch, M, N), 12, 3)
+    say("LinearOp backward")
+    y = nncl.LinearForward(dev(X), dev(W), dev(bias))
+    node = LinearOp(dev(X), dev(W), dev(bias), y, nncl)
+    gX, gW, gb = [host(t) for t in node.Backward(dev(G))]
+    tX = torch.tensor(X, requires_grad=True)
+    tW = torch.tensor(W, requires_grad=True)
+    tb = torch.tensor(bias, requires_grad=True)
+    ty = torch.matmul(tX, tW) + tb
+    ty.backward(torch.tensor(G))
+    np.testing.assert_allclose(host(y), ty.detach().numpy(), rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(gX, tX.grad.numpy(), rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(gW, tW.grad.numpy(), rtol=1e-4, atol=1e-3)
+    np.testing.assert_allclose(gb, tb.grad.numpy(), rtol=1e-4, atol=1e-4)
+    assert np.array_equal(gb, oracle.linear_bias_backward(G))  # same sequential order
+    check_gemm(gX, G, W, 0, 1, M=M, N=K, K=N, lda=N, ldb=N, sA=M * N, sB=0, batch=batch)
+    Xf = X.reshape(batch * M, K)
+    Gf = G.reshape(batch * M, N)
+    check_gemm(gW.reshape(K, N), Xf, Gf, 1, 0, M=K, N=N, K=batch * M, lda=K, ldb=N)
+
+
+def test_autograd_functions_match_torch(nncl):
+    from my_pytchon_opencl_lib_amd import autograd as ag
+    A = dev(oracle.normal((3, 20, 30), 13, 0)).requires_grad_()
+    B = dev(oracle.normal((1, 30, 25), 13, 1)).requires_grad_()
+    say("autograd bmm (broadcast B)")
+    out = ag.bmm(A, B)
+    g = dev(oracle.normal((3, 20, 25), 13, 2))
+    out.backward(g)
+    tA = A.detach().cpu().requires_grad_()
+    tB = B.detach().cpu().requires_grad_()
+    tout = torch.matmul(tA, tB)
+    tout.backward(g.cpu())
+    np.testing.assert_allclose(host(out), tout.detach().numpy(), rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(host(A.grad), tA.grad.numpy(), rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(host(B.grad), tB.grad.numpy(), rtol=1e-4, atol=1e-4)
+
+
+def test_permute_generic_and_transpose(nncl):
+    rng = np.random.default_rng(14)
+    for nd in range(1, 11):
+        shape = tuple(int(s) for s in rng.integers(1, 5, size=nd))
+        x = rng.standard_normal(shape).astype(np.float32)
+        axes = [int(a) for a in rng.permutation(nd)]
+        say("permute", shape, axes)
+        assert np.array_equal(host(nncl.Permute(dev(x), axes)), oracle.tensor_permute(x, axes))
+    x = oracle.normal((5, 70, 33), 14, 1)
+    assert np.array_equal(host(nncl.Permute(dev(x), [0, 2, 1])), x.transpose(0, 2, 1))
+
+
+def test_sum_and_bias_backward_bit_exact(nncl):
+    x = oracle.normal((4, 300, 37), 15, 0)
+    say("sum / bias backward")
+    for axis in (0, 1, 2):
+        got = host(nncl.Sum(dev(x), axis, keepDims=True))
+        assert np.array_equal(got, oracle.reduce_sum_axis(x, axis))
+    gb = host(nncl.LinearBiasBackward(dev(x), [37]))
+    assert np.array_equal(gb, oracle.linear_bias_backward(x))
+
+
+def test_shape_errors_before_launch(nncl):
+    from my_pytchon_opencl_lib_amd import ShapeError
+    a = dev(np.zeros((2, 3, 4), np.float32))
+    with pytest.raises(ShapeError):
+        nncl.Bmm(a, dev(np.zeros((3, 4, 5), np.float32)))  # batch 2 vs 3
+    with pytest.raises(ShapeError):
+        nncl.Bmm(a, dev(np.zeros((2, 5, 5), np.float32)))  # K 4 vs 5
+    with pytest.raises(ShapeError):
+        nncl.BmmPermute(a, dev(np.zeros((2, 5, 3), np.float32)), transB=True)
+    with pytest.raises(ShapeError):
+        nncl.Permute(a, [0, 1])

@@ -1,0 +1,239 @@
+"""Pins the CPU oracle (oracle/oracle.c) before anything is checked against it.
+
+The reference holds no golden vectors for the matmul path (its tests compare against live
+PyTorch at rtol=atol=1e-4: tests/test_matrix_ops.py:130, tests/test_bmm.py:70,
+tests/test_nncl_glob.py:165-173). The oracle is therefore pinned by what the mathematics
+fixes: exact known answers (every partial sum exactly representable), identities between
+the reference's forms, brute force against fp64 on tiny shapes, and library routines
+(numpy float64 matmul / transpose / cumulative sums). A planted-mistake test shows the
+known-answer tests catch a transposed operand, a dropped k term and a wrong bias.
+"""
+import itertools
+import json
+import os
+
+import numpy as np
+import pytest
+from hypothesis import given, settings, strategies as st
+
+import oracle
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def small_ints(shape, seed, lo=-4, hi=4):
+    rng = np.random.default_rng(seed)
+    return rng.integers(lo, hi + 1, size=shape).astype(np.float32)
+
+
+# ------------------------------------------------------------------------------ generator
+def test_generator_c_matches_numpy_mirror():
+    for seed, tid, n in [(0, 0, 1000), (3, 2, 4097), (12345, 7, 333)]:
+        c = oracle.uniform((n,), seed, tid)
+        p = oracle.uniform_np((n,), seed, tid)
+        assert np.array_equal(c, p)
+        assert c.min() >= -1.0 and c.max() < 1.0
+        cn = oracle.normal((n,), seed, tid)
+        pn = oracle.normal_np((n,), seed, tid)
+        # libm vs numpy cos/log may differ in the last double bit; fp32 rounding absorbs it
+        assert np.max(np.abs(cn.astype(np.float64) - pn)) <= 1e-6 * max(1.0, np.abs(cn).max())
+
+
+def test_generator_golden_values():
+    with open(os.path.join(GOLDEN, "generator.json")) as f:
+        g = json.load(f)
+    for case in g["uniform"]:
+        v = oracle.uniform((len(case["values"]),), case["seed"], case["tensor_id"],
+                           case["lo"], case["hi"])
+        assert v.tolist() == case["values"]
+    for case in g["normal"]:
+        v = oracle.normal((len(case["values"]),), case["seed"], case["tensor_id"],
+                          case["mean"], case["std"])
+        np.testing.assert_allclose(v, np.array(case["values"], dtype=np.float32), rtol=1e-6,
+                                   atol=1e-6)
+
+
+def test_generator_statistics():
+    u = oracle.uniform((1 << 18,), 4, 1)
+    assert abs(u.mean()) < 0.01 and abs(u.var() - 1.0 / 3.0) < 0.01
+    z = oracle.normal((1 << 18,), 1, 1)
+    assert abs(z.mean()) < 0.01 and abs(z.std() - 1.0) < 0.01
+    w = oracle.uniform((1 << 16,), 2, 3, -1.0 / 32, 1.0 / 32)
+    assert w.min() >= -1.0 / 32 and w.max() < 1.0 / 32
+
+
+# ------------------------------------------------------------------- known-answer tests
+@pytest.mark.parametrize("M,K,N", [(1, 1, 1), (17, 33, 5), (64, 128, 96), (31, 300, 47)])
+def test_matmul_tiled_small_int_exact(M, K, N):
+    A = small_ints((M, K), 1)
+    B = small_ints((K, N), 2)
+    expect = (A.astype(np.int64) @ B.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(oracle.matmul_tiled(A, B), expect)
+
+
+def test_matmul_tiled_identity_ones_rank1():
+    rng = np.random.default_rng(5)
+    A = rng.standard_normal((37, 37)).astype(np.float32)
+    eye = np.eye(37, dtype=np.float32)
+    assert np.array_equal(oracle.matmul_tiled(A, eye), A)
+    assert np.array_equal(oracle.matmul_tiled(eye, A), A)
+    ones_a = np.ones((9, 777), np.float32)
+    ones_b = np.ones((777, 13), np.float32)
+    assert np.all(oracle.matmul_tiled(ones_a, ones_b) == 777.0)
+    u = small_ints((23, 1), 3)
+    v = small_ints((1, 29), 4)
+    assert np.array_equal(oracle.matmul_tiled(u, v), u @ v)
+
+
+def probe_case(M, K, N, i, k, j):
+    A = np.zeros((M, K), np.float32)
+    B = np.zeros((K, N), np.float32)
+    A[i, k] = 3.0
+    B[k, j] = 5.0
+    C = np.zeros((M, N), np.float32)
+    C[i, j] = 15.0
+    return A, B, C
+
+
+def test_matmul_tiled_probes_every_edge():
+    M, K, N = 19, 35, 21  # no dimension a multiple of the 16-wide tile
+    for i, k, j in itertools.product([0, 15, 16, 18], [0, 15, 16, 31, 32, 34], [0, 15, 16, 20]):
+        A, B, C = probe_case(M, K, N, i, k, j)
+        assert np.array_equal(oracle.matmul_tiled(A, B), C), (i, k, j)
+
+
+# --------------------------------------------------------- brute force vs fp64 / numpy
+@settings(max_examples=60, deadline=None)
+@given(st.integers(1, 33), st.integers(1, 33), st.integers(1, 33), st.integers(0, 2**31 - 1))
+def test_matmul_tiled_vs_fp64_brute_force(M, K, N, seed):
+    A = oracle.uniform((M, K), seed, 0)
+    B = oracle.uniform((K, N), seed, 1)
+    C = oracle.matmul_tiled(A, B)
+    ref = np.zeros((M, N))
+    for k in range(K):  # explicit fp64 triple loop over k
+        ref += np.outer(A[:, k].astype(np.float64), B[k, :].astype(np.float64))
+    absprod = np.abs(A.astype(np.float64)) @ np.abs(B.astype(np.float64))
+    nw, cw = oracle.errors(C, ref, absprod)
+    assert nw <= oracle.tolerance(K) and cw <= oracle.tolerance(K)
+
+
+def test_gemm_f64_matches_numpy():
+    rng = np.random.default_rng(9)
+    for ta, tb in itertools.product([0, 1], [0, 1]):
+        M, N, K = 13, 17, 19
+        A = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+        B = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+        bias = rng.standard_normal(N).astype(np.float32)
+        got = oracle.gemm_f64(A, B, ta, tb, bias, M=M, N=N, K=K, lda=A.shape[1],
+                              ldb=B.shape[1])[0]
+        a64 = A.astype(np.float64).T if ta else A.astype(np.float64)
+        b64 = B.astype(np.float64).T if tb else B.astype(np.float64)
+        np.testing.assert_allclose(got, a64 @ b64 + bias, rtol=1e-12, atol=1e-12)
+        ap = oracle.gemm_absprod(A, B, ta, tb, None, M=M, N=N, K=K, lda=A.shape[1],
+                                 ldb=B.shape[1])[0]
+        np.testing.assert_allclose(ap, np.abs(a64) @ np.abs(b64), rtol=1e-12)
+
+
+# ----------------------------------------------------- identities between the forms
+def test_bmm_broadcast_equals_per_batch_loop():
+    A = oracle.uniform((4, 32, 64), 7, 0)
+    B1 = oracle.uniform((1, 64, 48), 7, 1)
+    C = oracle.bmm(A, B1)
+    for z in range(4):
+        assert np.array_equal(C[z], oracle.matmul_tiled(A[z], B1[0]))
+
+
+def test_permute_forms_equal_materialised_transposes():
+    A = oracle.uniform((3, 20, 37), 8, 0)   # [b, M, K]
+    B = oracle.uniform((3, 37, 26), 8, 1)   # [b, K, N]
+    nn = oracle.bmm(A, B)
+    assert np.array_equal(oracle.bmm_permute(A, B), nn)  # same fma chain as bmm_tiled
+    Bt = np.ascontiguousarray(B.transpose(0, 2, 1))
+    At = np.ascontiguousarray(A.transpose(0, 2, 1))
+    assert np.array_equal(oracle.bmm_permute(A, Bt, transB=True), nn)
+    assert np.array_equal(oracle.bmm_permute(At, B, transA=True), nn)
+    assert np.array_equal(oracle.bmm_permute(At, Bt, transA=True, transB=True), nn)
+
+
+def test_linear_forward_is_bmm_plus_bias():
+    X = oracle.uniform((2, 33, 40), 2, 0)
+    W = oracle.uniform((40, 70), 2, 1, -1 / 32, 1 / 32)
+    b = oracle.uniform((70,), 2, 2, -1 / 32, 1 / 32)
+    Y = oracle.linear_forward(X, W, b)
+    assert np.array_equal(Y, oracle.bmm(X, W[None]) + b)
+    assert np.array_equal(oracle.lstm_gemm_xw(X[0], W, b), Y[0])
+
+
+def test_tensor_permute_matches_numpy():
+    rng = np.random.default_rng(11)
+    for nd in range(1, 11):
+        shape = tuple(int(s) for s in rng.integers(1, 4, size=nd))
+        x = rng.standard_normal(shape).astype(np.float32)
+        axes = list(rng.permutation(nd))
+        assert np.array_equal(oracle.tensor_permute(x, axes), np.transpose(x, axes))
+
+
+def test_reduce_sum_axis_sequential():
+    x = small_ints((3, 50, 7), 4).astype(np.float32)
+    np.testing.assert_array_equal(oracle.reduce_sum_axis(x, 1)[:, 0, :], x.sum(axis=1))
+    y = oracle.normal((3, 1001, 5), 1, 2)
+    seq = np.add.accumulate(y, axis=1, dtype=np.float32)[:, -1, :]  # float32, ascending
+    assert np.array_equal(oracle.reduce_sum_axis(y, 1)[:, 0, :], seq)
+    g = oracle.normal((2, 9, 6), 3, 3)
+    assert np.array_equal(oracle.linear_bias_backward(g),
+                          np.add.accumulate(g.reshape(-1, 6), axis=0, dtype=np.float32)[-1])
+
+
+# ---------------------------------------- the reference's own test shapes
+@pytest.mark.parametrize("batch,M,K,N", [(1, 64, 128, 96), (4, 32, 64, 32), (4, 32, 64, 48),
+                                         (1, 8, 16, 8), (1, 4, 8, 8)])
+def test_reference_test_shapes_within_tolerance(batch, M, K, N):
+    A = oracle.normal((batch, M, K), 777, 0)
+    B = oracle.normal((batch, K, N), 777, 1)
+    C = oracle.bmm(A, B)
+    ref = np.einsum("bmk,bkn->bmn", A.astype(np.float64), B.astype(np.float64))
+    ap = np.einsum("bmk,bkn->bmn", np.abs(A.astype(np.float64)), np.abs(B.astype(np.float64)))
+    nw, cw = oracle.errors(C, ref, ap)
+    assert nw <= oracle.tolerance(K) and cw <= oracle.tolerance(K)
+    # the reference tests' own bar
+    np.testing.assert_allclose(C, ref, rtol=1e-4, atol=1e-4)
+
+
+def test_matmul_rows_bit_identical_to_matmul_tiled():
+    A = oracle.uniform((40, 777), 4, 0)
+    B = oracle.uniform((777, 50), 4, 1)
+    full = oracle.matmul_tiled(A, B)
+    assert np.array_equal(oracle.matmul_rows(A, B, 0, 40, threads=2), full)
+    assert np.array_equal(oracle.matmul_rows(A, B, 7, 19, threads=1), full[7:19])
+
+
+# ------------------------------------------------------------------- planted mistakes
+def test_known_answer_tests_catch_planted_mistakes():
+    """Mutated copies of the restatement (a transposed operand, a dropped last k term, a
+    bias added twice) must each fail at least one known-answer check."""
+    A = small_ints((19, 35), 1)
+    B = small_ints((35, 21), 2)
+    exact = (A.astype(np.int64) @ B.astype(np.int64)).astype(np.float32)
+
+    def transposed_b(a, b):
+        # B(k, n) read at B[n*K + k] instead of B[k*N + n]: a transposed index formula
+        wrong = np.ascontiguousarray(b).reshape(1, b.shape[1], b.shape[0])
+        return oracle.bmm_permute(a[None], wrong, transB=True)[0]
+
+    def dropped_last_k(a, b):
+        return oracle.matmul_tiled(np.ascontiguousarray(a[:, :-1]),
+                                   np.ascontiguousarray(b[:-1, :]))
+
+    for bad in (transposed_b, dropped_last_k):
+        caught = not np.array_equal(bad(A, B), exact)
+        for (i, k, j) in [(0, 34, 0), (18, 0, 20), (5, 16, 7)]:
+            pa, pb, pc = probe_case(19, 35, 21, i, k, j)
+            caught |= not np.array_equal(bad(pa, pb), pc)
+        assert caught, bad.__name__
+
+    X = small_ints((1, 5, 6), 3)
+    W = small_ints((6, 4), 4)
+    bias = small_ints((4,), 5)
+    twice = oracle.linear_forward(X, W, bias) + bias
+    assert not np.array_equal(twice[0], (X[0] @ W) + bias)
+    assert np.array_equal(oracle.linear_forward(X, W, bias)[0], (X[0] @ W) + bias)
