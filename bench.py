@@ -57,17 +57,22 @@ def cpu_baseline(target_s):
         if elapsed >= target_s / 4 or rows >= n:
             break
         rows = min(n, int(rows * max(2.0, (target_s / 4) / max(elapsed, 1e-3))))
-    # final timed sample sized to about target_s
-    rows = min(n, max(rows, int(rows * target_s / max(elapsed, 1e-3))))
+    # final timed sample sized to about target_s (the whole GEMM, repeated, if it is fast)
+    reps = 1
+    if rows >= n:
+        reps = max(1, int(round(target_s / max(elapsed, 1e-3))))
+    else:
+        rows = min(n, max(rows, int(rows * target_s / max(elapsed, 1e-3))))
     t0 = time.perf_counter()
-    oracle.matmul_rows(A, B, 0, rows, threads=threads)
+    for _ in range(reps):
+        oracle.matmul_rows(A, B, 0, rows, threads=threads)
     elapsed = time.perf_counter() - t0
-    flop = 2.0 * rows * n * n
-    return {"value": flop / elapsed / 1e12, "unit": "TFLOP/s", "cores": threads,
+    flop = 2.0 * rows * n * n * reps
+    return {"value": round(flop / elapsed / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
-            "sample": f"rows 0..{rows} of the 4096^3 NN GEMM ({flop / 1e9:.1f} GFLOP) with the "
-                      f"oracle's matmul_tiled restatement (fp32 fma chains, ascending k), "
-                      f"{threads} threads, {elapsed:.1f} s",
+            "sample": f"{reps} x rows 0..{rows} of the 4096^3 NN GEMM ({flop / 1e9:.1f} GFLOP) "
+                      f"with the oracle's matmul_tiled restatement (fp32 fma chains, ascending "
+                      f"k; i-k-j order, AVX2), {threads} threads, {elapsed:.1f} s",
             "openmp": bool(oracle.lib().oracle_openmp_enabled())}
 
 
@@ -182,20 +187,30 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def measure_all_configs(torch, nncl, _native, reps=50):
-    """Per-config kernel time (mean of HIP-event timed launches) for DESIGN.md."""
+def measure_all_configs(torch, nncl, _native, reps=20):
+    """Per-config device time per call, from HIP events around a HIP graph that replays
+    `reps` back-to-back calls (so host launch overhead is not measured). Inputs rotate
+    where the working set must exceed the 256 MB MALL."""
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(0)
     out = {}
 
-    def timed(fn, reps=reps):
-        for _ in range(5):
-            fn()
+    def timed(fns):
+        for f in fns:
+            f()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps // len(fns)):
+                for f in fns:
+                    f()
+        graph.replay()
+        torch.cuda.synchronize()
         t = Timer(torch)
-        for _ in range(reps):
-            t.around(fn)
-        return t.mean_ms()
+        for _ in range(5):
+            t.around(graph.replay)
+        return t.mean_ms() / ((reps // len(fns)) * len(fns))
 
     def rec(name, ms, flop, byts):
         out[name] = {"us": round(ms * 1e3, 2), "tflops": round(flop / (ms * 1e-3) / 1e12, 3),
@@ -205,28 +220,29 @@ def measure_all_configs(torch, nncl, _native, reps=50):
                      "pct_hbm_peak": round(100 * byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2)}
 
     r = lambda *s: torch.rand(*s, device=dev, generator=g) * 2 - 1
-    A = r(256, 256)
-    B = r(256, 256)
-    rec("1_nn_256", timed(lambda: nncl.gemm(A, B)), 2 * 256 ** 3, 4 * 3 * 256 * 256)
+    A, B, C = r(256, 256), r(256, 256), torch.empty(256, 256, device=dev)
+    rec("1_nn_256", timed([lambda: nncl.gemm(A, B, out=C)]), 2 * 256 ** 3, 4 * 3 * 256 * 256)
     Q, Kt, P, V = r(32, 128, 64), r(32, 64, 128), r(32, 128, 128), r(32, 128, 64)
-    rec("2a_bmm_qk", timed(lambda: nncl.BmmPermute(Q, Kt)), 2 * 32 * 128 * 128 * 64,
+    S, O = torch.empty(32, 128, 128, device=dev), torch.empty(32, 128, 64, device=dev)
+    rec("2a_bmm_qk", timed([lambda: nncl.gemm(Q, Kt, out=S)]), 2 * 32 * 128 * 128 * 64,
         4 * 32 * (128 * 64 * 2 + 128 * 128))
-    rec("2b_bmm_pv", timed(lambda: nncl.BmmPermute(P, V)), 2 * 32 * 128 * 128 * 64,
+    rec("2b_bmm_pv", timed([lambda: nncl.gemm(P, V, out=O)]), 2 * 32 * 128 * 128 * 64,
         4 * 32 * (128 * 128 + 128 * 64 * 2))
-    X = r(100, 64, 1536)
-    W = r(1, 1536, 4096) / 32
+    X = r(20, 64, 1536)
+    W = r(1536, 4096) / 32
     bias = r(4096) / 32
-    steps = iter(range(10 ** 9))
-    rec("3_lstm_gate_step", timed(lambda: nncl.LinearForward(X[next(steps) % 100][None], W, bias)),
+    Y = torch.empty(64, 4096, device=dev)
+    rec("3_lstm_gate_step",
+        timed([lambda i=i: nncl.gemm(X[i], W, bias=bias, out=Y) for i in range(20)]),
         2 * 64 * 1536 * 4096, 4 * (64 * 1536 + 1536 * 4096 + 64 * 4096 + 4096))
-    A5, B5 = r(1000, 777), r(777, 3000)
-    rec("5a_ragged", timed(lambda: nncl.gemm(A5, B5)), 2 * 1000 * 3000 * 777,
+    A5, B5, C5 = r(1000, 777), r(777, 3000), torch.empty(1000, 3000, device=dev)
+    rec("5a_ragged", timed([lambda: nncl.gemm(A5, B5, out=C5)]), 2 * 1000 * 3000 * 777,
         4 * (1000 * 777 + 777 * 3000 + 1000 * 3000))
     x = r(1, 4096)
     copies = [r(4096, 11008) for _ in range(3)]  # 541 MB > the 256 MB MALL
-    it = iter(range(10 ** 9))
-    rec("5b_gemv", timed(lambda: nncl.gemm(x, copies[next(it) % 3])), 2 * 4096 * 11008,
-        4 * (4096 + 4096 * 11008 + 11008))
+    y = torch.empty(1, 11008, device=dev)
+    rec("5b_gemv", timed([lambda c=c: nncl.gemm(x, c, out=y) for c in copies]),
+        2 * 4096 * 11008, 4 * (4096 + 4096 * 11008 + 11008))
     return out
 
 

@@ -70,9 +70,10 @@ int hip_check(hipError_t e, const char *what) {
     return set_error(MIGEMM_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-// One growing buffer per device. The first 1 MiB holds arrival counters that every kernel
-// using them returns to zero; it is cleared once when the buffer is (re)allocated. Calls
-// that use the workspace must be ordered on one stream (they share the buffer).
+// One growing buffer per device. A buffer that is outgrown is retired, not freed: work
+// already queued, or a HIP graph captured earlier, may still refer to it, so retired
+// buffers live until the process ends. Calls that use the workspace must be ordered on
+// one stream (they share the buffer).
 void *workspace(size_t bytes, int *status) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -84,27 +85,16 @@ void *workspace(size_t bytes, int *status) {
     if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
     DeviceWorkspace &w = g_ws[dev];
     if (w.bytes < bytes) {
-        if (w.ptr != nullptr) {
-            // Work queued earlier may still read the old buffer.
-            e = hipDeviceSynchronize();
-            if (e == hipSuccess) e = hipFree(w.ptr);
-            w.ptr = nullptr;
-            w.bytes = 0;
-            if (e != hipSuccess) {
-                *status = hip_check(e, "workspace release");
-                return nullptr;
-            }
-        }
         size_t want = bytes < ((size_t)8 << 20) ? ((size_t)8 << 20) : bytes;
-        e = hipMalloc(&w.ptr, want);
-        if (e == hipSuccess) e = hipMemset(w.ptr, 0, want);
-        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (want < 2 * w.bytes) want = 2 * w.bytes;
+        void *p = nullptr;
+        e = hipMalloc(&p, want);
         if (e != hipSuccess) {
-            w.ptr = nullptr;
             *status = set_error(MIGEMM_ERR_WORKSPACE, "workspace of %zu bytes: %s", want,
                                 hipGetErrorString(e));
             return nullptr;
         }
+        w.ptr = p;  // the previous buffer (if any) is retired, never freed
         w.bytes = want;
     }
     *status = MIGEMM_OK;

@@ -26,10 +26,16 @@
 //  * Edges: rows beyond M / columns beyond N are clamped on load (they only feed outputs
 //    that are never stored); k >= K is zero-filled in both operands, as the reference's
 //    zero padding does (matmul.cl:39-52). Stores are guarded to [M x N].
+//  * Split-K: when the output has too few tiles to occupy the 256 CUs (skinny M, e.g. the
+//    64-row LSTM gate GEMM), the k-tiles are divided into S contiguous ranges; range s
+//    writes its fp32 partial tile to the library workspace and reduce_slices_kernel adds
+//    the S partials of each output in order s = 0..S-1, then the bias (deterministic).
 //  * Work-group ids are remapped so that consecutive output tiles land on the same XCD
 //    (the dispatcher deals work-groups round-robin over the 8 XCDs, each with its own
 //    L2), then rastered in groups of 8 tile-rows so concurrently running tiles share
 //    A and B panels in that L2.
+#include <stdlib.h>
+
 #include "migemm_internal.h"
 
 namespace migemm {
@@ -47,7 +53,11 @@ struct TiledArgs {
     int64_t sA, sB, sC;
     int M, N, K;
     int tiles_m, tiles_n;  // tiles per batch entry
-    int total;             // tiles_m * tiles_n * batch
+    int batch;
+    int total;             // tiles_m * tiles_n * batch * splits
+    int splits;            // split-K ranges (1 = no split)
+    int kt_per_split;      // k-tiles per range
+    float *partial;        // [splits][batch][M][N] partial sums when splits > 1
 };
 
 constexpr int PAD_K = 4;  // pad of a K-contiguous LDS tile row  [i][BK + 4]
@@ -197,6 +207,9 @@ gemm_mfma_kernel(TiledArgs p) {
     const int total = p.total;
     if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
     const int per_batch = p.tiles_m * p.tiles_n;
+    const int per_split = per_batch * p.batch;
+    const int split = pid / per_split;
+    pid -= split * per_split;
     const int b = pid / per_batch;
     const int t = pid - b * per_batch;
     constexpr int GROUP = 8;
@@ -223,19 +236,20 @@ gemm_mfma_kernel(TiledArgs p) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     const int K = p.K;
-    const int nk = (K + BK - 1) / BK;
-    const int nfull = K / BK;
+    const int nfull = K / BK;  // k-tiles entirely inside K; a later one is the zero-filled tail
+    const int kt0 = split * p.kt_per_split;
+    const int kt1 = min((K + BK - 1) / BK, kt0 + p.kt_per_split);
 
-    opa.load(Ab, p.lda, m0, p.M, 0, K, nfull == 0, tid);
-    opb.load(Bb, p.ldb, n0, p.N, 0, K, nfull == 0, tid);
+    opa.load(Ab, p.lda, m0, p.M, kt0 * BK, K, kt0 >= nfull, tid);
+    opb.load(Bb, p.ldb, n0, p.N, kt0 * BK, K, kt0 >= nfull, tid);
     opa.store(smem, tid);
     opb.store(smem + A_FL, tid);
     __syncthreads();
 
-    for (int kt = 0; kt < nk; ++kt) {
-        const float *cur = smem + (kt & 1) * STAGE;
-        float *nxt = smem + ((kt + 1) & 1) * STAGE;
-        const bool more = kt + 1 < nk;
+    for (int kt = kt0; kt < kt1; ++kt) {
+        const float *cur = smem + ((kt - kt0) & 1) * STAGE;
+        float *nxt = smem + ((kt - kt0 + 1) & 1) * STAGE;
+        const bool more = kt + 1 < kt1;
         if (more) {
             const bool tail = kt + 1 >= nfull;
             opa.load(Ab, p.lda, m0, p.M, (kt + 1) * BK, K, tail, tid);
@@ -267,6 +281,21 @@ gemm_mfma_kernel(TiledArgs p) {
     // r%4, column lane%32 of its 32x32 block; bias is added after the k loop ----
     const int lo = lane & 31;
     const int hi = lane >> 5;
+    if (p.splits > 1) {
+        float *Pb = p.partial + ((int64_t)split * p.batch + b) * p.M * p.N;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int col = n0 + wn * WTN + j * 32 + lo;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+                    if (col < p.N && row < p.M) Pb[(int64_t)row * p.N + col] = acc[i][j][r];
+                }
+        }
+        return;
+    }
     float *Cb = p.C + (int64_t)b * p.sC;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
@@ -286,6 +315,26 @@ gemm_mfma_kernel(TiledArgs p) {
                 }
             }
         }
+    }
+}
+
+// C_b[m, n] = partial[0][b][m][n] + ... + partial[S-1][b][m][n] (+ bias[n]), in order.
+__global__ void __launch_bounds__(256)
+reduce_slices_kernel(const float *__restrict__ partial, int slices, int batch, int M, int N,
+                     const float *__restrict__ bias, float *__restrict__ C, int64_t ldc,
+                     int64_t strideC) {
+    const int64_t total = (int64_t)batch * M * N;
+    const int64_t plane = total;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += step) {
+        const int64_t bm = t / N;
+        const int n = (int)(t - bm * N);
+        const int64_t b = bm / M;
+        const int m = (int)(bm - b * M);
+        float v = partial[t];
+        for (int s = 1; s < slices; ++s) v += partial[t + (int64_t)s * plane];
+        if (bias != nullptr) v = v + bias[n];
+        C[b * strideC + (int64_t)m * ldc + n] = v;
     }
 }
 
@@ -327,6 +376,25 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 }  // namespace
 
+int launch_reduce_slices(hipStream_t stream, const float *partial, int slices, int batch,
+                         int M, int N, const float *bias, float *C, int64_t ldc,
+                         int64_t strideC) {
+    const int64_t total = (int64_t)batch * M * N;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(reduce_slices_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       partial, slices, batch, M, N, bias, C, ldc, strideC);
+    return hip_check(hipGetLastError(), "reduce_slices_kernel launch");
+}
+
+namespace {
+// Tuning overrides (MIGEMM_TILE = 32 | 64 | 128, MIGEMM_SPLITK = S), read once.
+int env_int(const char *name) {
+    const char *v = getenv(name);
+    return v != nullptr ? atoi(v) : 0;
+}
+}  // namespace
+
 int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     // Operand orientation: A is K-contiguous unless transposed; B is K-contiguous only
     // when transposed.
@@ -354,30 +422,57 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     a.M = d.M;
     a.N = d.N;
     a.K = d.K;
+    a.batch = d.batch;
 
     auto tiles = [&](int bm, int bn) {
         return (int64_t)((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn) * d.batch;
     };
-    // Pick the largest tile that still gives the 256 CUs enough work-groups.
-    int cfg;
-    if (tiles(128, 128) >= 512)
+    const int nk32 = (d.K + 31) / 32;
+    // Largest tile that still gives the 256 CUs two work-groups each; otherwise 64x64
+    // tiles, split along K when K is long enough for every range to keep >= 4 k-tiles.
+    int cfg, splits = 1;
+    if (tiles(128, 128) >= 512) {
         cfg = 128;
-    else if (tiles(64, 64) >= 256)
+    } else if (tiles(64, 64) >= 512 || nk32 < 8) {
+        cfg = tiles(64, 64) >= 256 ? 64 : 32;
+    } else {
         cfg = 64;
-    else
-        cfg = 32;
+        const int64_t want = (512 + tiles(64, 64) - 1) / tiles(64, 64);
+        const int64_t cap = nk32 / 4 < 16 ? nk32 / 4 : 16;
+        splits = (int)(want < cap ? want : cap);
+        if (splits < 1) splits = 1;
+    }
+    static const int force_tile = env_int("MIGEMM_TILE");
+    static const int force_split = env_int("MIGEMM_SPLITK");
+    if (force_tile == 32 || force_tile == 64 || force_tile == 128) cfg = force_tile;
+    if (force_split >= 1) splits = force_split < nk32 ? force_split : nk32;
+
     a.tiles_m = (d.M + cfg - 1) / cfg;
     a.tiles_n = (d.N + cfg - 1) / cfg;
-    const int64_t total = tiles(cfg, cfg);
+    a.kt_per_split = (nk32 + splits - 1) / splits;
+    splits = (nk32 + a.kt_per_split - 1) / a.kt_per_split;  // no empty range
+    a.splits = splits;
+    a.partial = nullptr;
+    if (splits > 1) {
+        int st = MIGEMM_OK;
+        a.partial = static_cast<float *>(
+            workspace((size_t)splits * d.batch * d.M * d.N * sizeof(float), &st));
+        if (a.partial == nullptr) return st;
+    }
+    const int64_t total = tiles(cfg, cfg) * splits;
     if (total > INT32_MAX)
         return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm: %lld tiles exceed one launch",
                          (long long)total);
     a.total = (int)total;
+    int rc;
     switch (cfg) {
-        case 128: return launch_layout<128, 128, 32, 2, 2>(stream, a, akc, bkc, av, bv);
-        case 64: return launch_layout<64, 64, 32, 2, 2>(stream, a, akc, bkc, av, bv);
-        default: return launch_layout<32, 32, 32, 1, 1>(stream, a, akc, bkc, av, bv);
+        case 128: rc = launch_layout<128, 128, 32, 2, 2>(stream, a, akc, bkc, av, bv); break;
+        case 64: rc = launch_layout<64, 64, 32, 2, 2>(stream, a, akc, bkc, av, bv); break;
+        default: rc = launch_layout<32, 32, 32, 1, 1>(stream, a, akc, bkc, av, bv); break;
     }
+    if (rc != MIGEMM_OK || splits == 1) return rc;
+    return launch_reduce_slices(stream, a.partial, splits, d.batch, d.M, d.N, d.bias, d.C,
+                                d.ldc, d.sC);
 }
 
 }  // namespace migemm

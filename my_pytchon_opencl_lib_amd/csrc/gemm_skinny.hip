@@ -4,11 +4,13 @@
 //
 // Work split: a work-group of 4 wavefronts owns 256 consecutive columns (one float4 of
 // B per lane) and a slice of KC rows of K; wavefront w accumulates rows w, w+4, ... of
-// its slice with fp32 FMA chains, the 4 wavefronts are combined through LDS, and the
-// S = ceil(K / KC) slices of a column block are combined in slice order by whichever
-// work-group of that block finishes last (an atomic arrival counter per column block,
-// reset by that work-group, so no memset is needed between calls). The result is
-// deterministic: the association order depends only on (K, KC), never on timing.
+// its slice with fp32 FMA chains and the 4 wavefronts are combined through LDS. With
+// S = ceil(K / KC) > 1 slices, each slice writes its partial sums to the library
+// workspace and a second kernel (reduce_slices_kernel, gemm_mfma.hip) adds the S partials
+// of every output in slice order, then the bias. The result is deterministic: the
+// association order depends only on (K, KC), never on timing. (A single-kernel
+// "last work-group combines" variant needs an agent-scope release fence per work-group,
+// which writes back the XCD's whole L2 on MI355X and cost more than the GEMV itself.)
 #include "migemm_internal.h"
 
 namespace migemm {
@@ -32,14 +34,13 @@ struct SkinnyArgs {
     int kc;        // rows of K per slice (multiple of 4)
     int slices;    // ceil(K / kc)
     int cblocks;   // ceil(N / 256)
-    float *partial;          // [batch][slices][M][N] when slices > 1
-    unsigned int *counter;   // [batch][cblocks] arrival counters, zero between calls
+    float *partial;  // [slices][batch][M][N] when slices > 1
+    int batch;
 };
 
 template <int MR, bool VEC>
 __global__ void __launch_bounds__(SK_THREADS) gemm_skinny_kernel(SkinnyArgs p) {
     __shared__ f4 red[4][MR][64];
-    __shared__ int is_last;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -128,7 +129,7 @@ __global__ void __launch_bounds__(SK_THREADS) gemm_skinny_kernel(SkinnyArgs p) {
                 }
             }
         } else {
-            float *part = p.partial + (((int64_t)b * p.slices + s) * p.M) * p.N;
+            float *part = p.partial + (((int64_t)s * p.batch + b) * p.M) * p.N;
 #pragma unroll
             for (int m = 0; m < MR; ++m)
 #pragma unroll
@@ -136,32 +137,6 @@ __global__ void __launch_bounds__(SK_THREADS) gemm_skinny_kernel(SkinnyArgs p) {
                     if (n + e < p.N) part[(int64_t)m * p.N + n + e] = tot[m][e];
         }
     }
-    if (p.slices == 1) return;
-
-    // Arrival: release this slice's partial sums, count the work-group in.
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        unsigned int prev = atomicAdd(&p.counter[(int64_t)b * p.cblocks + cb], 1u);
-        is_last = (prev == (unsigned int)p.slices - 1u);
-    }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();  // acquire the other slices' partial sums
-
-    // The last work-group of this column block sums slices 0..S-1 in order.
-    for (int idx = tid; idx < MR * SK_COLS; idx += SK_THREADS) {
-        const int m = idx / SK_COLS;
-        const int col = cb * SK_COLS + idx % SK_COLS;
-        if (col >= p.N) continue;
-        const float *part = p.partial + ((int64_t)b * p.slices * p.M + m) * p.N + col;
-        float v = __builtin_nontemporal_load(part);
-        for (int q = 1; q < p.slices; ++q)
-            v += __builtin_nontemporal_load(part + (int64_t)q * p.M * p.N);
-        if (p.bias != nullptr) v = v + p.bias[col];
-        p.C[(int64_t)b * p.sC + (int64_t)m * p.ldc + col] = v;
-    }
-    if (tid == 0) p.counter[(int64_t)b * p.cblocks + cb] = 0u;
 }
 
 template <int MR>
@@ -214,30 +189,25 @@ int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {
         a.slices = (d.K + a.kc - 1) / a.kc;
     }
     a.partial = nullptr;
-    a.counter = nullptr;
-    // Arrival counters occupy the first kCounterBytes of the library workspace (kept at
-    // zero between calls); partial sums follow. Too many column blocks: no split.
-    constexpr size_t kCounterBytes = (size_t)1 << 20;
-    if ((size_t)d.batch * a.cblocks * sizeof(unsigned int) > kCounterBytes) {
-        a.kc = d.K;
-        a.slices = 1;
-    }
+    a.batch = d.batch;
     if (a.slices > 1) {
-        const size_t part_bytes = (size_t)d.batch * a.slices * d.M * d.N * sizeof(float);
+        const size_t part_bytes = (size_t)a.slices * d.batch * d.M * d.N * sizeof(float);
         int st = MIGEMM_OK;
-        char *ws = static_cast<char *>(workspace(kCounterBytes + part_bytes, &st));
-        if (ws == nullptr) return st;
-        a.counter = reinterpret_cast<unsigned int *>(ws);
-        a.partial = reinterpret_cast<float *>(ws + kCounterBytes);
+        a.partial = static_cast<float *>(workspace(part_bytes, &st));
+        if (a.partial == nullptr) return st;
     }
     const bool vec = (reinterpret_cast<uintptr_t>(d.B) & 15u) == 0 && d.ldb % 4 == 0 &&
                      d.N % 4 == 0 && (d.batch == 1 || d.sB % 4 == 0);
+    int rc;
     switch (d.M) {
-        case 1: return launch_mr<1>(stream, a, vec, d.batch);
-        case 2: return launch_mr<2>(stream, a, vec, d.batch);
-        case 3: return launch_mr<3>(stream, a, vec, d.batch);
-        default: return launch_mr<4>(stream, a, vec, d.batch);
+        case 1: rc = launch_mr<1>(stream, a, vec, d.batch); break;
+        case 2: rc = launch_mr<2>(stream, a, vec, d.batch); break;
+        case 3: rc = launch_mr<3>(stream, a, vec, d.batch); break;
+        default: rc = launch_mr<4>(stream, a, vec, d.batch); break;
     }
+    if (rc != MIGEMM_OK || a.slices == 1) return rc;
+    return launch_reduce_slices(stream, a.partial, a.slices, d.batch, d.M, d.N, d.bias, d.C,
+                                d.ldc, d.sC);
 }
 
 }  // namespace migemm

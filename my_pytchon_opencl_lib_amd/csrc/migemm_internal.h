@@ -40,8 +40,13 @@ int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d);
 bool skinny_applicable(const GemmDesc &d);
 
 // Device workspace owned by the library (one growing buffer per device), used by
-// split reductions. Returns nullptr and records MIGEMM_ERR_WORKSPACE on failure.
+// split-K partial sums. Returns nullptr and records MIGEMM_ERR_WORKSPACE on failure.
 void *workspace(size_t bytes, int *status);
+
+// C_b[m, n] = sum over s = 0..S-1 (in order) of partial[s][b][m][n] (+ bias[n]).
+int launch_reduce_slices(hipStream_t stream, const float *partial, int slices, int batch,
+                         int M, int N, const float *bias, float *C, int64_t ldc,
+                         int64_t strideC);
 
 int launch_permute(hipStream_t stream, const float *src, float *dst,
                    const int *src_dims, const int *axes, int num_dims, int64_t total);

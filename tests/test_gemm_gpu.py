@@ -250,3 +250,34 @@ def test_skinny_rows_and_bias(nncl, M):
     At = np.ascontiguousarray(A.T)
     C2 = gemm_gpu(nncl, At, B, transA=True, bias=bias)
     assert np.array_equal(C, C2)
+
+
+def test_graph_capture_replays_match_eager(nncl):
+    """Callers may capture the GEMMs in a HIP graph. Replays are interleaved with eager
+    work and synchronisations, and every replay is compared with the eager result."""
+    dev_ = torch.device("cuda:0")
+    A = dev(oracle.normal((64, 1536), 21, 0))
+    W = dev(oracle.uniform((1536, 4096), 21, 1, -1 / 32, 1 / 32))
+    bias = dev(oracle.uniform((4096,), 21, 2, -1 / 32, 1 / 32))
+    x = dev(oracle.uniform((1, 4096), 21, 3))
+    Bv = dev(oracle.uniform((4096, 11008), 21, 4))
+    say("graph capture: split-K gate GEMM + split GEMV")
+    y1 = torch.empty(64, 4096, device=dev_)
+    y2 = torch.empty(1, 11008, device=dev_)
+    eager1 = host(nncl.gemm(A, W, bias=bias)).copy()
+    eager2 = host(nncl.gemm(x, Bv)).copy()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        nncl.gemm(A, W, bias=bias, out=y1)
+        nncl.gemm(x, Bv, out=y2)
+    for i in range(3):
+        y1.fill_(float("nan"))
+        y2.fill_(float("nan"))
+        noise = nncl.gemm(Bv[:64, :4096].contiguous(), W[:4096 // 4].T.contiguous())  # eager work
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(y1), eager1), f"replay {i}: gate GEMM differs"
+        assert np.array_equal(host(y2), eager2), f"replay {i}: GEMV differs"
+        del noise
