@@ -68,94 +68,116 @@ struct TileFloats {
     static constexpr int value = KC ? T * (BK + PAD_K) : BK * (T + PAD_I);
 };
 
+// 16 contiguous bytes from a 4-byte aligned address: gfx950 global loads do not need
+// natural alignment (the target has unaligned-buffer-access), so this is one
+// global_load_dwordx4 whatever the row stride of the operand.
+__device__ __forceinline__ f4 load16(const float *p) {
+    f4 v;
+    __builtin_memcpy(&v, p, sizeof(v));
+    return v;
+}
+
 // One operand tile (T rows of the M or N dimension by BK of the K dimension).
 //  KC  : element (i, k) lives at base[i*ld + k] (K contiguous) else at base[k*ld + i].
-//  VEC : 128-bit global loads are legal (16-byte aligned base, ld % 4 == 0 and the
-//        contiguous extent % 4 == 0); otherwise four 32-bit loads per register.
+//  VEC : the contiguous extent (K for KC, else the M or N extent) is a multiple of 4, so
+//        every group of 4 contiguous elements is entirely inside or entirely outside the
+//        matrix and is fetched with one 128-bit load. Otherwise a KC operand still uses
+//        128-bit loads for full k-tiles and 32-bit loads only in the tail tile, and an
+//        I-contiguous operand fetches its 4 columns (clamped at the edge) one by one.
+// Per-thread source pointers are formed once per tile (rows beyond `rows` clamped), so a
+// k-step only adds a uniform offset. load<false> is the unpredicated main-loop fetch whose
+// registers are consumed only by store() after the MFMA work (the loads stay in flight
+// across it); load<true> zero-fills k >= K for the single tail tile.
 template <int T, int BK, int NT, bool KC, bool VEC>
 struct Operand {
     static_assert((T * BK) % (4 * NT) == 0, "operand tile does not split over the threads");
     static constexpr int NLOAD = T * BK / (4 * NT);
+    static constexpr int TPR = KC ? BK / 4 : T / 4;  // threads per LDS tile row
+    static constexpr int RPP = NT / TPR;             // LDS tile rows per pass
     f4 r[NLOAD];
+    const float *ptr[NLOAD];  // KC: start of global row i; else element (k = kr + p*RPP, i)
+    int coff[4];              // !KC && !VEC: clamped column offsets of the 4 elements
+    int c, rr;                // this thread's column (x4) and first tile row
 
-    // Fetch tile (i0.., k0..) into registers. `rows` is the extent along i (M or N).
-    // With `tail` set, k >= K is zero-filled; every address formed stays inside the
-    // operand's rows [0, rows) and columns [0, K) whether or not it is used.
-    __device__ __forceinline__ void load(const float *__restrict__ base, int64_t ld, int i0,
-                                         int rows, int k0, int K, bool tail, int tid) {
+    __device__ __forceinline__ void init(const float *__restrict__ base, int64_t ld, int i0,
+                                         int rows, int tid) {
+        c = (tid % TPR) * 4;
+        rr = tid / TPR;
         if constexpr (KC) {
-            constexpr int TPR = BK / 4;    // threads per tile row
-            constexpr int RPP = NT / TPR;  // tile rows per pass
-            const int c = (tid % TPR) * 4;
-            const int rr = tid / TPR;
-            const int gk = k0 + c;
 #pragma unroll
             for (int p = 0; p < NLOAD; ++p) {
                 int gi = i0 + rr + p * RPP;
                 gi = gi < rows ? gi : rows - 1;
-                const float *rowp = base + (int64_t)gi * ld;
-                if constexpr (VEC) {
-                    const bool ok = !tail || gk < K;
-                    f4 v = *reinterpret_cast<const f4 *>(rowp + (ok ? gk : 0));
+                ptr[p] = base + (int64_t)gi * ld;
+            }
+        } else {
+            int gi = i0 + c;
+            if constexpr (VEC) {
+                gi = gi < rows ? gi : rows - 4;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int g = i0 + c + e;
+                    coff[e] = (g < rows ? g : rows - 1) - i0 - c;
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < NLOAD; ++p) ptr[p] = base + (int64_t)(rr + p * RPP) * ld + gi;
+        }
+    }
+
+    template <bool TAIL>
+    __device__ __forceinline__ void load(int64_t ld, int k0, int K) {
+        if constexpr (KC) {
+            const int gk = k0 + c;
+#pragma unroll
+            for (int p = 0; p < NLOAD; ++p) {
+                if constexpr (!TAIL) {
+                    r[p] = load16(ptr[p] + gk);  // a full k-tile: gk + 3 < K
+                } else if constexpr (VEC) {
+                    const bool ok = gk < K;
+                    const f4 v = load16(ptr[p] + (ok ? gk : 0));
                     r[p] = ok ? v : f4{0.f, 0.f, 0.f, 0.f};
                 } else {
-                    f4 v;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const bool ok = !tail || gk + e < K;
-                        const float x = rowp[ok ? gk + e : 0];
-                        v[e] = ok ? x : 0.f;
+                        const bool ok = gk + e < K;
+                        const float x = ptr[p][ok ? gk + e : 0];
+                        r[p][e] = ok ? x : 0.f;
                     }
-                    r[p] = v;
                 }
             }
         } else {
-            constexpr int TPR = T / 4;
-            constexpr int RPP = NT / TPR;
-            const int c = (tid % TPR) * 4;
-            const int kr = tid / TPR;
+            const int64_t koff = (int64_t)k0 * ld;
 #pragma unroll
             for (int p = 0; p < NLOAD; ++p) {
-                const int gk = k0 + kr + p * RPP;
-                const bool ok = !tail || gk < K;
-                const float *rowp = base + (int64_t)(ok ? gk : 0) * ld;
-                if constexpr (VEC) {
-                    int gi = i0 + c;
-                    gi = gi < rows ? gi : rows - 4;
-                    f4 v = *reinterpret_cast<const f4 *>(rowp + gi);
-                    r[p] = ok ? v : f4{0.f, 0.f, 0.f, 0.f};
-                } else {
-                    f4 v;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        int gi = i0 + c + e;
-                        gi = gi < rows ? gi : rows - 1;
-                        const float x = rowp[gi];
-                        v[e] = ok ? x : 0.f;
-                    }
-                    r[p] = v;
+                const float *src = ptr[p] + koff;
+                bool ok = true;
+                if constexpr (TAIL) {
+                    ok = k0 + rr + p * RPP < K;
+                    // a k row past K is replaced by row 0 of the tile's source
+                    src = ok ? src : ptr[p] - (int64_t)(rr + p * RPP) * ld;
                 }
+                f4 v;
+                if constexpr (VEC) {
+                    v = load16(src);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = src[coff[e]];
+                }
+                if constexpr (TAIL) v = ok ? v : f4{0.f, 0.f, 0.f, 0.f};
+                r[p] = v;
             }
         }
     }
 
-    __device__ __forceinline__ void store(float *lds, int tid) const {
-        if constexpr (KC) {
-            constexpr int TPR = BK / 4;
-            constexpr int RPP = NT / TPR;
-            const int c = (tid % TPR) * 4;
-            const int rr = tid / TPR;
+    __device__ __forceinline__ void store(float *lds) const {
 #pragma unroll
-            for (int p = 0; p < NLOAD; ++p)
+        for (int p = 0; p < NLOAD; ++p) {
+            if constexpr (KC)
                 *reinterpret_cast<f4 *>(lds + (rr + p * RPP) * (BK + PAD_K) + c) = r[p];
-        } else {
-            constexpr int TPR = T / 4;
-            constexpr int RPP = NT / TPR;
-            const int c = (tid % TPR) * 4;
-            const int kr = tid / TPR;
-#pragma unroll
-            for (int p = 0; p < NLOAD; ++p)
-                *reinterpret_cast<f4 *>(lds + (kr + p * RPP) * (T + PAD_I) + c) = r[p];
+            else
+                *reinterpret_cast<f4 *>(lds + (rr + p * RPP) * (T + PAD_I) + c) = r[p];
         }
     }
 };
@@ -240,10 +262,17 @@ gemm_mfma_kernel(TiledArgs p) {
     const int kt0 = split * p.kt_per_split;
     const int kt1 = min((K + BK - 1) / BK, kt0 + p.kt_per_split);
 
-    opa.load(Ab, p.lda, m0, p.M, kt0 * BK, K, kt0 >= nfull, tid);
-    opb.load(Bb, p.ldb, n0, p.N, kt0 * BK, K, kt0 >= nfull, tid);
-    opa.store(smem, tid);
-    opb.store(smem + A_FL, tid);
+    opa.init(Ab, p.lda, m0, p.M, tid);
+    opb.init(Bb, p.ldb, n0, p.N, tid);
+    if (kt0 < nfull) {
+        opa.template load<false>(p.lda, kt0 * BK, K);
+        opb.template load<false>(p.ldb, kt0 * BK, K);
+    } else {
+        opa.template load<true>(p.lda, kt0 * BK, K);
+        opb.template load<true>(p.ldb, kt0 * BK, K);
+    }
+    opa.store(smem);
+    opb.store(smem + A_FL);
     __syncthreads();
 
     for (int kt = kt0; kt < kt1; ++kt) {
@@ -251,9 +280,13 @@ gemm_mfma_kernel(TiledArgs p) {
         float *nxt = smem + ((kt - kt0 + 1) & 1) * STAGE;
         const bool more = kt + 1 < kt1;
         if (more) {
-            const bool tail = kt + 1 >= nfull;
-            opa.load(Ab, p.lda, m0, p.M, (kt + 1) * BK, K, tail, tid);
-            opb.load(Bb, p.ldb, n0, p.N, (kt + 1) * BK, K, tail, tid);
+            if (kt + 1 < nfull) {
+                opa.template load<false>(p.lda, (kt + 1) * BK, K);
+                opb.template load<false>(p.ldb, (kt + 1) * BK, K);
+            } else {
+                opa.template load<true>(p.lda, (kt + 1) * BK, K);
+                opb.template load<true>(p.ldb, (kt + 1) * BK, K);
+            }
         }
 #pragma unroll
         for (int g = 0; g < BK / 8; ++g) {
@@ -271,8 +304,8 @@ gemm_mfma_kernel(TiledArgs p) {
                                                                          acc[i][j], 0, 0, 0);
         }
         if (more) {
-            opa.store(nxt, tid);
-            opb.store(nxt + A_FL, tid);
+            opa.store(nxt);
+            opb.store(nxt + A_FL);
         }
         __syncthreads();
     }
@@ -318,21 +351,36 @@ gemm_mfma_kernel(TiledArgs p) {
     }
 }
 
-// C_b[m, n] = partial[0][b][m][n] + ... + partial[S-1][b][m][n] (+ bias[n]), in order.
+// C_b[m, n] = partial[0][b][m][n] + ... + partial[S-1][b][m][n] (+ bias[n]), added in
+// slice order. One output per thread; the partials are read RS_GROUP slices at a time
+// with every load of a group issued before the group is summed (a serial load-add chain
+// would pay one full memory latency per slice).
+constexpr int RS_GROUP = 16;
+
 __global__ void __launch_bounds__(256)
 reduce_slices_kernel(const float *__restrict__ partial, int slices, int batch, int M, int N,
                      const float *__restrict__ bias, float *__restrict__ C, int64_t ldc,
                      int64_t strideC) {
     const int64_t total = (int64_t)batch * M * N;
-    const int64_t plane = total;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
     for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += step) {
-        const int64_t bm = t / N;
-        const int n = (int)(t - bm * N);
-        const int64_t b = bm / M;
-        const int m = (int)(bm - b * M);
-        float v = partial[t];
-        for (int s = 1; s < slices; ++s) v += partial[t + (int64_t)s * plane];
+        const float *src = partial + t;
+        float v = 0.f;
+        for (int s0 = 0; s0 < slices; s0 += RS_GROUP) {
+            float x[RS_GROUP];
+#pragma unroll
+            for (int g = 0; g < RS_GROUP; ++g) {
+                const int sl = s0 + g < slices ? s0 + g : slices - 1;
+                x[g] = src[(int64_t)sl * total];
+            }
+#pragma unroll
+            for (int g = 0; g < RS_GROUP; ++g)
+                if (s0 + g < slices) v = (s0 + g == 0) ? x[g] : v + x[g];
+        }
+        const int64_t row = t / N;
+        const int n = (int)(t - row * N);
+        const int64_t b = row / M;
+        const int m = (int)(row - b * M);
         if (bias != nullptr) v = v + bias[n];
         C[b * strideC + (int64_t)m * ldc + n] = v;
     }
@@ -372,7 +420,24 @@ int launch_layout(hipStream_t s, const TiledArgs &a, bool akc, bool bkc, bool av
     return launch_vec<BM, BN, BK, WM, WN, false, false>(s, a, av, bv);
 }
 
-bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+// Sets the tile grid for a BM x BN tile and the split-K ranges (a.splits requested on
+// entry; on return the number of non-empty ranges, each of kt_per_split BK-wide k-tiles),
+// then launches.
+template <int BM, int BN, int BK, int WM, int WN>
+int launch_tiles(hipStream_t s, TiledArgs &a, bool akc, bool bkc, bool av, bool bv) {
+    a.tiles_m = (a.M + BM - 1) / BM;
+    a.tiles_n = (a.N + BN - 1) / BN;
+    const int nk = (a.K + BK - 1) / BK;
+    const int want = a.splits < nk ? a.splits : nk;
+    a.kt_per_split = (nk + want - 1) / want;
+    a.splits = (nk + a.kt_per_split - 1) / a.kt_per_split;
+    const int64_t total = (int64_t)a.tiles_m * a.tiles_n * a.batch * a.splits;
+    if (total > INT32_MAX)
+        return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm: %lld tiles exceed one launch",
+                         (long long)total);
+    a.total = (int)total;
+    return launch_layout<BM, BN, BK, WM, WN>(s, a, akc, bkc, av, bv);
+}
 
 }  // namespace
 
@@ -381,7 +446,7 @@ int launch_reduce_slices(hipStream_t stream, const float *partial, int slices, i
                          int64_t strideC) {
     const int64_t total = (int64_t)batch * M * N;
     int64_t blocks = (total + 255) / 256;
-    if (blocks > 8192) blocks = 8192;
+    if (blocks > 16384) blocks = 16384;
     hipLaunchKernelGGL(reduce_slices_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
                        partial, slices, batch, M, N, bias, C, ldc, strideC);
     return hip_check(hipGetLastError(), "reduce_slices_kernel launch");
@@ -400,13 +465,10 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     // when transposed.
     const bool akc = !d.transA;
     const bool bkc = d.transB;
-    // 128-bit loads need a 16-byte aligned start for every batch entry, a leading
-    // dimension that keeps rows 16-byte aligned and a contiguous extent that is a
-    // multiple of 4 (so a float4 is entirely inside or entirely outside the matrix).
-    const bool av = aligned16(d.A) && d.lda % 4 == 0 && (d.batch == 1 || d.sA % 4 == 0) &&
-                    (akc ? d.K % 4 == 0 : d.M % 4 == 0);
-    const bool bv = aligned16(d.B) && d.ldb % 4 == 0 && (d.batch == 1 || d.sB % 4 == 0) &&
-                    (bkc ? d.K % 4 == 0 : d.N % 4 == 0);
+    // Groups of 4 contiguous elements never straddle the matrix edge when the
+    // contiguous extent is a multiple of 4 (alignment does not matter, see load16).
+    const bool av = akc ? d.K % 4 == 0 : d.M % 4 == 0;
+    const bool bv = bkc ? d.K % 4 == 0 : d.N % 4 == 0;
 
     TiledArgs a;
     a.A = d.A;
@@ -444,13 +506,10 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     }
     static const int force_tile = env_int("MIGEMM_TILE");
     static const int force_split = env_int("MIGEMM_SPLITK");
+    static const int variant = env_int("MIGEMM_VARIANT");
     if (force_tile == 32 || force_tile == 64 || force_tile == 128) cfg = force_tile;
-    if (force_split >= 1) splits = force_split < nk32 ? force_split : nk32;
+    if (force_split >= 1) splits = force_split;
 
-    a.tiles_m = (d.M + cfg - 1) / cfg;
-    a.tiles_n = (d.N + cfg - 1) / cfg;
-    a.kt_per_split = (nk32 + splits - 1) / splits;
-    splits = (nk32 + a.kt_per_split - 1) / a.kt_per_split;  // no empty range
     a.splits = splits;
     a.partial = nullptr;
     if (splits > 1) {
@@ -459,17 +518,27 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
             workspace((size_t)splits * d.batch * d.M * d.N * sizeof(float), &st));
         if (a.partial == nullptr) return st;
     }
-    const int64_t total = tiles(cfg, cfg) * splits;
-    if (total > INT32_MAX)
-        return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm: %lld tiles exceed one launch",
-                         (long long)total);
-    a.total = (int)total;
     int rc;
-    switch (cfg) {
-        case 128: rc = launch_layout<128, 128, 32, 2, 2>(stream, a, akc, bkc, av, bv); break;
-        case 64: rc = launch_layout<64, 64, 32, 2, 2>(stream, a, akc, bkc, av, bv); break;
-        default: rc = launch_layout<32, 32, 32, 1, 1>(stream, a, akc, bkc, av, bv); break;
+    if (variant != 0 && cfg == 128 && av && bv) {
+        // Tile-shape variants for tuning sweeps (MIGEMM_VARIANT); 128-bit loads only.
+        switch (variant) {
+            case 1: rc = launch_tiles<256, 128, 32, 4, 2>(stream, a, akc, bkc, true, true); break;
+            case 2: rc = launch_tiles<128, 256, 32, 2, 4>(stream, a, akc, bkc, true, true); break;
+            case 3: rc = launch_tiles<128, 128, 32, 2, 2>(stream, a, akc, bkc, true, true); break;
+            case 4: rc = launch_tiles<256, 128, 16, 4, 2>(stream, a, akc, bkc, true, true); break;
+            case 5: rc = launch_tiles<128, 256, 16, 2, 4>(stream, a, akc, bkc, true, true); break;
+            case 6: rc = launch_tiles<128, 128, 8, 2, 2>(stream, a, akc, bkc, true, true); break;
+            case 7: rc = launch_tiles<128, 128, 16, 4, 1>(stream, a, akc, bkc, true, true); break;
+            default: rc = launch_tiles<128, 128, 16, 2, 2>(stream, a, akc, bkc, av, bv); break;
+        }
+    } else {
+        switch (cfg) {
+            case 128: rc = launch_tiles<128, 128, 16, 2, 2>(stream, a, akc, bkc, av, bv); break;
+            case 64: rc = launch_tiles<64, 64, 32, 2, 2>(stream, a, akc, bkc, av, bv); break;
+            default: rc = launch_tiles<32, 32, 32, 1, 1>(stream, a, akc, bkc, av, bv); break;
+        }
     }
+    splits = a.splits;
     if (rc != MIGEMM_OK || splits == 1) return rc;
     return launch_reduce_slices(stream, a.partial, splits, d.batch, d.M, d.N, d.bias, d.C,
                                 d.ldc, d.sC);

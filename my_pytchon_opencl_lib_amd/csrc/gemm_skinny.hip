@@ -3,14 +3,17 @@
 // is therefore bound by HBM bandwidth (0.5 FLOP/byte at M = 1), not by the matrix cores.
 //
 // Work split: a work-group of 4 wavefronts owns 256 consecutive columns (one float4 of
-// B per lane) and a slice of KC rows of K; wavefront w accumulates rows w, w+4, ... of
-// its slice with fp32 FMA chains and the 4 wavefronts are combined through LDS. With
+// B per lane) and a slice of KC rows of K; wavefront w accumulates the w-th quarter of
+// the slice with fp32 FMA chains, 16 rows of loads in flight at a time, and the 4
+// wavefronts are combined through LDS. With
 // S = ceil(K / KC) > 1 slices, each slice writes its partial sums to the library
 // workspace and a second kernel (reduce_slices_kernel, gemm_mfma.hip) adds the S partials
 // of every output in slice order, then the bias. The result is deterministic: the
 // association order depends only on (K, KC), never on timing. (A single-kernel
 // "last work-group combines" variant needs an agent-scope release fence per work-group,
 // which writes back the XCD's whole L2 on MI355X and cost more than the GEMV itself.)
+#include <stdlib.h>
+
 #include "migemm_internal.h"
 
 namespace migemm {
@@ -21,6 +24,7 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 constexpr int SK_THREADS = 256;
 constexpr int SK_COLS = 256;  // columns per work-group (64 lanes x float4)
 constexpr int SK_MAXM = 4;
+constexpr int SK_UNROLL = 16;  // rows of B in flight per wavefront
 
 struct SkinnyArgs {
     const float *A;
@@ -52,52 +56,48 @@ __global__ void __launch_bounds__(SK_THREADS) gemm_skinny_kernel(SkinnyArgs p) {
 
     const float *Ab = p.A + (int64_t)b * p.sA;
     const float *Bb = p.B + (int64_t)b * p.sB;
+    // Wavefront w owns the contiguous rows [k_lo, k_hi) of this work-group's slice.
     const int kb = s * p.kc;
     const int ke = min(p.K, kb + p.kc);
+    const int per_wave = p.kc / 4;
+    const int k_lo = min(ke, kb + w * per_wave);
+    const int k_hi = min(ke, k_lo + per_wave);
+
+    // Columns beyond N read a clamped, in-bounds column; their sums are never stored.
+    const float *colp = Bb + (VEC ? (n < p.N ? n : p.N - 4) : 0);
+    int nc[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) nc[e] = min(n + e, p.N - 1);
 
     f4 acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = f4{0.f, 0.f, 0.f, 0.f};
 
-    // Columns beyond N read a clamped, in-bounds column; their sums are never stored.
-    int nc[4];
+    // Batches of SK_UNROLL rows: every load of a batch is issued before its FMAs, so each
+    // wavefront keeps SK_UNROLL x 1 KiB of B in flight.
+    for (int k0 = k_lo; k0 < k_hi; k0 += SK_UNROLL) {
+        f4 v[SK_UNROLL];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) nc[e] = min(n + e, p.N - 1);
-
-    auto row_of_b = [&](int k) -> f4 {
-        const float *rowp = Bb + (int64_t)k * p.ldb;
-        if constexpr (VEC) {
-            return *reinterpret_cast<const f4 *>(rowp + (n < p.N ? n : p.N - 4));
-        } else {
-            return f4{rowp[nc[0]], rowp[nc[1]], rowp[nc[2]], rowp[nc[3]]};
+        for (int u = 0; u < SK_UNROLL; ++u) {
+            const int k = min(k0 + u, k_hi - 1);
+            const float *rowp = colp + (int64_t)k * p.ldb;
+            if constexpr (VEC)
+                __builtin_memcpy(&v[u], rowp, sizeof(f4));
+            else
+                v[u] = f4{rowp[nc[0]], rowp[nc[1]], rowp[nc[2]], rowp[nc[3]]};
         }
-    };
-
-    int k = kb + w;
-    // 4 rows in flight per wavefront per iteration.
-    for (; k + 12 < ke; k += 16) {
-        f4 v0 = row_of_b(k), v1 = row_of_b(k + 4), v2 = row_of_b(k + 8), v3 = row_of_b(k + 12);
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             const float *ap = Ab + m * p.a_rs;
-            const float a0 = ap[(int64_t)k * p.a_ks], a1 = ap[(int64_t)(k + 4) * p.a_ks];
-            const float a2 = ap[(int64_t)(k + 8) * p.a_ks], a3 = ap[(int64_t)(k + 12) * p.a_ks];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                acc[m][e] = __builtin_fmaf(a0, v0[e], acc[m][e]);
-                acc[m][e] = __builtin_fmaf(a1, v1[e], acc[m][e]);
-                acc[m][e] = __builtin_fmaf(a2, v2[e], acc[m][e]);
-                acc[m][e] = __builtin_fmaf(a3, v3[e], acc[m][e]);
+            for (int u = 0; u < SK_UNROLL; ++u) {
+                const bool ok = k0 + u < k_hi;
+                const int k = ok ? k0 + u : k_lo;
+                const float a = ok ? ap[(int64_t)k * p.a_ks] : 0.f;
+                const f4 vv = ok ? v[u] : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[m][e] = __builtin_fmaf(a, vv[e], acc[m][e]);
             }
-        }
-    }
-    for (; k < ke; k += 4) {
-        f4 v = row_of_b(k);
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            const float a = Ab[m * p.a_rs + (int64_t)k * p.a_ks];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[m][e] = __builtin_fmaf(a, v[e], acc[m][e]);
         }
     }
 
@@ -173,19 +173,22 @@ int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {
     a.K = d.K;
     a.cblocks = (d.N + SK_COLS - 1) / SK_COLS;
 
-    // Aim for >= ~2048 work-groups so every CU holds several and HBM sees enough
-    // requests in flight; slices are at least 64 rows so the final combine stays small.
-    const int64_t want = 2048;
-    int64_t slices = (want + (int64_t)a.cblocks * d.batch - 1) / ((int64_t)a.cblocks * d.batch);
-    int kc = (int)((d.K + slices - 1) / slices);
-    kc = (kc + 15) / 16 * 16;
-    if (kc < 64) kc = 64;
-    if (kc > d.K) kc = (d.K + 3) / 4 * 4;
+    // Slices of KC = 4 wavefronts x 32 rows (two batches of 16 per wavefront) give the
+    // 5b shape (11008 x 4096) 43 x 32 = 1376 work-groups, all resident at once, each
+    // wavefront streaming 32 KiB of B; small K gets one slice.
+    int kc = 128;
+    const int64_t blocks = (int64_t)a.cblocks * d.batch;
+    if (blocks >= 1024) kc = 512;  // enough column blocks already: fewer partials
+    static const int force_kc = [] {
+        const char *v = getenv("MIGEMM_GEMV_KC");
+        return v != nullptr ? atoi(v) : 0;
+    }();
+    if (force_kc >= 4) kc = force_kc / 4 * 4;
+    if (kc >= d.K) kc = (d.K + 3) / 4 * 4;
     a.kc = kc;
     a.slices = (d.K + kc - 1) / kc;
     if (a.slices > 65535) {
-        a.kc = (d.K + 65534) / 65535;
-        a.kc = (a.kc + 3) / 4 * 4;
+        a.kc = ((d.K + 65534) / 65535 + 3) / 4 * 4;
         a.slices = (d.K + a.kc - 1) / a.kc;
     }
     a.partial = nullptr;
@@ -196,8 +199,9 @@ int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {
         a.partial = static_cast<float *>(workspace(part_bytes, &st));
         if (a.partial == nullptr) return st;
     }
-    const bool vec = (reinterpret_cast<uintptr_t>(d.B) & 15u) == 0 && d.ldb % 4 == 0 &&
-                     d.N % 4 == 0 && (d.batch == 1 || d.sB % 4 == 0);
+    // 4-column groups never straddle N when N % 4 == 0 (16-byte loads need only 4-byte
+    // alignment on gfx950).
+    const bool vec = d.N % 4 == 0;
     int rc;
     switch (d.M) {
         case 1: rc = launch_mr<1>(stream, a, vec, d.batch); break;

@@ -281,3 +281,30 @@ def test_graph_capture_replays_match_eager(nncl):
         assert np.array_equal(host(y1), eager1), f"replay {i}: gate GEMM differs"
         assert np.array_equal(host(y2), eager2), f"replay {i}: GEMV differs"
         del noise
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_unaligned_bases_and_leading_dims(nncl, ta, tb):
+    """Operands that start 4 bytes past a 16-byte boundary with leading dimensions that
+    are not multiples of 4 (128-bit loads from dword-aligned addresses)."""
+    import ctypes
+    from my_pytchon_opencl_lib_amd import _native
+    M, K, N = 260, 300, 196
+    A = small_ints((K, M) if ta else (M, K), 31)
+    B = small_ints((N, K) if tb else (K, N), 32)
+    lda, ldb = A.shape[1] + 1, B.shape[1] + 3
+    abuf = np.zeros(1 + A.shape[0] * lda, np.float32)
+    bbuf = np.zeros(3 + B.shape[0] * ldb, np.float32)
+    abuf[1:].reshape(A.shape[0], lda)[:, :A.shape[1]] = A
+    bbuf[3:].reshape(B.shape[0], ldb)[:, :B.shape[1]] = B
+    a, b = dev(abuf), dev(bbuf)
+    c = torch.full((M, N), float("nan"), device="cuda:0")
+    say("unaligned", ta, tb)
+    _native.call("migemm_gemm_strided_batched",
+                 ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), ta, tb, M, N, K,
+                 ctypes.c_void_p(a.data_ptr() + 4), lda, 0, ctypes.c_void_p(b.data_ptr() + 12),
+                 ldb, 0, None, ctypes.c_void_p(c.data_ptr()), N, 0, 1)
+    Aop = A.T if ta else A
+    Bop = B.T if tb else B
+    expect = (Aop.astype(np.int64) @ Bop.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(host(c), expect)
