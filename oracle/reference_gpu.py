@@ -1,0 +1,68 @@
+"""Runs the reference's own OpenCL kernels on the GPU -- TEST INFRASTRUCTURE ONLY.
+
+oracle/_ref/ holds the reference kernel sources compiled for gfx950 (oracle/Makefile, target
+`ref`, built from /root/reference when it is mounted) and ref_runner, this repository's
+OpenCL host for them (oracle/ref_runner.c). Each call runs one kernel in a child process
+through the ROCm OpenCL runtime with the reference hosts' launch geometry and returns its
+output buffer, so the oracle's restatement can be compared bit-for-bit with the reference
+arithmetic as the GPU's OpenCL compiler emits it.
+"""
+import json
+import os
+import subprocess
+import tempfile
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REF_DIR = os.path.join(HERE, "_ref")
+RUNNER = os.path.join(REF_DIR, "ref_runner")
+
+CODE_OBJECT = {
+    "matmul_tiled": "matmul.co",
+    "bmm_tiled": "matmul.co",
+    "bmm_permute_tiled": "bmm_permute_tiled.co",
+    "linear_forward_tiled": "linear.co",
+    "tensor_permute": "permute.co",
+}
+
+
+class Unavailable(RuntimeError):
+    """The reference kernels cannot run here (not built, or no OpenCL GPU device)."""
+
+
+def available():
+    return os.path.exists(RUNNER) and all(
+        os.path.exists(os.path.join(REF_DIR, f)) for f in set(CODE_OBJECT.values()))
+
+
+def run(kernel, A, B=None, bias=None, M=0, K=0, N=0, batch=1, sA=0, sB=0, sC=0, transA=0,
+        transB=0, reps=3, out_elems=None):
+    """Run one reference kernel; returns (flat float32 output, info dict)."""
+    if not available():
+        raise Unavailable("oracle/_ref is not built (needs the reference sources at build time)")
+    with tempfile.TemporaryDirectory() as td:
+        def dump(name, arr, dtype=np.float32):
+            if arr is None:
+                return "-"
+            path = os.path.join(td, name)
+            np.ascontiguousarray(arr, dtype=dtype).tofile(path)
+            return path
+
+        a = dump("a.bin", A)
+        b = dump("b.bin", B, np.int32 if kernel == "tensor_permute" else np.float32)
+        bi = dump("bias.bin", bias)
+        out = os.path.join(td, "out.bin")
+        cmd = [RUNNER, os.path.join(REF_DIR, CODE_OBJECT[kernel]), kernel, str(M), str(K),
+               str(N), str(batch), str(sA), str(sB), str(sC), str(int(transA)),
+               str(int(transB)), a, b, bi, out, str(reps)]
+        p = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+        if p.returncode == 3:
+            raise Unavailable(p.stderr.strip())
+        if p.returncode != 0:
+            raise RuntimeError(f"ref_runner failed ({p.returncode}): {p.stderr.strip()}")
+        info = json.loads(p.stdout.strip().splitlines()[-1])
+        res = np.fromfile(out, dtype=np.float32)
+    if out_elems is not None:
+        res = res[:out_elems]
+    return res, info

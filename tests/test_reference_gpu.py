@@ -1,0 +1,145 @@
+"""The reference's own OpenCL kernels, run on the GPU, against the oracle and the HIP path.
+
+oracle/_ref holds cl_kernels/matmul.cl, cl_kernels/permute.cl and the C# tree's
+bmm_permute_tiled.cl / linear.cl compiled for gfx950 (oracle/Makefile target `ref`), run by
+oracle/ref_runner.c through the ROCm OpenCL runtime with the reference hosts' launch
+geometry. Two claims are checked on identical seeded inputs:
+  1. the oracle's C restatement reproduces the reference kernels bit-for-bit (this pins the
+     restatement's fp32 fma-chain arithmetic against the reference itself);
+  2. the HIP path is within 1e-5*sqrt(K) (relative, componentwise |A||B|) of the
+     reference's output, and of fp64.
+Skipped (with the reason) when oracle/_ref was not built or no OpenCL GPU device exists.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from oracle import reference_gpu as ref
+from parity import check_gemm, dev, host, sample_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def run_ref(*args, **kw):
+    try:
+        return ref.run(*args, **kw)
+    except ref.Unavailable as e:
+        pytest.skip(f"reference OpenCL kernels unavailable: {e}")
+
+
+def ulp_report(a, b):
+    ai = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    bi = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    return int(np.max(np.abs(ai - bi))) if ai.size else 0
+
+
+def rel_distance(C, R, absprod):
+    d = np.abs(np.asarray(C, np.float64) - np.asarray(R, np.float64))
+    with np.errstate(divide="ignore", invalid="ignore"):
+        return float(np.max(np.where(absprod > 0, d / absprod, np.where(d > 0, np.inf, 0.0))))
+
+
+@pytest.mark.parametrize("M,K,N,seed", [(256, 256, 256, 0), (64, 128, 96, 10), (65, 129, 31, 6),
+                                        (17, 33, 5, 7)])
+def test_matmul_tiled_reference(nncl, M, K, N, seed):
+    A = oracle.uniform((M, K), seed, 0)
+    B = oracle.uniform((K, N), seed, 1)
+    say("reference matmul_tiled", M, K, N)
+    R, info = run_ref("matmul_tiled", A, B, M=M, K=K, N=N)
+    R = R.reshape(M, N)
+    say(info)
+    ours = oracle.matmul_tiled(A, B)
+    assert np.array_equal(ours, R), f"restatement differs by {ulp_report(ours, R)} ulp"
+    C = host(nncl.gemm(dev(A), dev(B)))
+    ap = oracle.gemm_absprod(A, B, 0, 0, None, M=M, N=N, K=K, lda=K, ldb=N)[0]
+    assert rel_distance(C, R, ap) <= oracle.tolerance(K)
+    check_gemm(C, A, B, 0, 0, M=M, N=N, K=K, lda=K, ldb=N)
+
+
+@pytest.mark.parametrize("batch,M,K,N,bcast", [(4, 32, 64, 48, False), (3, 40, 24, 36, True),
+                                               (32, 128, 64, 128, False)])
+def test_bmm_tiled_reference(nncl, batch, M, K, N, bcast):
+    A = oracle.normal((batch, M, K), 777, 0)
+    B = oracle.normal((1 if bcast else batch, K, N), 777, 1)
+    sB = 0 if bcast else K * N
+    say("reference bmm_tiled", batch, M, K, N, "broadcast" if bcast else "")
+    R, info = run_ref("bmm_tiled", A, B, M=M, K=K, N=N, batch=batch, sA=M * K, sB=sB, sC=M * N)
+    R = R.reshape(batch, M, N)
+    say(info)
+    ours = oracle.bmm(A, B)
+    assert np.array_equal(ours, R), f"restatement differs by {ulp_report(ours, R)} ulp"
+    C = host(nncl.Bmm(dev(A), dev(B)))
+    ap = oracle.gemm_absprod(A, B, 0, 0, None, M=M, N=N, K=K, lda=K, ldb=N, sA=M * K, sB=sB,
+                             batch=batch)
+    assert rel_distance(C, R, ap) <= oracle.tolerance(K)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_bmm_permute_tiled_reference(nncl, ta, tb):
+    batch, M, K, N = 4, 32, 64, 48
+    A = oracle.normal((batch, K, M) if ta else (batch, M, K), 778, 0)
+    B = oracle.normal((batch, N, K) if tb else (batch, K, N), 778, 1)
+    say("reference bmm_permute_tiled", ta, tb)
+    R, info = run_ref("bmm_permute_tiled", A, B, M=M, K=K, N=N, batch=batch, sA=M * K,
+                      sB=K * N, sC=M * N, transA=ta, transB=tb)
+    R = R.reshape(batch, M, N)
+    say(info)
+    ours = oracle.bmm_permute(A, B, transA=bool(ta), transB=bool(tb))
+    assert np.array_equal(ours, R), f"restatement differs by {ulp_report(ours, R)} ulp"
+    C = host(nncl.BmmPermute(dev(A), dev(B), transA=bool(ta), transB=bool(tb)))
+    ap = oracle.gemm_absprod(A, B, ta, tb, None, M=M, N=N, K=K, lda=M if ta else K,
+                             ldb=K if tb else N, sA=M * K, sB=K * N, batch=batch)
+    assert rel_distance(C, R, ap) <= oracle.tolerance(K)
+
+
+@pytest.mark.parametrize("batch,M,K,N", [(2, 33, 40, 70), (1, 64, 1536, 4096)])
+def test_linear_forward_tiled_reference(nncl, batch, M, K, N):
+    X = oracle.normal((batch, M, K), 2, 0)
+    W = oracle.uniform((K, N), 2, 1, -1 / 32, 1 / 32)
+    bias = oracle.uniform((N,), 2, 2, -1 / 32, 1 / 32)
+    say("reference linear_forward_tiled", batch, M, K, N)
+    R, info = run_ref("linear_forward_tiled", X, W, bias, M=M, K=K, N=N, batch=batch,
+                      sA=M * K, sC=M * N)
+    R = R.reshape(batch, M, N)
+    say(info)
+    ours = oracle.linear_forward(X, W, bias)
+    assert np.array_equal(ours, R), f"restatement differs by {ulp_report(ours, R)} ulp"
+    C = host(nncl.LinearForward(dev(X), dev(W[None]), dev(bias)))
+    ap = oracle.gemm_absprod(X, W, 0, 0, bias, M=M, N=N, K=K, lda=K, ldb=N, sA=M * K, sB=0,
+                             batch=batch)
+    assert rel_distance(C, R, ap) <= oracle.tolerance(K)
+
+
+def test_tensor_permute_reference(nncl):
+    rng = np.random.default_rng(3)
+    for shape, axes in [((4, 32, 48), [0, 2, 1]), ((3, 5), [1, 0]),
+                        ((2, 3, 4, 5, 6), [3, 0, 4, 2, 1])]:
+        x = rng.standard_normal(shape).astype(np.float32)
+        meta = np.array(list(shape) + list(axes), dtype=np.int32)
+        say("reference tensor_permute", shape, axes)
+        R, _ = run_ref("tensor_permute", x, meta, M=len(shape))
+        assert np.array_equal(oracle.tensor_permute(x, axes).ravel(), R)
+        assert np.array_equal(host(nncl.Permute(dev(x), axes)).ravel(), R)
+
+
+def test_config4_nn_4096_reference(nncl):
+    """BASELINE config 4 forward through the reference bmm_tiled on the GPU: the oracle's
+    restatement matches it bit-for-bit on sampled rows, the HIP path within tolerance."""
+    n = 4096
+    A = oracle.normal((n, n), 3, 0, 0.0, 1.0 / 64)
+    B = oracle.normal((n, n), 3, 1, 0.0, 1.0 / 64)
+    say("reference bmm_tiled 4096^3")
+    R, info = run_ref("bmm_tiled", A, B, M=n, K=n, N=n, batch=1, sA=n * n, sB=0, sC=n * n,
+                      reps=2)
+    R = R.reshape(n, n)
+    say(info)
+    rows = sample_rows(n, 12)
+    for r in rows:
+        ours = oracle.matmul_rows(A, B, r, r + 1, threads=8)[0]
+        assert np.array_equal(ours, R[r]), f"row {r}: restatement differs"
+    C = host(nncl.gemm(dev(A), dev(B)))
+    check_gemm(C, A, B, 0, 0, M=n, N=n, K=n, lda=n, ldb=n, rows=rows, ref=R)
