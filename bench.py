@@ -37,6 +37,10 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="target duration of the bounded CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--pmc-target", action="store_true",
+                   help="run only the profiling target for rocprofv3 --pmc passes: the three "
+                        "4096^3 forms 3x each, then a 256 MiB device copy 3x (the reference "
+                        "for scaling FETCH_SIZE / WRITE_SIZE to bytes)")
     return p.parse_args()
 
 
@@ -108,6 +112,9 @@ def main():
     import torch
     from my_pytchon_opencl_lib_amd import NnClGlob, _native
 
+    if args.pmc_target:
+        pmc_target(torch, NnClGlob("cuda:0"))
+        return
     nncl = NnClGlob("cuda:0")
     dev = torch.device("cuda:0")
     n = 4096
@@ -181,10 +188,44 @@ def main():
         "roofline": {"bound": "mfma", "kernel": f"gemm_mfma_kernel ({dominant} form)",
                      "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": load_traffic(dominant)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def pmc_target(torch, nncl):
+    n = 4096
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(3)
+    A = torch.randn(n, n, device="cuda:0", generator=g) / 64
+    B = torch.randn(n, n, device="cuda:0", generator=g) / 64
+    C = torch.empty(n, n, device="cuda:0")
+    for _ in range(3):
+        nncl.gemm(A, B, out=C)
+        nncl.gemm(A, B, transB=True, out=C)
+        nncl.gemm(A, B, transA=True, out=C)
+    src = torch.ones(64 * 1024 * 1024, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("pmc target done", flush=True)
+
+
+def load_traffic(kernel_substr):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, each
+    scaled by the copy-kernel factor) for the dominant kernel, from the committed profile
+    summary; None when no summary covers that kernel."""
+    path = os.path.join(ROOT, "profiles", "gemm_mfma_4096_pmc.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("TRAFFIC_BYTES_PER_LAUNCH"):
+            _, form, nbytes = line.split()[:3]
+            if form == kernel_substr:
+                return int(nbytes)
+    return None
 
 
 def measure_all_configs(torch, nncl, _native, reps=20):

@@ -98,6 +98,12 @@ def load():
                     f"libmigemm.so not found at {LIB_PATH}: build it first "
                     "(python -c 'import __graft_entry__ as g; g.build()' or "
                     "python my_pytchon_opencl_lib_amd/build_native.py)")
+            # torch ships its own libamdhip64.so.7 (same soname as /opt/rocm's). Loading
+            # torch first makes the dynamic linker bind libmigemm.so to that runtime, so the
+            # process holds one HIP runtime and tensors from torch are valid here. Loaded
+            # first, libmigemm.so would pull in /opt/rocm's copy and torch would then load a
+            # second runtime beside it.
+            import torch  # noqa: F401
             L = ctypes.CDLL(LIB_PATH)
             for name, (args, res) in SIGNATURES.items():
                 fn = getattr(L, name)

@@ -60,8 +60,20 @@ struct TiledArgs {
     float *partial;        // [splits][batch][M][N] partial sums when splits > 1
 };
 
-constexpr int PAD_K = 4;  // pad of a K-contiguous LDS tile row  [i][BK + 4]
+constexpr int PAD_K = 4;  // pad of a K-contiguous LDS tile row [i][BK + 4]
 constexpr int PAD_I = 8;  // pad of an I-contiguous LDS tile row [k][T + 8]
+
+// LDS layout of a K-contiguous tile: rows of BK floats padded to BK + 4 (row strides of 20
+// and 36 floats). Measured on gfx950 with SQ_LDS_BANK_CONFLICT for 64-lane 128-bit
+// accesses: the MFMA fragment reads (32 consecutive rows x 2 chunks) are conflict-free at
+// both strides, and so are writes whose lanes cover 8 rows x 8 chunks (BK = 32) or 16
+// rows x 4 chunks (BK = 16). Writes covering 16 rows as 4 consecutive lanes per row
+// conflict (8 extra cycles per instruction at stride 20), which is why Operand lays its
+// BK = 16 lanes out row-fastest.
+template <int BK>
+__device__ __forceinline__ int kc_off(int row, int chunk) {
+    return row * (BK + PAD_K) + 4 * chunk;
+}
 
 template <int T, int BK, bool KC>
 struct TileFloats {
@@ -85,24 +97,32 @@ __device__ __forceinline__ f4 load16(const float *p) {
 //        128-bit loads for full k-tiles and 32-bit loads only in the tail tile, and an
 //        I-contiguous operand fetches its 4 columns (clamped at the edge) one by one.
 // Per-thread source pointers are formed once per tile (rows beyond `rows` clamped), so a
-// k-step only adds a uniform offset. load<false> is the unpredicated main-loop fetch whose
-// registers are consumed only by store() after the MFMA work (the loads stay in flight
-// across it); load<true> zero-fills k >= K for the single tail tile.
+// k-step only adds a uniform offset. load<false> is the unpredicated main-loop fetch;
+// load<true> zero-fills k >= K for the single tail tile. The fetched registers are
+// written to LDS one k-tile later (see the main loop), so loads stay in flight across a
+// whole k-tile of MFMA work.
 template <int T, int BK, int NT, bool KC, bool VEC>
 struct Operand {
     static_assert((T * BK) % (4 * NT) == 0, "operand tile does not split over the threads");
     static constexpr int NLOAD = T * BK / (4 * NT);
     static constexpr int TPR = KC ? BK / 4 : T / 4;  // threads per LDS tile row
     static constexpr int RPP = NT / TPR;             // LDS tile rows per pass
-    f4 r[NLOAD];
+    typedef f4 Regs[NLOAD];                          // one k-tile in flight
     const float *ptr[NLOAD];  // KC: start of global row i; else element (k = kr + p*RPP, i)
     int coff[4];              // !KC && !VEC: clamped column offsets of the 4 elements
     int c, rr;                // this thread's column (x4) and first tile row
 
     __device__ __forceinline__ void init(const float *__restrict__ base, int64_t ld, int i0,
                                          int rows, int tid) {
-        c = (tid % TPR) * 4;
-        rr = tid / TPR;
+        if constexpr (KC && BK == 16) {
+            // lanes row-fastest: a wavefront's 64 lanes cover 16 rows x 4 chunks
+            const int lane = tid & 63;
+            rr = (tid >> 6) * 16 + (lane & 15);
+            c = (lane >> 4) * 4;
+        } else {
+            c = (tid % TPR) * 4;
+            rr = tid / TPR;
+        }
         if constexpr (KC) {
 #pragma unroll
             for (int p = 0; p < NLOAD; ++p) {
@@ -127,7 +147,7 @@ struct Operand {
     }
 
     template <bool TAIL>
-    __device__ __forceinline__ void load(int64_t ld, int k0, int K) {
+    __device__ __forceinline__ void load(Regs &r, int64_t ld, int k0, int K) const {
         if constexpr (KC) {
             const int gk = k0 + c;
 #pragma unroll
@@ -171,11 +191,11 @@ struct Operand {
         }
     }
 
-    __device__ __forceinline__ void store(float *lds) const {
+    __device__ __forceinline__ void store(const Regs &r, float *lds) const {
 #pragma unroll
         for (int p = 0; p < NLOAD; ++p) {
             if constexpr (KC)
-                *reinterpret_cast<f4 *>(lds + (rr + p * RPP) * (BK + PAD_K) + c) = r[p];
+                *reinterpret_cast<f4 *>(lds + kc_off<BK>(rr + p * RPP, c >> 2)) = r[p];
             else
                 *reinterpret_cast<f4 *>(lds + (rr + p * RPP) * (T + PAD_I) + c) = r[p];
         }
@@ -192,8 +212,7 @@ __device__ __forceinline__ void read_frags(const float *lds, int off, int g, int
     if constexpr (KC) {
 #pragma unroll
         for (int f = 0; f < F; ++f)
-            fr[f] = *reinterpret_cast<const f4 *>(lds + (off + f * 32 + lo) * (BK + PAD_K) +
-                                                  8 * g + 4 * hi);
+            fr[f] = *reinterpret_cast<const f4 *>(lds + kc_off<BK>(off + f * 32 + lo, 2 * g + hi));
     } else {
 #pragma unroll
         for (int f = 0; f < F; ++f)
@@ -204,7 +223,7 @@ __device__ __forceinline__ void read_frags(const float *lds, int off, int g, int
 }
 
 template <int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, bool AV, bool BV>
-__global__ void __launch_bounds__(WM *WN * 64)
+__global__ void __launch_bounds__(WM *WN * 64) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_mfma_kernel(TiledArgs p) {
     constexpr int NT = WM * WN * 64;
     constexpr int WTM = BM / WM;
@@ -246,8 +265,10 @@ gemm_mfma_kernel(TiledArgs p) {
     const float *Ab = p.A + (int64_t)b * p.sA;
     const float *Bb = p.B + (int64_t)b * p.sB;
 
-    Operand<BM, BK, NT, AKC, AV> opa;
-    Operand<BN, BK, NT, BKC, BV> opb;
+    typedef Operand<BM, BK, NT, AKC, AV> OpA;
+    typedef Operand<BN, BK, NT, BKC, BV> OpB;
+    OpA opa;
+    OpB opb;
 
     f16 acc[FM][FN];
 #pragma unroll
@@ -264,50 +285,64 @@ gemm_mfma_kernel(TiledArgs p) {
 
     opa.init(Ab, p.lda, m0, p.M, tid);
     opb.init(Bb, p.ldb, n0, p.N, tid);
-    if (kt0 < nfull) {
-        opa.template load<false>(p.lda, kt0 * BK, K);
-        opb.template load<false>(p.ldb, kt0 * BK, K);
-    } else {
-        opa.template load<true>(p.lda, kt0 * BK, K);
-        opb.template load<true>(p.ldb, kt0 * BK, K);
-    }
-    opa.store(smem);
-    opb.store(smem + A_FL);
-    __syncthreads();
 
-    for (int kt = kt0; kt < kt1; ++kt) {
+    // Pipeline: global loads run two k-tiles ahead of the MFMAs in two register sets, the
+    // LDS holds two stages. While tile kt is multiplied out of stage kt%2, the registers
+    // of tile kt+1 (fetched one iteration earlier) are written to the other stage halfway
+    // through, and tile kt+2 is being fetched. The barrier closing tile kt then only
+    // orders LDS traffic; it never waits on global memory.
+    auto fetch = [&](typename OpA::Regs &ra, typename OpB::Regs &rb, int kt) {
+        if (kt < nfull) {
+            opa.template load<false>(ra, p.lda, kt * BK, K);
+            opb.template load<false>(rb, p.ldb, kt * BK, K);
+        } else {
+            opa.template load<true>(ra, p.lda, kt * BK, K);
+            opb.template load<true>(rb, p.ldb, kt * BK, K);
+        }
+    };
+    auto group = [&](const float *cur, int g) {
+        f4 fa[FM];
+        f4 fb[FN];
+        read_frags<BM, BK, AKC, FM>(cur, wm * WTM, g, lane, fa);
+        read_frags<BN, BK, BKC, FN>(cur + A_FL, wn * WTN, g, lane, fb);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s],
+                                                                     acc[i][j], 0, 0, 0);
+    };
+    // One k-tile: `held` carries tile kt+1 in, `spare` receives tile kt+2.
+    auto step = [&](int kt, typename OpA::Regs &helda, typename OpB::Regs &heldb,
+                    typename OpA::Regs &sparea, typename OpB::Regs &spareb) {
         const float *cur = smem + ((kt - kt0) & 1) * STAGE;
         float *nxt = smem + ((kt - kt0 + 1) & 1) * STAGE;
-        const bool more = kt + 1 < kt1;
-        if (more) {
-            if (kt + 1 < nfull) {
-                opa.template load<false>(p.lda, (kt + 1) * BK, K);
-                opb.template load<false>(p.ldb, (kt + 1) * BK, K);
-            } else {
-                opa.template load<true>(p.lda, (kt + 1) * BK, K);
-                opb.template load<true>(p.ldb, (kt + 1) * BK, K);
-            }
+        if (kt + 2 < kt1) fetch(sparea, spareb, kt + 2);
+        constexpr int G = BK / 8;
+#pragma unroll
+        for (int g = 0; g < (G + 1) / 2; ++g) group(cur, g);
+        if (kt + 1 < kt1) {
+            opa.store(helda, nxt);
+            opb.store(heldb, nxt + A_FL);
         }
 #pragma unroll
-        for (int g = 0; g < BK / 8; ++g) {
-            f4 fa[FM];
-            f4 fb[FN];
-            read_frags<BM, BK, AKC, FM>(cur, wm * WTM, g, lane, fa);
-            read_frags<BN, BK, BKC, FN>(cur + A_FL, wn * WTN, g, lane, fb);
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s],
-                                                                         acc[i][j], 0, 0, 0);
-        }
-        if (more) {
-            opa.store(nxt);
-            opb.store(nxt + A_FL);
-        }
+        for (int g = (G + 1) / 2; g < G; ++g) group(cur, g);
         __syncthreads();
+    };
+
+    typename OpA::Regs ra0, ra1;
+    typename OpB::Regs rb0, rb1;
+    fetch(ra0, rb0, kt0);
+    opa.store(ra0, smem);
+    opb.store(rb0, smem + A_FL);
+    if (kt0 + 1 < kt1) fetch(ra0, rb0, kt0 + 1);
+    __syncthreads();
+
+    for (int kt = kt0; kt < kt1; kt += 2) {
+        step(kt, ra0, rb0, ra1, rb1);
+        if (kt + 1 < kt1) step(kt + 1, ra1, rb1, ra0, rb0);
     }
 
     // ---- epilogue: accumulator (i, j) register r holds C row 8*(r/4) + 4*(lane/32) +
@@ -393,10 +428,14 @@ struct TileCfg {
     int bm, bn;
 };
 
+int lds_pad_bytes();
+
 template <int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, bool AV, bool BV>
 int launch_one(hipStream_t s, const TiledArgs &a) {
+    // Dynamic LDS is unused by the kernel; a tuning override (MIGEMM_LDS_PAD bytes) may
+    // reserve some to cap how many work-groups share a CU.
     hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AKC, BKC, AV, BV>),
-                       dim3(a.total), dim3(WM * WN * 64), 0, s, a);
+                       dim3(a.total), dim3(WM * WN * 64), lds_pad_bytes(), s, a);
     return hip_check(hipGetLastError(), "gemm_mfma_kernel launch");
 }
 
@@ -453,10 +492,15 @@ int launch_reduce_slices(hipStream_t stream, const float *partial, int slices, i
 }
 
 namespace {
-// Tuning overrides (MIGEMM_TILE = 32 | 64 | 128, MIGEMM_SPLITK = S), read once.
+// Tuning overrides (MIGEMM_TILE = 32 | 64 | 128, MIGEMM_SPLITK = S, MIGEMM_VARIANT,
+// MIGEMM_LDS_PAD), read once.
 int env_int(const char *name) {
     const char *v = getenv(name);
     return v != nullptr ? atoi(v) : 0;
+}
+int lds_pad_bytes() {
+    static const int pad = env_int("MIGEMM_LDS_PAD");
+    return pad > 0 && pad <= 65536 ? pad : 0;
 }
 }  // namespace
 
@@ -529,11 +573,23 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
             case 5: rc = launch_tiles<128, 256, 16, 2, 4>(stream, a, akc, bkc, true, true); break;
             case 6: rc = launch_tiles<128, 128, 8, 2, 2>(stream, a, akc, bkc, true, true); break;
             case 7: rc = launch_tiles<128, 128, 16, 4, 1>(stream, a, akc, bkc, true, true); break;
+            case 8: rc = launch_tiles<128, 128, 16, 1, 4>(stream, a, akc, bkc, true, true); break;
+            case 9: rc = launch_tiles<128, 128, 32, 4, 1>(stream, a, akc, bkc, true, true); break;
             default: rc = launch_tiles<128, 128, 16, 2, 2>(stream, a, akc, bkc, av, bv); break;
         }
     } else {
         switch (cfg) {
-            case 128: rc = launch_tiles<128, 128, 16, 2, 2>(stream, a, akc, bkc, av, bv); break;
+            case 128:
+                // Measured at 4096^3 (graph replay, 5 rounds): with 4 wavefronts of 32x128
+                // each (125 VGPRs, 4 work-groups per CU) NN / TN run at ~137 TFLOP/s but NT,
+                // whose two K-contiguous operands read 64-byte half lines per k-tile, drops
+                // to ~106 from extra L2 misses at that occupancy; 2x2 wavefronts of 64x64
+                // (2 work-groups per CU) give NT ~131.
+                if (akc && bkc)
+                    rc = launch_tiles<128, 128, 16, 2, 2>(stream, a, akc, bkc, av, bv);
+                else
+                    rc = launch_tiles<128, 128, 16, 4, 1>(stream, a, akc, bkc, av, bv);
+                break;
             case 64: rc = launch_tiles<64, 64, 32, 2, 2>(stream, a, akc, bkc, av, bv); break;
             default: rc = launch_tiles<32, 32, 32, 1, 1>(stream, a, akc, bkc, av, bv); break;
         }
