@@ -146,25 +146,23 @@ struct Operand {
         }
     }
 
+    // Fetch k-tile k0.. into registers. TAIL (the tile holding K's end) only clamps the
+    // addresses of k >= K to column / row 0 so every access stays inside the operand; the
+    // fetched values there are discarded by store<true>. Both forms issue the same loads,
+    // which keeps the compiler's load counters exact across the main loop.
     template <bool TAIL>
     __device__ __forceinline__ void load(Regs &r, int64_t ld, int k0, int K) const {
         if constexpr (KC) {
             const int gk = k0 + c;
 #pragma unroll
             for (int p = 0; p < NLOAD; ++p) {
-                if constexpr (!TAIL) {
+                if constexpr (VEC) {
+                    r[p] = load16(ptr[p] + ((!TAIL || gk < K) ? gk : 0));
+                } else if constexpr (!TAIL) {
                     r[p] = load16(ptr[p] + gk);  // a full k-tile: gk + 3 < K
-                } else if constexpr (VEC) {
-                    const bool ok = gk < K;
-                    const f4 v = load16(ptr[p] + (ok ? gk : 0));
-                    r[p] = ok ? v : f4{0.f, 0.f, 0.f, 0.f};
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const bool ok = gk + e < K;
-                        const float x = ptr[p][ok ? gk + e : 0];
-                        r[p][e] = ok ? x : 0.f;
-                    }
+                    for (int e = 0; e < 4; ++e) r[p][e] = ptr[p][gk + e < K ? gk + e : 0];
                 }
             }
         } else {
@@ -172,32 +170,39 @@ struct Operand {
 #pragma unroll
             for (int p = 0; p < NLOAD; ++p) {
                 const float *src = ptr[p] + koff;
-                bool ok = true;
                 if constexpr (TAIL) {
-                    ok = k0 + rr + p * RPP < K;
                     // a k row past K is replaced by row 0 of the tile's source
-                    src = ok ? src : ptr[p] - (int64_t)(rr + p * RPP) * ld;
+                    if (k0 + rr + p * RPP >= K) src = ptr[p] - (int64_t)(rr + p * RPP) * ld;
                 }
-                f4 v;
                 if constexpr (VEC) {
-                    v = load16(src);
+                    r[p] = load16(src);
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = src[coff[e]];
+                    for (int e = 0; e < 4; ++e) r[p][e] = src[coff[e]];
                 }
-                if constexpr (TAIL) v = ok ? v : f4{0.f, 0.f, 0.f, 0.f};
-                r[p] = v;
             }
         }
     }
 
-    __device__ __forceinline__ void store(const Regs &r, float *lds) const {
+    // Write a fetched k-tile to LDS; TAIL zero-fills k >= K (matmul.cl:39-52 pads both
+    // operands with zeros) before the write.
+    template <bool TAIL>
+    __device__ __forceinline__ void store(const Regs &r, float *lds, int k0, int K) const {
 #pragma unroll
         for (int p = 0; p < NLOAD; ++p) {
+            f4 v = r[p];
+            if constexpr (TAIL) {
+                if constexpr (KC) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = (k0 + c + e < K) ? v[e] : 0.f;
+                } else {
+                    if (k0 + rr + p * RPP >= K) v = f4{0.f, 0.f, 0.f, 0.f};
+                }
+            }
             if constexpr (KC)
-                *reinterpret_cast<f4 *>(lds + kc_off<BK>(rr + p * RPP, c >> 2)) = r[p];
+                *reinterpret_cast<f4 *>(lds + kc_off<BK>(rr + p * RPP, c >> 2)) = v;
             else
-                *reinterpret_cast<f4 *>(lds + (rr + p * RPP) * (T + PAD_I) + c) = r[p];
+                *reinterpret_cast<f4 *>(lds + (rr + p * RPP) * (T + PAD_I) + c) = v;
         }
     }
 };
@@ -291,14 +296,16 @@ gemm_mfma_kernel(TiledArgs p) {
     // of tile kt+1 (fetched one iteration earlier) are written to the other stage halfway
     // through, and tile kt+2 is being fetched. The barrier closing tile kt then only
     // orders LDS traffic; it never waits on global memory.
+    // Full k-tiles [kt0, kf) run through the pipelined main loop, which contains no tail
+    // code; the zero-filled tail tile (K % BK != 0, index nfull) follows it.
     auto fetch = [&](typename OpA::Regs &ra, typename OpB::Regs &rb, int kt) {
-        if (kt < nfull) {
-            opa.template load<false>(ra, p.lda, kt * BK, K);
-            opb.template load<false>(rb, p.ldb, kt * BK, K);
-        } else {
-            opa.template load<true>(ra, p.lda, kt * BK, K);
-            opb.template load<true>(rb, p.ldb, kt * BK, K);
-        }
+        opa.template load<false>(ra, p.lda, kt * BK, K);
+        opb.template load<false>(rb, p.ldb, kt * BK, K);
+    };
+    auto put = [&](const typename OpA::Regs &ra, const typename OpB::Regs &rb, float *stage,
+                   int kt) {
+        opa.template store<false>(ra, stage, kt * BK, K);
+        opb.template store<false>(rb, stage + A_FL, kt * BK, K);
     };
     auto group = [&](const float *cur, int g) {
         f4 fa[FM];
@@ -314,19 +321,21 @@ gemm_mfma_kernel(TiledArgs p) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s],
                                                                      acc[i][j], 0, 0, 0);
     };
-    // One k-tile: `held` carries tile kt+1 in, `spare` receives tile kt+2.
+    const int kf = min(kt1, nfull);  // end of the full k-tiles of this range
+    // One k-tile: `held` carries tile kt+1 in, `spare` receives tile kt+2. Every fetch and
+    // LDS write in the main loop is unconditional (past the last full tile the fetch
+    // re-reads it and the write lands in the stage nobody reads again), and the loop runs
+    // whole pairs of steps, so the compiler's load counters see one straight-line pattern
+    // and each LDS write waits only on the previous step's loads.
     auto step = [&](int kt, typename OpA::Regs &helda, typename OpB::Regs &heldb,
                     typename OpA::Regs &sparea, typename OpB::Regs &spareb) {
         const float *cur = smem + ((kt - kt0) & 1) * STAGE;
         float *nxt = smem + ((kt - kt0 + 1) & 1) * STAGE;
-        if (kt + 2 < kt1) fetch(sparea, spareb, kt + 2);
+        fetch(sparea, spareb, min(kt + 2, kf - 1));
         constexpr int G = BK / 8;
 #pragma unroll
         for (int g = 0; g < (G + 1) / 2; ++g) group(cur, g);
-        if (kt + 1 < kt1) {
-            opa.store(helda, nxt);
-            opb.store(heldb, nxt + A_FL);
-        }
+        put(helda, heldb, nxt, kt + 1);
 #pragma unroll
         for (int g = (G + 1) / 2; g < G; ++g) group(cur, g);
         __syncthreads();
@@ -334,15 +343,32 @@ gemm_mfma_kernel(TiledArgs p) {
 
     typename OpA::Regs ra0, ra1;
     typename OpB::Regs rb0, rb1;
-    fetch(ra0, rb0, kt0);
-    opa.store(ra0, smem);
-    opb.store(rb0, smem + A_FL);
-    if (kt0 + 1 < kt1) fetch(ra0, rb0, kt0 + 1);
-    __syncthreads();
-
-    for (int kt = kt0; kt < kt1; kt += 2) {
-        step(kt, ra0, rb0, ra1, rb1);
-        if (kt + 1 < kt1) step(kt + 1, ra1, rb1, ra0, rb0);
+    int kt = kt0;
+    if (kt0 < kf) {
+        fetch(ra0, rb0, kt0);
+        put(ra0, rb0, smem, kt0);
+        fetch(ra0, rb0, min(kt0 + 1, kf - 1));
+        __syncthreads();
+        for (; kt + 1 < kf; kt += 2) {
+            step(kt, ra0, rb0, ra1, rb1);
+            step(kt + 1, ra1, rb1, ra0, rb0);
+        }
+        if (kt < kf) {  // an odd last full tile, already in its LDS stage
+            const float *cur = smem + ((kt - kt0) & 1) * STAGE;
+#pragma unroll
+            for (int g = 0; g < BK / 8; ++g) group(cur, g);
+            ++kt;
+        }
+    }
+    if (kt < kt1) {  // the tail tile: k >= K zero-filled in both operands
+        opa.template load<true>(ra1, p.lda, kt * BK, K);
+        opb.template load<true>(rb1, p.ldb, kt * BK, K);
+        __syncthreads();  // every wavefront is done reading the stages
+        opa.template store<true>(ra1, smem, kt * BK, K);
+        opb.template store<true>(rb1, smem + A_FL, kt * BK, K);
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < BK / 8; ++g) group(smem, g);
     }
 
     // ---- epilogue: accumulator (i, j) register r holds C row 8*(r/4) + 4*(lane/32) +
@@ -548,10 +574,25 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         splits = (int)(want < cap ? want : cap);
         if (splits < 1) splits = 1;
     }
+    // Large outputs: pick the macro-tile by the busiest CU's share of the work. The work-
+    // groups are dealt over the 256 CUs, so a CU carries ceil(tiles / 256) tiles; the
+    // factor is each shape's measured MFMA efficiency at 4096^3 (256x256: 143.8, 128x256:
+    // 141.1, 128x128: 138.9 TFLOP/s over NN / NT / TN).
+    int big = 0;  // 0: 128x128, 1: 128x256, 2: 256x256
+    if (cfg == 128) {
+        const double c0 = (double)((tiles(128, 128) + 255) / 256) * 16384.0 / 0.966;
+        const double c1 = (double)((tiles(128, 256) + 255) / 256) * 32768.0 / 0.981;
+        const double c2 = (double)((tiles(256, 256) + 255) / 256) * 65536.0 / 1.0;
+        big = c2 <= c1 && c2 <= c0 ? 2 : (c1 <= c0 ? 1 : 0);
+    }
     static const int force_tile = env_int("MIGEMM_TILE");
     static const int force_split = env_int("MIGEMM_SPLITK");
     static const int variant = env_int("MIGEMM_VARIANT");
     if (force_tile == 32 || force_tile == 64 || force_tile == 128) cfg = force_tile;
+    if (force_tile == 256) {
+        cfg = 128;
+        big = 2;
+    }
     if (force_split >= 1) splits = force_split;
 
     a.splits = splits;
@@ -566,27 +607,27 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     if (variant != 0 && cfg == 128 && av && bv) {
         // Tile-shape variants for tuning sweeps (MIGEMM_VARIANT); 128-bit loads only.
         switch (variant) {
-            case 1: rc = launch_tiles<256, 128, 32, 4, 2>(stream, a, akc, bkc, true, true); break;
-            case 2: rc = launch_tiles<128, 256, 32, 2, 4>(stream, a, akc, bkc, true, true); break;
-            case 3: rc = launch_tiles<128, 128, 32, 2, 2>(stream, a, akc, bkc, true, true); break;
+            case 1: rc = launch_tiles<256, 128, 16, 8, 1>(stream, a, akc, bkc, true, true); break;
+            case 2: rc = launch_tiles<128, 256, 16, 4, 2>(stream, a, akc, bkc, true, true); break;
+            case 3: rc = launch_tiles<128, 128, 32, 4, 1>(stream, a, akc, bkc, true, true); break;
             case 4: rc = launch_tiles<256, 128, 16, 4, 2>(stream, a, akc, bkc, true, true); break;
-            case 5: rc = launch_tiles<128, 256, 16, 2, 4>(stream, a, akc, bkc, true, true); break;
-            case 6: rc = launch_tiles<128, 128, 8, 2, 2>(stream, a, akc, bkc, true, true); break;
-            case 7: rc = launch_tiles<128, 128, 16, 4, 1>(stream, a, akc, bkc, true, true); break;
-            case 8: rc = launch_tiles<128, 128, 16, 1, 4>(stream, a, akc, bkc, true, true); break;
-            case 9: rc = launch_tiles<128, 128, 32, 4, 1>(stream, a, akc, bkc, true, true); break;
-            default: rc = launch_tiles<128, 128, 16, 2, 2>(stream, a, akc, bkc, av, bv); break;
+            case 5: rc = launch_tiles<128, 128, 16, 2, 2>(stream, a, akc, bkc, true, true); break;
+            case 6: rc = launch_tiles<128, 128, 16, 1, 4>(stream, a, akc, bkc, true, true); break;
+            case 7: rc = launch_tiles<256, 256, 16, 8, 2>(stream, a, akc, bkc, true, true); break;
+            default: rc = launch_tiles<128, 128, 16, 4, 1>(stream, a, akc, bkc, av, bv); break;
         }
     } else {
         switch (cfg) {
             case 128:
-                // Measured at 4096^3 (graph replay, 5 rounds): with 4 wavefronts of 32x128
-                // each (125 VGPRs, 4 work-groups per CU) NN / TN run at ~137 TFLOP/s but NT,
-                // whose two K-contiguous operands read 64-byte half lines per k-tile, drops
-                // to ~106 from extra L2 misses at that occupancy; 2x2 wavefronts of 64x64
-                // (2 work-groups per CU) give NT ~131.
-                if (akc && bkc)
-                    rc = launch_tiles<128, 128, 16, 2, 2>(stream, a, akc, bkc, av, bv);
+                // Wavefronts of 32x128 (124-128 VGPRs, 4 per SIMD). Measured at 4096^3
+                // (graph replay, 5 rounds), NN / NT / TN TFLOP/s: 256x256 with 16 wavefronts
+                // 141.4 / 145.4 / 144.6; 128x256 with 8: 141.2 / 140.5 / 141.5; 128x128 with
+                // 4: 140.2 / 136.1 / 140.3; 128x128 with 2x2 wavefronts of 64x64: 140.1 /
+                // 125.9 / 140.2.
+                if (big == 2)
+                    rc = launch_tiles<256, 256, 16, 8, 2>(stream, a, akc, bkc, av, bv);
+                else if (big == 1)
+                    rc = launch_tiles<128, 256, 16, 4, 2>(stream, a, akc, bkc, av, bv);
                 else
                     rc = launch_tiles<128, 128, 16, 4, 1>(stream, a, akc, bkc, av, bv);
                 break;

@@ -308,3 +308,18 @@ def test_unaligned_bases_and_leading_dims(nncl, ta, tb):
     Bop = B.T if tb else B
     expect = (Aop.astype(np.int64) @ Bop.astype(np.int64)).astype(np.float32)
     assert np.array_equal(host(c), expect)
+
+
+@pytest.mark.parametrize("M,K,N", [(2000, 50, 3980), (3000, 70, 2900), (4000, 50, 4090)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+def test_large_tile_shapes_exact(nncl, M, K, N, ta, tb):
+    """Ragged shapes on which the dispatcher picks each large macro-tile (128x256,
+    128x128, 256x256), with a zero-filled K tail; exact small-integer products."""
+    say("large tiles exact", M, K, N, ta, tb)
+    A = small_ints((K, M) if ta else (M, K), M + K)
+    B = small_ints((N, K) if tb else (K, N), N + K)
+    Aop = (A.T if ta else A).astype(np.float64)
+    Bop = (B.T if tb else B).astype(np.float64)
+    expect = (Aop @ Bop).astype(np.float32)  # exact: |sums| <= 16*K << 2^24
+    got = gemm_gpu(nncl, A, B, bool(ta), bool(tb))
+    assert np.array_equal(got, expect)
