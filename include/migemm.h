@@ -173,6 +173,21 @@ const char *migemm_last_error(void);
 /* Library version, e.g. "0.1.0". */
 const char *migemm_version(void);
 
+/* ------------------------------------------------------------------------------- */
+/* (4) Kernel selection. The reference has one kernel per form (cl_kernels/matmul.cl:8,
+ *     :78; cs/cl_kernels/bmm_permute_tiled.cl:7); this library chooses per shape among
+ *     three kernel families. The policy is process-wide and exists for tests and tuning:
+ *     every policy computes the same product within the fp32 tolerance, only the kernel
+ *     family (and so the association order of the sums) changes. */
+#define MIGEMM_POLICY_AUTO 0   /* choice by shape (default) */
+#define MIGEMM_POLICY_TILED 1  /* LDS-tiled 32x32x2 MFMA kernel (+ split-K) for every shape */
+#define MIGEMM_POLICY_SMALL 2  /* k-split 16x16x4 MFMA small-output kernel for every shape */
+#define MIGEMM_POLICY_SKINNY 3 /* fp32-FMA kernel wherever it applies (M <= 4, B not
+                                  transposed), otherwise the AUTO choice */
+/* Sets the policy; *previous (if not NULL) receives the one it replaces. Calls already
+ * enqueued are unaffected. */
+int migemm_set_gemm_policy(int policy, int *previous);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,6 +19,12 @@ MIGEMM_ERR_NO_DEVICE = 4
 MIGEMM_ERR_WORKSPACE = 5
 MIGEMM_ERR_UNSUPPORTED = 6
 
+# Kernel-family policies (migemm_set_gemm_policy)
+MIGEMM_POLICY_AUTO = 0
+MIGEMM_POLICY_TILED = 1
+MIGEMM_POLICY_SMALL = 2
+MIGEMM_POLICY_SKINNY = 3
+
 STATUS_NAMES = {
     MIGEMM_OK: "MIGEMM_OK",
     MIGEMM_ERR_INVALID_ARG: "MIGEMM_ERR_INVALID_ARG",
@@ -80,6 +86,7 @@ SIGNATURES = {
     "migemm_stream_synchronize": ([_vp], _i32),
     "migemm_last_error": ([], ctypes.c_char_p),
     "migemm_version": ([], ctypes.c_char_p),
+    "migemm_set_gemm_policy": ([_i32, _ip], _i32),
 }
 
 _lib = None
@@ -130,3 +137,10 @@ def check(status):
 def call(name, *args):
     """Call an exported function and raise on a non-zero status."""
     check(getattr(load(), name)(*args))
+
+
+def set_gemm_policy(policy):
+    """Select the kernel family for later GEMM calls; returns the previous policy."""
+    prev = ctypes.c_int(0)
+    call("migemm_set_gemm_policy", int(policy), ctypes.byref(prev))
+    return prev.value

@@ -9,6 +9,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -156,8 +157,17 @@ static int validate_gemm(int transA, int transB, int M, int N, int K, const floa
     return MIGEMM_OK;
 }
 
+// Kernel-family policy (migemm_set_gemm_policy), process-wide.
+static std::atomic<int> g_policy{MIGEMM_POLICY_AUTO};
+
 static int run_gemm(hipStream_t stream, const GemmDesc &d) {
+    switch (g_policy.load(std::memory_order_relaxed)) {
+        case MIGEMM_POLICY_TILED: return launch_gemm_tiled(stream, d);
+        case MIGEMM_POLICY_SMALL: return launch_gemm_small(stream, d);
+        default: break;
+    }
     if (skinny_applicable(d)) return launch_gemm_skinny(stream, d);
+    if (small_preferred(d)) return launch_gemm_small(stream, d);
     return launch_gemm_tiled(stream, d);
 }
 
@@ -417,5 +427,14 @@ int migemm_stream_synchronize(void *stream) {
 const char *migemm_last_error(void) { return g_last_error; }
 
 const char *migemm_version(void) { return "0.1.0"; }
+
+int migemm_set_gemm_policy(int policy, int *previous) {
+    clear_error();
+    if (policy < MIGEMM_POLICY_AUTO || policy > MIGEMM_POLICY_SKINNY)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "set_gemm_policy: unknown policy %d", policy);
+    const int old = g_policy.exchange(policy);
+    if (previous != nullptr) *previous = old;
+    return MIGEMM_OK;
+}
 
 }  // extern "C"

@@ -413,37 +413,61 @@ gemm_mfma_kernel(TiledArgs p) {
 }
 
 // C_b[m, n] = partial[0][b][m][n] + ... + partial[S-1][b][m][n] (+ bias[n]), added in
-// slice order. One output per thread; the partials are read RS_GROUP slices at a time
-// with every load of a group issued before the group is summed (a serial load-add chain
-// would pay one full memory latency per slice).
+// slice order. Each thread owns VW consecutive outputs of the flattened [batch][M][N]
+// partial array (VW = 4: one 128-bit load per slice, for large outputs; VW = 1 spreads a
+// small output, such as a GEMV's, over more CUs) and reads RS_GROUP slices at a time with
+// every load of a group issued before the group is summed (a serial load-add chain would
+// pay one full memory latency per slice).
 constexpr int RS_GROUP = 16;
 
+template <int VW>
 __global__ void __launch_bounds__(256)
 reduce_slices_kernel(const float *__restrict__ partial, int slices, int batch, int M, int N,
                      const float *__restrict__ bias, float *__restrict__ C, int64_t ldc,
                      int64_t strideC) {
+    typedef float vec __attribute__((ext_vector_type(VW)));
     const int64_t total = (int64_t)batch * M * N;
+    const int64_t nvec = (total + VW - 1) / VW;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += step) {
+    for (int64_t vi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; vi < nvec; vi += step) {
+        const int64_t t = vi * VW;
+        const int cnt = total - t >= VW ? VW : (int)(total - t);
         const float *src = partial + t;
-        float v = 0.f;
-        for (int s0 = 0; s0 < slices; s0 += RS_GROUP) {
-            float x[RS_GROUP];
+        vec v = {};
+        if (cnt == VW) {
+            for (int s0 = 0; s0 < slices; s0 += RS_GROUP) {
+                vec x[RS_GROUP];
 #pragma unroll
-            for (int g = 0; g < RS_GROUP; ++g) {
-                const int sl = s0 + g < slices ? s0 + g : slices - 1;
-                x[g] = src[(int64_t)sl * total];
+                for (int g = 0; g < RS_GROUP; ++g)
+                    if (s0 + g < slices) __builtin_memcpy(&x[g], src + (int64_t)(s0 + g) * total,
+                                                          sizeof(vec));
+#pragma unroll
+                for (int g = 0; g < RS_GROUP; ++g)
+                    if (s0 + g < slices) v = (s0 + g == 0) ? x[g] : v + x[g];
             }
-#pragma unroll
-            for (int g = 0; g < RS_GROUP; ++g)
-                if (s0 + g < slices) v = (s0 + g == 0) ? x[g] : v + x[g];
+        } else {
+            for (int e = 0; e < cnt; ++e) {
+                float acc = src[e];
+                for (int sl = 1; sl < slices; ++sl) acc = acc + src[(int64_t)sl * total + e];
+                v[e] = acc;
+            }
         }
-        const int64_t row = t / N;
-        const int n = (int)(t - row * N);
-        const int64_t b = row / M;
-        const int m = (int)(row - b * M);
-        if (bias != nullptr) v = v + bias[n];
-        C[b * strideC + (int64_t)m * ldc + n] = v;
+        int64_t row = t / N;  // flattened (b, m)
+        int n = (int)(t - row * N);
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+            if (e < cnt) {
+                const int64_t b = row / M;
+                const int m = (int)(row - b * M);
+                float o = v[e];
+                if (bias != nullptr) o = o + bias[n];
+                C[b * strideC + (int64_t)m * ldc + n] = o;
+            }
+            if (++n == N) {
+                n = 0;
+                ++row;
+            }
+        }
     }
 }
 
@@ -510,10 +534,16 @@ int launch_reduce_slices(hipStream_t stream, const float *partial, int slices, i
                          int M, int N, const float *bias, float *C, int64_t ldc,
                          int64_t strideC) {
     const int64_t total = (int64_t)batch * M * N;
-    int64_t blocks = (total + 255) / 256;
+    // 4 outputs per thread once that still gives every CU a work-group
+    const bool wide = total >= 4 * 256 * 256;
+    int64_t blocks = ((wide ? (total + 3) / 4 : total) + 255) / 256;
     if (blocks > 16384) blocks = 16384;
-    hipLaunchKernelGGL(reduce_slices_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
-                       partial, slices, batch, M, N, bias, C, ldc, strideC);
+    if (wide)
+        hipLaunchKernelGGL(reduce_slices_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                           partial, slices, batch, M, N, bias, C, ldc, strideC);
+    else
+        hipLaunchKernelGGL(reduce_slices_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                           partial, slices, batch, M, N, bias, C, ldc, strideC);
     return hip_check(hipGetLastError(), "reduce_slices_kernel launch");
 }
 

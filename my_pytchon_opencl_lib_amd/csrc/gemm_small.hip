@@ -1,0 +1,381 @@
+// Small-output fp32 GEMM for gfx950 (v_mfma_f32_16x16x4_f32): shapes whose C has too few
+// 64x64 tiles to occupy the 256 CUs. These are the latency-bound calls of the matmul path:
+// the 256^3 matmul_tiled test GEMM, the batch-32 attention BMMs, and the 64-row gate GEMM
+// of lstm_gemm_xw (cs/cl_kernels/lstm.cl:273) and linear_forward_tiled
+// (cs/cl_kernels/linear.cl:14) at small batch ("cs/" = csharp/cstorchcl/cstorchcl/).
+//
+// In the tiled kernel one wavefront walks the whole K range of its 32x32 sub-tile, so with
+// few tiles the MFMA chain of a single wavefront is the run time. Here the K range is
+// divided among the wavefronts instead:
+//  * A work-group owns a (16*MB) x 16 tile of C and has NW wavefronts; wavefront w
+//    multiplies the w-th contiguous share of the work-group's 16-wide k-groups, and the NW
+//    partial tiles are added in LDS in the order w = 0..NW-1 (deterministic).
+//  * No LDS staging of operands: wavefronts of one work-group share no operand data (each
+//    has its own k range), so fragments go from global memory (L2) straight to registers,
+//    three k-groups in flight per wavefront.
+//  * Fragments: in step j (0..3) of a k-group, lane l supplies row/column l%16 at
+//    k = 4*(l/16) + j. An operand contiguous in M or N fetches four 32-bit values, 16
+//    lanes covering 64 contiguous bytes. A K-contiguous operand is fetched with one
+//    coalesced 128-bit load per lane (4 rows x 64 bytes per 16 lanes) and moved into
+//    fragment order by a lane permutation. Both operands use the same k order, so the
+//    sum is the full dot product; only the fp32 association order differs from the
+//    reference's ascending chain.
+//  * Edges: rows beyond M and columns beyond N are clamped on load and never stored; the
+//    last, partial k-group (K % 16 != 0) is loaded element by element with k >= K set to
+//    zero in both operands.
+//  * If the output tiles times the wavefronts still cannot fill the chip, the k-groups
+//    are further divided into S ranges over work-groups; range s writes its partial tile
+//    to the library workspace and reduce_slices_kernel adds the ranges in order (then the
+//    bias), as the tiled kernel's split-K does.
+#include <stdlib.h>
+
+#include "migemm_internal.h"
+
+namespace migemm {
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+struct SmallArgs {
+    const float *A;
+    const float *B;
+    const float *bias;
+    float *C;
+    int64_t lda, ldb, ldc;
+    int64_t sA, sB, sC;
+    int M, N, K;
+    int tiles_m, tiles_n;  // tiles per batch entry
+    int batch;
+    int total;             // tiles_m * tiles_n * batch * splits
+    int splits;            // k ranges over work-groups (1 = none)
+    int groups_per_split;  // 16-wide k-groups per range
+    float *partial;        // [splits][batch][M][N] when splits > 1
+};
+
+constexpr int KG = 16;       // k values per k-group (4 MFMA steps of 4)
+constexpr int INFLIGHT = 3;  // k-groups of loads in flight per wavefront
+
+__device__ __forceinline__ f4 load16(const float *p) {
+    f4 v;
+    __builtin_memcpy(&v, p, sizeof(v));
+    return v;
+}
+
+// One k-group (16 values of k, four MFMA steps j of 4) of a wavefront's operands: a[blk]
+// for 16-row block blk of A, b for B. M/N-contiguous operand: the fragment values of steps
+// j = 0..3. K-contiguous operand: the 128-bit load, before the lane permutation.
+template <int MB>
+struct Frag {
+    f4 a[MB];
+    f4 b;
+};
+
+template <int MB, int NW, bool AKC, bool BKC>
+__global__ void __launch_bounds__(NW * 64) gemm_small_kernel(SmallArgs p) {
+    __shared__ float red[NW][MB * 4][64];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int li = lane & 15;  // fragment row (A) / column (B) of this lane in a 16-block
+    const int lq = lane >> 4;  // fragment k quarter of this lane in a k-group
+
+    // ---- work-group -> (split, batch, tile); consecutive tiles share an XCD ----
+    int pid = blockIdx.x;
+    const int total = p.total;
+    if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
+    const int per_batch = p.tiles_m * p.tiles_n;
+    const int per_split = per_batch * p.batch;
+    const int split = pid / per_split;
+    pid -= split * per_split;
+    const int b = pid / per_batch;
+    const int t = pid - b * per_batch;
+    const int tm = t / p.tiles_n;
+    const int tn = t - tm * p.tiles_n;
+    const int m0 = tm * 16 * MB;
+    const int n0 = tn * 16;
+
+    const float *Ab = p.A + (int64_t)b * p.sA;
+    const float *Bb = p.B + (int64_t)b * p.sB;
+
+    // Per-lane operand pointers at k-group 0 (rows / columns clamped).
+    // AKC: A(i, k) = Ab[i*lda + k]; else A(i, k) = Ab[k*lda + i]. BKC: B(k, n) = Bb[n*ldb + k];
+    // else B(k, n) = Bb[k*ldb + n].
+    // An operand contiguous in M or N is read in fragment order: lane (lq, li) loads
+    // row/column li at k = 4*lq + j, and each 16-lane group covers 64 contiguous bytes.
+    // A K-contiguous operand read in fragment order would give every 16-lane group 16
+    // different rows (16 bytes each, 4x the L1 accesses of the data), so it is read
+    // coalesced instead: lane (lq, li = 4a + c) loads the 16 bytes of row 4*lq + a at
+    // k = 4c .. 4c+3 (a 16-lane group reads 4 rows x 64 contiguous bytes), and a lane
+    // permutation (ds_bpermute, no LDS storage) gives lane (lq, li) row li at k = 4*lq + j.
+    const int crow = 4 * lq + (li >> 2);
+    const int ck = 4 * (li & 3);
+    const int perm_src = (16 * (li >> 2) + 4 * (li & 3) + lq) * 4;  // byte index of source lane
+    const float *pa[MB];
+#pragma unroll
+    for (int blk = 0; blk < MB; ++blk) {
+        if constexpr (AKC)
+            pa[blk] = Ab + (int64_t)min(m0 + blk * 16 + crow, p.M - 1) * p.lda + ck;
+        else
+            pa[blk] = Ab + (int64_t)(4 * lq) * p.lda + min(m0 + blk * 16 + li, p.M - 1);
+    }
+    const float *pb = BKC ? Bb + (int64_t)min(n0 + crow, p.N - 1) * p.ldb + ck
+                          : Bb + (int64_t)(4 * lq) * p.ldb + min(n0 + li, p.N - 1);
+    // distance between consecutive k-groups
+    const int64_t a_gstep = AKC ? KG : (int64_t)KG * p.lda;
+    const int64_t b_gstep = BKC ? KG : (int64_t)KG * p.ldb;
+
+    auto load = [&](Frag<MB> &f, int g) {
+#pragma unroll
+        for (int blk = 0; blk < MB; ++blk) {
+            const float *q = pa[blk] + g * a_gstep;
+            if constexpr (AKC)
+                f.a[blk] = load16(q);
+            else
+                f.a[blk] = f4{q[0], q[p.lda], q[2 * p.lda], q[3 * p.lda]};
+        }
+        const float *q = pb + g * b_gstep;
+        if constexpr (BKC)
+            f.b = load16(q);
+        else
+            f.b = f4{q[0], q[p.ldb], q[2 * p.ldb], q[3 * p.ldb]};
+    };
+
+    auto permute = [&](f4 v) {
+        f4 r;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            r[j] = __int_as_float(__builtin_amdgcn_ds_bpermute(perm_src, __float_as_int(v[j])));
+        return r;
+    };
+
+    f4 acc[MB];
+#pragma unroll
+    for (int blk = 0; blk < MB; ++blk) acc[blk] = f4{0.f, 0.f, 0.f, 0.f};
+
+    // `direct`: the operands were loaded in fragment order (the partial k-group).
+    auto mma = [&](const Frag<MB> &f, bool direct) {
+        f4 fa[MB];
+#pragma unroll
+        for (int blk = 0; blk < MB; ++blk)
+            fa[blk] = AKC && !direct ? permute(f.a[blk]) : f.a[blk];
+        const f4 fb = BKC && !direct ? permute(f.b) : f.b;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int blk = 0; blk < MB; ++blk)
+                acc[blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[blk][j], fb[j], acc[blk],
+                                                                0, 0, 0);
+    };
+
+    // ---- k-groups of this wavefront ----
+    const int K = p.K;
+    const int G = (K + KG - 1) / KG;
+    const int gfull = K / KG;  // k-groups entirely inside K
+    const int gs0 = split * p.groups_per_split;
+    const int gs1 = min(G, gs0 + p.groups_per_split);
+    const int per_wave = (gs1 - gs0 + NW - 1) / NW;
+    const int glo = min(gs1, gs0 + w * per_wave);
+    const int ghi = min(gs1, glo + per_wave);
+    const int gend = min(ghi, gfull);
+
+    if (glo < gend) {
+        // Each work-group starts its wavefronts' ranges at its own rotation, so the work-
+        // groups of an XCD, which read the same A (or B) panel, do not all request the
+        // same lines from the same L2 channels at the same time.
+        const int nfg = gend - glo;
+        const int rot = (int)((blockIdx.x * 5u) % (unsigned)nfg);
+        auto kgroup = [&](int i) {  // i-th k-group of the range, i < nfg
+            const int x = i + rot;
+            return glo + (x >= nfg ? x - nfg : x);
+        };
+        // INFLIGHT register sets rotate; every load in the loop is unconditional (past the
+        // end it re-reads the last k-group, which is never multiplied). The scheduling
+        // barriers keep each set's loads together and in order: left free, the scheduler
+        // sinks all refills to the end of the iteration and interleaves the sets, so the
+        // first MFMA of an iteration has to wait for almost every load in flight.
+        Frag<MB> f[INFLIGHT];
+#pragma unroll
+        for (int i = 0; i < INFLIGHT; ++i) {
+            load(f[i], kgroup(min(i, nfg - 1)));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        int i0 = 0;
+        for (; i0 + INFLIGHT <= nfg; i0 += INFLIGHT) {
+#pragma unroll
+            for (int i = 0; i < INFLIGHT; ++i) {
+                mma(f[i], false);
+                __builtin_amdgcn_sched_barrier(0);
+                load(f[i], kgroup(min(i0 + INFLIGHT + i, nfg - 1)));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < INFLIGHT; ++i)
+            if (i < nfg - i0) mma(f[i], false);
+    }
+    if (ghi > gfull && glo <= gfull) {
+        // the partial k-group: element-wise loads in fragment order, k >= K zero in both
+        // operands
+        Frag<MB> f;
+        const int nc = min(n0 + li, p.N - 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k = gfull * KG + 4 * lq + j;
+            const bool ok = k < K;
+#pragma unroll
+            for (int blk = 0; blk < MB; ++blk) {
+                const int i = min(m0 + blk * 16 + li, p.M - 1);
+                const int64_t off = AKC ? (int64_t)i * p.lda + k : (int64_t)k * p.lda + i;
+                f.a[blk][j] = ok ? Ab[off] : 0.f;
+            }
+            const int64_t off = BKC ? (int64_t)nc * p.ldb + k : (int64_t)k * p.ldb + nc;
+            f.b[j] = ok ? Bb[off] : 0.f;
+        }
+        mma(f, true);
+    }
+
+    // ---- combine the NW wavefronts in order, then store (or write the partial) ----
+    // Output layout of v_mfma_f32_16x16x4_f32: lane l, register r holds row 4*(l/16) + r,
+    // column l%16 of its 16x16 block.
+#pragma unroll
+    for (int blk = 0; blk < MB; ++blk)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[w][blk * 4 + r][lane] = acc[blk][r];
+    __syncthreads();
+
+    for (int e = tid; e < MB * 256; e += NW * 64) {
+        const int row = e >> 4;  // 0 .. 16*MB-1
+        const int col = e & 15;
+        const int slot = (row >> 4) * 4 + (row & 3);
+        const int src = ((row & 15) >> 2) * 16 + col;
+        float v = red[0][slot][src];
+#pragma unroll
+        for (int q = 1; q < NW; ++q) v += red[q][slot][src];
+        const int m = m0 + row;
+        const int n = n0 + col;
+        if (m < p.M && n < p.N) {
+            if (p.splits == 1) {
+                if (p.bias != nullptr) v = v + p.bias[n];
+                p.C[(int64_t)b * p.sC + (int64_t)m * p.ldc + n] = v;
+            } else {
+                p.partial[(((int64_t)split * p.batch + b) * p.M + m) * p.N + n] = v;
+            }
+        }
+    }
+}
+
+template <int MB, int NW>
+int launch_layout(hipStream_t st, const SmallArgs &a, bool akc, bool bkc) {
+    const dim3 grid(a.total), block(NW * 64);
+    if (akc && bkc)
+        hipLaunchKernelGGL((gemm_small_kernel<MB, NW, true, true>), grid, block, 0, st, a);
+    else if (akc)
+        hipLaunchKernelGGL((gemm_small_kernel<MB, NW, true, false>), grid, block, 0, st, a);
+    else if (bkc)
+        hipLaunchKernelGGL((gemm_small_kernel<MB, NW, false, true>), grid, block, 0, st, a);
+    else
+        hipLaunchKernelGGL((gemm_small_kernel<MB, NW, false, false>), grid, block, 0, st, a);
+    return hip_check(hipGetLastError(), "gemm_small_kernel launch");
+}
+
+template <int MB>
+int launch_nw(hipStream_t st, const SmallArgs &a, int nw, bool akc, bool bkc) {
+    return nw == 8 ? launch_layout<MB, 8>(st, a, akc, bkc) : launch_layout<MB, 4>(st, a, akc, bkc);
+}
+
+int env_value(const char *name) {
+    const char *v = getenv(name);
+    return v != nullptr ? atoi(v) : 0;
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+struct SmallPlan {
+    int mb, nw, splits;
+    int64_t wgs;  // work-groups without the k split
+};
+
+// Largest row block MB (<= 4, no larger than M needs) whose tiles, after dividing K over
+// at most 16 ranges of >= 2 k-groups per wavefront, give the 256 CUs a work-group each;
+// failing that MB = 1. A larger MB reads B fewer times (B is re-read once per 16*MB rows).
+SmallPlan plan_small(const GemmDesc &d) {
+    const int G = (int)cdiv(d.K, KG);
+    const int nw = G >= 16 ? 8 : 4;
+    const int mb_max = (int)(d.M > 48 ? 4 : cdiv(d.M, 16));
+    SmallPlan pl{1, nw, 1, 0};
+    for (int mb = mb_max; mb >= 1; --mb) {
+        const int64_t wgs = cdiv(d.M, 16 * mb) * cdiv(d.N, 16) * d.batch;
+        const int64_t need = cdiv(256, wgs);
+        int64_t cap = G / (2 * nw);
+        if (cap > 16) cap = 16;
+        if (cap < 1) cap = 1;
+        const int s = (int)(need < cap ? need : cap);
+        pl = SmallPlan{mb, nw, s, wgs};
+        if (wgs * s >= 256) break;
+    }
+    return pl;
+}
+
+}  // namespace
+
+// Chosen when C has fewer 64x64 tiles than CUs and K is at most 2048. Measured (graph
+// replay, us, small / tiled split-K): 256^3 3.3 / 8.2; 32 x 128x128x64 4.7 / 5.9; 64 x 4096
+// x 1536 15.6 / 19.0; at K = 4096 the tiled kernel wins: 64 x 1536 x 4096 23.8 / 18.9,
+// 128 x 4096 x 4096 64 / 49, 256 x 256 x 4096 13.4 / 13.1.
+bool small_preferred(const GemmDesc &d) {
+    const int64_t tiles64 = cdiv(d.M, 64) * cdiv(d.N, 64) * d.batch;
+    return tiles64 < 256 && d.K <= 2048;
+}
+
+int launch_gemm_small(hipStream_t stream, const GemmDesc &d) {
+    SmallPlan pl = plan_small(d);
+    static const int force_split = env_value("MIGEMM_SMALL_SPLITK");
+    if (force_split >= 1) pl.splits = force_split;
+
+    SmallArgs a;
+    a.A = d.A;
+    a.B = d.B;
+    a.bias = d.bias;
+    a.C = d.C;
+    a.lda = d.lda;
+    a.ldb = d.ldb;
+    a.ldc = d.ldc;
+    a.sA = d.sA;
+    a.sB = d.sB;
+    a.sC = d.sC;
+    a.M = d.M;
+    a.N = d.N;
+    a.K = d.K;
+    a.tiles_m = (int)cdiv(d.M, 16 * pl.mb);
+    a.tiles_n = (int)cdiv(d.N, 16);
+    a.batch = d.batch;
+    const int G = (int)cdiv(d.K, KG);
+    a.groups_per_split = (int)cdiv(G, pl.splits);
+    a.splits = (int)cdiv(G, a.groups_per_split);  // no empty range
+    const int64_t total = pl.wgs * a.splits;
+    if (total > 0x7fffffff)
+        return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm_small: %lld work-groups", (long long)total);
+    a.total = (int)total;
+    a.partial = nullptr;
+    if (a.splits > 1) {
+        int st = MIGEMM_OK;
+        a.partial = static_cast<float *>(
+            workspace((size_t)a.splits * d.batch * d.M * d.N * sizeof(float), &st));
+        if (a.partial == nullptr) return st;
+    }
+    const bool akc = !d.transA;
+    const bool bkc = d.transB;
+    int rc;
+    switch (pl.mb) {
+        case 4: rc = launch_nw<4>(stream, a, pl.nw, akc, bkc); break;
+        case 3: rc = launch_nw<3>(stream, a, pl.nw, akc, bkc); break;
+        case 2: rc = launch_nw<2>(stream, a, pl.nw, akc, bkc); break;
+        default: rc = launch_nw<1>(stream, a, pl.nw, akc, bkc); break;
+    }
+    if (rc != MIGEMM_OK || a.splits == 1) return rc;
+    return launch_reduce_slices(stream, a.partial, a.splits, d.batch, d.M, d.N, d.bias, d.C,
+                                d.ldc, d.sC);
+}
+
+}  // namespace migemm

@@ -38,6 +38,9 @@ struct GemmDesc {
 int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d);
 int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d);
 bool skinny_applicable(const GemmDesc &d);
+int launch_gemm_small(hipStream_t stream, const GemmDesc &d);
+// True when C has too few 64x64 tiles to occupy the 256 CUs (gemm_small_kernel).
+bool small_preferred(const GemmDesc &d);
 
 // Device workspace owned by the library (one growing buffer per device), used by
 // split-K partial sums. Returns nullptr and records MIGEMM_ERR_WORKSPACE on failure.

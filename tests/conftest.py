@@ -18,3 +18,15 @@ def nncl():
     from my_pytchon_opencl_lib_amd import NnClGlob
     assert torch.cuda.is_available(), "GPU test run without a visible GPU"
     return NnClGlob("cuda:0")
+
+
+POLICIES = {"auto": 0, "tiled": 1, "small": 2}
+
+
+@pytest.fixture(params=sorted(POLICIES))
+def policy(request):
+    """Runs a test once per kernel family (migemm_set_gemm_policy), restoring AUTO after."""
+    from my_pytchon_opencl_lib_amd import _native
+    prev = _native.set_gemm_policy(POLICIES[request.param])
+    yield request.param
+    _native.set_gemm_policy(prev)

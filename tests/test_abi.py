@@ -131,6 +131,17 @@ def test_services_validate_without_device(lib):
     assert lib.migemm_free(None) == 0
 
 
+def test_gemm_policy_set_and_rejected(lib):
+    prev = ctypes.c_int(-7)
+    assert lib.migemm_set_gemm_policy(2, ctypes.byref(prev)) == 0
+    assert prev.value == 0
+    assert lib.migemm_set_gemm_policy(0, ctypes.byref(prev)) == 0
+    assert prev.value == 2
+    expect(lib.migemm_set_gemm_policy(4, None), INVALID, "policy")
+    expect(lib.migemm_set_gemm_policy(-1, None), INVALID, "policy")
+    assert lib.migemm_set_gemm_policy(0, None) == 0
+
+
 def test_python_wrapper_maps_status_to_exceptions():
     with pytest.raises(_native.MigemmArgumentError):
         _native.call("migemm_bmm_tiled", NULL, P[0], P[1], P[2], 4, 0, 4, 16, 16, 16, 1)

@@ -66,8 +66,8 @@ SHAPES = [(1, 1, 1), (5, 7, 3), (17, 33, 5), (64, 128, 96), (127, 129, 65), (128
 
 @pytest.mark.parametrize("M,K,N", SHAPES)
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-def test_small_int_exact_all_layouts(nncl, M, K, N, ta, tb):
-    say("exact", M, K, N, "transA", ta, "transB", tb)
+def test_small_int_exact_all_layouts(nncl, policy, M, K, N, ta, tb):
+    say("exact", policy, M, K, N, "transA", ta, "transB", tb)
     A = small_ints((K, M) if ta else (M, K), M * 7 + K)
     B = small_ints((N, K) if tb else (K, N), N * 3 + K)
     Aop = A.T if ta else A
@@ -77,11 +77,11 @@ def test_small_int_exact_all_layouts(nncl, M, K, N, ta, tb):
     assert np.array_equal(got, expect)
 
 
-def test_probe_matrices_hit_every_edge(nncl):
+def test_probe_matrices_hit_every_edge(nncl, policy):
     """Single non-zero probes at tile boundaries of every tile size the dispatcher uses."""
     for (M, K, N) in [(1000, 777, 3000), (100, 70, 90), (33, 65, 130)]:
         for ta, tb in [(0, 0), (0, 1), (1, 0)]:
-            say("probe", M, K, N, ta, tb)
+            say("probe", policy, M, K, N, ta, tb)
             cases = list(itertools.product(
                 sorted({0, 31, 32, 63, 64, 127, 128, M - 1} & set(range(M))),
                 sorted({0, 7, 8, 31, 32, K - 1} & set(range(K))),
@@ -101,7 +101,7 @@ def test_probe_matrices_hit_every_edge(nncl):
 
 
 # --------------------------------------------------------------- output-boundary canary
-def test_writes_stay_inside_m_by_n(nncl):
+def test_writes_stay_inside_m_by_n(nncl, policy):
     """Pooled buffers may be larger than M*N (OpenCLBufferManager.cs:29-40): nothing
     outside C's [M x N] per batch entry may change."""
     M, K, N, batch = 70, 33, 45, 3
@@ -152,11 +152,11 @@ def test_broadcast_equals_per_batch_loop(nncl):
         assert np.array_equal(got[z], gemm_gpu(nncl, A[z], B[0]))
 
 
-def test_bias_epilogue_is_gemm_plus_row_add(nncl):
+def test_bias_epilogue_is_gemm_plus_row_add(nncl, policy):
     X = oracle.normal((2, 64, 1536), 2, 0)
     W = oracle.uniform((1, 1536, 4096), 2, 1, -1 / 32, 1 / 32)
     bias = oracle.uniform((4096,), 2, 2, -1 / 32, 1 / 32)
-    say("bias epilogue")
+    say("bias epilogue", policy)
     y = host(nncl.LinearForward(dev(X), dev(W), dev(bias)))
     plain = host(nncl.Bmm(dev(X), dev(W)))
     assert np.array_equal(y, (plain + bias).astype(np.float32))
@@ -239,12 +239,12 @@ def test_config5b_gemv(nncl):
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
-def test_skinny_rows_and_bias(nncl, M):
+def test_skinny_rows_and_bias(nncl, policy, M):
     K, N = 1000, 1030  # N not a multiple of 4 -> scalar loads; K not a slice multiple
     A = oracle.uniform((M, K), 6, M)
     B = oracle.uniform((K, N), 6, 10 + M)
     bias = oracle.uniform((N,), 6, 20 + M)
-    say("skinny", M)
+    say("skinny", policy, M)
     C = gemm_gpu(nncl, A, B, bias=bias)
     check_gemm(C, A, B, 0, 0, bias=bias, M=M, N=N, K=K, lda=K, ldb=N)
     At = np.ascontiguousarray(A.T)
@@ -284,7 +284,7 @@ def test_graph_capture_replays_match_eager(nncl):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-def test_unaligned_bases_and_leading_dims(nncl, ta, tb):
+def test_unaligned_bases_and_leading_dims(nncl, policy, ta, tb):
     """Operands that start 4 bytes past a 16-byte boundary with leading dimensions that
     are not multiples of 4 (128-bit loads from dword-aligned addresses)."""
     import ctypes
@@ -299,7 +299,7 @@ def test_unaligned_bases_and_leading_dims(nncl, ta, tb):
     bbuf[3:].reshape(B.shape[0], ldb)[:, :B.shape[1]] = B
     a, b = dev(abuf), dev(bbuf)
     c = torch.full((M, N), float("nan"), device="cuda:0")
-    say("unaligned", ta, tb)
+    say("unaligned", policy, ta, tb)
     _native.call("migemm_gemm_strided_batched",
                  ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), ta, tb, M, N, K,
                  ctypes.c_void_p(a.data_ptr() + 4), lda, 0, ctypes.c_void_p(b.data_ptr() + 12),
