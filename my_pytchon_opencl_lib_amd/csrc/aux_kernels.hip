@@ -65,27 +65,56 @@ __global__ void __launch_bounds__(256) transpose_kernel(const float *__restrict_
     }
 }
 
-// Y[o, i] = sum_{a ascending} X[(o*axis + a)*inner + i], one thread per output.
+// Sum over the middle axis of X[outer][axis][inner], in chunks of `rows` consecutive a:
+//   out[c][o][i] = sum over a in [c*rows, min((c+1)*rows, axis)), ascending from +0.0f,
+//                  of X[(o*axis + a)*inner + i].
+// The reference kernels (cs/cl_kernels/reduce_sum_axis.cl:3-27, linear.cl:149-168) run one
+// ascending chain per output over the whole axis: a single dependent chain per column,
+// which at 12000 rows leaves the GPU waiting on one load at a time. With one chunk (axis <=
+// rows) this is exactly the reference's order; otherwise the chunk sums are added in
+// chunk order by reduce_slices_kernel (deterministic, and within the blocked-summation
+// error bound (rows - 1 + chunks - 1) * 2^-24 * sum |x|). Each thread owns VW consecutive i
+// (128-bit loads when VW = 4) and keeps CS_INFLIGHT rows of loads in flight.
+constexpr int CS_INFLIGHT = 16;
+
+template <int VW>
 __global__ void __launch_bounds__(256) column_sum_kernel(const float *__restrict__ X,
-                                                           float *__restrict__ Y, int outer,
-                                                           int axis, int inner) {
+                                                           float *__restrict__ out, int outer,
+                                                           int axis, int inner, int rows) {
+    typedef float vec __attribute__((ext_vector_type(VW)));
+    const int vecs = (inner + VW - 1) / VW;
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= (int64_t)outer * inner) return;
-    const int64_t o = t / inner;
-    const int64_t i = t - o * inner;
-    const float *x = X + o * (int64_t)axis * inner + i;
-    float sum = 0.0f;
-    int a = 0;
-    for (; a + 4 <= axis; a += 4) {
-        const float x0 = x[(int64_t)a * inner], x1 = x[(int64_t)(a + 1) * inner];
-        const float x2 = x[(int64_t)(a + 2) * inner], x3 = x[(int64_t)(a + 3) * inner];
-        sum += x0;
-        sum += x1;
-        sum += x2;
-        sum += x3;
+    if (t >= (int64_t)outer * vecs) return;
+    const int o = (int)(t / vecs);
+    const int i0 = (int)(t - (int64_t)o * vecs) * VW;
+    const int cnt = inner - i0 < VW ? inner - i0 : VW;
+    const int c = blockIdx.y;
+    const int a0 = c * rows;
+    const int a1 = axis - a0 < rows ? axis : a0 + rows;
+    const float *x = X + ((int64_t)o * axis + a0) * inner + i0;
+    vec sum = {};
+    if (cnt == VW) {
+        for (int a = a0; a < a1; a += CS_INFLIGHT) {
+            vec v[CS_INFLIGHT];
+#pragma unroll
+            for (int g = 0; g < CS_INFLIGHT; ++g)
+                if (a + g < a1)
+                    __builtin_memcpy(&v[g], x + (int64_t)(a - a0 + g) * inner, sizeof(vec));
+#pragma unroll
+            for (int g = 0; g < CS_INFLIGHT; ++g)
+                if (a + g < a1) sum += v[g];
+        }
+    } else {
+        for (int e = 0; e < cnt; ++e) {
+            float s = 0.0f;
+            for (int a = a0; a < a1; ++a) s += x[(int64_t)(a - a0) * inner + e];
+            sum[e] = s;
+        }
     }
-    for (; a < axis; ++a) sum += x[(int64_t)a * inner];
-    Y[t] = sum;
+    float *y = out + ((int64_t)c * outer + o) * inner + i0;
+#pragma unroll
+    for (int e = 0; e < VW; ++e)
+        if (e < cnt) y[e] = sum[e];
 }
 
 }  // namespace
@@ -132,11 +161,30 @@ int launch_permute(hipStream_t stream, const float *src, float *dst, const int *
 
 int launch_column_sum(hipStream_t stream, const float *X, float *Y, int outer, int axis,
                       int inner) {
-    const int64_t outputs = (int64_t)outer * inner;
-    const int64_t blocks = (outputs + 255) / 256;
-    hipLaunchKernelGGL(column_sum_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, X, Y,
-                       outer, axis, inner);
-    return hip_check(hipGetLastError(), "column_sum_kernel launch");
+    // Chunks of 256 rows: 12000 x 6565 (the Linear(500 -> 6565) bias gradient) is 47 chunks
+    // of 7 work-groups, each thread with 16 rows of 128-bit loads in flight.
+    int rows = 256;
+    if ((axis + rows - 1) / rows > 65535) rows = (axis + 65534) / 65535;
+    const int chunks = (axis + rows - 1) / rows;
+    float *dst = Y;
+    if (chunks > 1) {
+        int st = MIGEMM_OK;
+        dst = static_cast<float *>(
+            workspace((size_t)chunks * outer * inner * sizeof(float), &st));
+        if (dst == nullptr) return st;
+    }
+    const bool vec = inner % 4 == 0;
+    const int64_t threads = (int64_t)outer * (vec ? inner / 4 : inner);
+    const dim3 grid((unsigned)((threads + 255) / 256), (unsigned)chunks);
+    if (vec)
+        hipLaunchKernelGGL(column_sum_kernel<4>, grid, dim3(256), 0, stream, X, dst, outer,
+                           axis, inner, rows);
+    else
+        hipLaunchKernelGGL(column_sum_kernel<1>, grid, dim3(256), 0, stream, X, dst, outer,
+                           axis, inner, rows);
+    const int rc = hip_check(hipGetLastError(), "column_sum_kernel launch");
+    if (rc != MIGEMM_OK || chunks == 1) return rc;
+    return launch_reduce_slices(stream, dst, chunks, outer, 1, inner, nullptr, Y, inner, inner);
 }
 
 }  // namespace migemm

@@ -35,6 +35,7 @@
 //    L2), then rastered in groups of 8 tile-rows so concurrently running tiles share
 //    A and B panels in that L2.
 #include <stdlib.h>
+#include <string.h>
 
 #include "migemm_internal.h"
 
@@ -548,8 +549,8 @@ int launch_reduce_slices(hipStream_t stream, const float *partial, int slices, i
 }
 
 namespace {
-// Tuning overrides (MIGEMM_TILE = 32 | 64 | 128, MIGEMM_SPLITK = S, MIGEMM_VARIANT,
-// MIGEMM_LDS_PAD), read once.
+// Tuning overrides (MIGEMM_TILE = 32 | 64 | 128 | 256, MIGEMM_SPLITK = S, MIGEMM_VARIANT,
+// MIGEMM_LDS_PAD).
 int env_int(const char *name) {
     const char *v = getenv(name);
     return v != nullptr ? atoi(v) : 0;
@@ -590,11 +591,20 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         return (int64_t)((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn) * d.batch;
     };
     const int nk32 = (d.K + 31) / 32;
-    // Largest tile that still gives the 256 CUs two work-groups each; otherwise 64x64
-    // tiles, split along K when K is long enough for every range to keep >= 4 k-tiles.
+    // Largest tile that still gives the 256 CUs two work-groups each. Below that, a long K
+    // (>= 4096) with M, N >= 128 keeps 128x128 tiles and splits K until there are >= 1024
+    // work-groups (an even number of ranges, at most 8). Otherwise 64x64 tiles, split along
+    // K when K is long enough for every range to keep >= 4 k-tiles. Measured (graph replay,
+    // us): the Linear(500 -> 6565) gradients dX 12000x500x6565 (NT) 128x128 / 4 ranges 664,
+    // 64x64 767; dW 500x6565x12000 (TN) 128x128 / 6 ranges 691, 64x64 916.
     int cfg, splits = 1;
     if (tiles(128, 128) >= 512) {
         cfg = 128;
+    } else if (d.K >= 4096 && d.M >= 128 && d.N >= 128) {
+        cfg = 128;
+        int64_t want = (1024 + tiles(128, 128) - 1) / tiles(128, 128);
+        want += want & 1;
+        splits = (int)(want < 8 ? want : 8);
     } else if (tiles(64, 64) >= 512 || nk32 < 8) {
         cfg = tiles(64, 64) >= 256 ? 64 : 32;
     } else {
@@ -605,23 +615,37 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         if (splits < 1) splits = 1;
     }
     // Large outputs: pick the macro-tile by the busiest CU's share of the work. The work-
-    // groups are dealt over the 256 CUs, so a CU carries ceil(tiles / 256) tiles; the
-    // factor is each shape's measured MFMA efficiency at 4096^3 (256x256: 143.8, 128x256:
-    // 141.1, 128x128: 138.9 TFLOP/s over NN / NT / TN).
+    // groups are dealt over the 256 CUs, so a CU carries ceil(tiles / 256) tiles of area x K
+    // multiply-adds; the factor is each shape's measured MFMA efficiency at 4096^3 (256x256:
+    // 143.8, 128x256: 141.1, 128x128: 138.9 TFLOP/s over NN / NT / TN). A 256x256 work-group
+    // fills its CU alone, so its prologue and epilogue (the C store) are not overlapped by
+    // another work-group: they cost about 32 k-steps' worth per tile (16 for 128x256, 2 per
+    // CU), which decides short K: 12000 x 6565 x 500 runs 729 us at 128x128, 747 at 256x256.
     int big = 0;  // 0: 128x128, 1: 128x256, 2: 256x256
-    if (cfg == 128) {
-        const double c0 = (double)((tiles(128, 128) + 255) / 256) * 16384.0 / 0.966;
-        const double c1 = (double)((tiles(128, 256) + 255) / 256) * 32768.0 / 0.981;
-        const double c2 = (double)((tiles(256, 256) + 255) / 256) * 65536.0 / 1.0;
+    if (cfg == 128 && splits == 1) {
+        const double k = d.K;
+        const double c0 = (double)((tiles(128, 128) + 255) / 256) * 16384.0 * k / 0.966;
+        const double c1 = (double)((tiles(128, 256) + 255) / 256) * 32768.0 * (k + 16) / 0.981;
+        const double c2 = (double)((tiles(256, 256) + 255) / 256) * 65536.0 * (k + 32);
         big = c2 <= c1 && c2 <= c0 ? 2 : (c1 <= c0 ? 1 : 0);
     }
-    static const int force_tile = env_int("MIGEMM_TILE");
-    static const int force_split = env_int("MIGEMM_SPLITK");
-    static const int variant = env_int("MIGEMM_VARIANT");
-    if (force_tile == 32 || force_tile == 64 || force_tile == 128) cfg = force_tile;
-    if (force_tile == 256) {
-        cfg = 128;
-        big = 2;
+    // read per call, so a tuning sweep can change them between calls in one process;
+    // MIGEMM_TILE = 32 | 64 | 128 | 128x256 | 256
+    const char *tile_env = getenv("MIGEMM_TILE");
+    const int force_split = env_int("MIGEMM_SPLITK");
+    const int variant = env_int("MIGEMM_VARIANT");
+    if (tile_env != nullptr) {
+        const int ft = atoi(tile_env);
+        if (strcmp(tile_env, "128x256") == 0) {
+            cfg = 128;
+            big = 1;
+        } else if (ft == 32 || ft == 64 || ft == 128) {
+            cfg = ft;
+            big = 0;
+        } else if (ft == 256) {
+            cfg = 128;
+            big = 2;
+        }
     }
     if (force_split >= 1) splits = force_split;
 

@@ -330,7 +330,7 @@ bool small_preferred(const GemmDesc &d) {
 
 int launch_gemm_small(hipStream_t stream, const GemmDesc &d) {
     SmallPlan pl = plan_small(d);
-    static const int force_split = env_value("MIGEMM_SMALL_SPLITK");
+    const int force_split = env_value("MIGEMM_SMALL_SPLITK");  // tuning, read per call
     if (force_split >= 1) pl.splits = force_split;
 
     SmallArgs a;

@@ -310,16 +310,48 @@ def test_unaligned_bases_and_leading_dims(nncl, policy, ta, tb):
     assert np.array_equal(host(c), expect)
 
 
-@pytest.mark.parametrize("M,K,N", [(2000, 50, 3980), (3000, 70, 2900), (4000, 50, 4090)])
+@pytest.fixture
+def forced_tile(request):
+    """Forces one macro-tile of the tiled kernel (the library's per-call MIGEMM_TILE tuning
+    override) under the TILED policy, restoring both afterwards."""
+    from my_pytchon_opencl_lib_amd import _native
+    prev_env = os.environ.get("MIGEMM_TILE")
+    prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_TILED)
+    os.environ["MIGEMM_TILE"] = request.param
+    yield request.param
+    if prev_env is None:
+        os.environ.pop("MIGEMM_TILE", None)
+    else:
+        os.environ["MIGEMM_TILE"] = prev_env
+    _native.set_gemm_policy(prev)
+
+
+@pytest.mark.parametrize("forced_tile", ["128", "128x256", "256"], indirect=True)
+@pytest.mark.parametrize("M,K,N", [(2000, 50, 3980), (3000, 70, 2900), (1000, 300, 1100)])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
-def test_large_tile_shapes_exact(nncl, M, K, N, ta, tb):
-    """Ragged shapes on which the dispatcher picks each large macro-tile (128x256,
-    128x128, 256x256), with a zero-filled K tail; exact small-integer products."""
-    say("large tiles exact", M, K, N, ta, tb)
+def test_large_tile_shapes_exact(nncl, forced_tile, M, K, N, ta, tb):
+    """Ragged shapes through each large macro-tile (128x128, 128x256, 256x256), with a
+    zero-filled K tail; exact small-integer products."""
+    say("large tiles exact", forced_tile, M, K, N, ta, tb)
     A = small_ints((K, M) if ta else (M, K), M + K)
     B = small_ints((N, K) if tb else (K, N), N + K)
     Aop = (A.T if ta else A).astype(np.float64)
     Bop = (B.T if tb else B).astype(np.float64)
     expect = (Aop @ Bop).astype(np.float32)  # exact: |sums| <= 16*K << 2^24
+    got = gemm_gpu(nncl, A, B, bool(ta), bool(tb))
+    assert np.array_equal(got, expect)
+
+
+@pytest.mark.parametrize("M,K,N", [(300, 5000, 200), (129, 4099, 131), (500, 12000, 700)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_long_k_split_tiles_exact(nncl, M, K, N, ta, tb):
+    """Long K with few 128x128 tiles: 128x128 tiles with K split into ranges (ragged M, N
+    and a K tail in the last range); exact small-integer products."""
+    say("long-K split exact", M, K, N, ta, tb)
+    A = small_ints((K, M) if ta else (M, K), M + 2 * K, -2, 2)
+    B = small_ints((N, K) if tb else (K, N), N + 2 * K, -2, 2)
+    Aop = (A.T if ta else A).astype(np.float64)
+    Bop = (B.T if tb else B).astype(np.float64)
+    expect = (Aop @ Bop).astype(np.float32)  # exact: |sums| <= 4*K << 2^24
     got = gemm_gpu(nncl, A, B, bool(ta), bool(tb))
     assert np.array_equal(got, expect)

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import oracle
-from parity import check_gemm, dev, host
+from parity import check_gemm, dev, host, sample_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -147,13 +147,75 @@ def test_permute_generic_and_transpose(nncl):
 
 
 def test_sum_and_bias_backward_bit_exact(nncl):
-    x = oracle.normal((4, 300, 37), 15, 0)
-    say("sum / bias backward")
+    """Up to 256 summed rows the library adds in the reference's order (one ascending
+    chain from +0.0f, reduce_sum_axis.cl:3-27, linear.cl:149-168): bit-identical."""
+    x = oracle.normal((4, 200, 37), 15, 0)
+    say("sum / bias backward, one chunk")
     for axis in (0, 1, 2):
         got = host(nncl.Sum(dev(x), axis, keepDims=True))
         assert np.array_equal(got, oracle.reduce_sum_axis(x, axis))
-    gb = host(nncl.LinearBiasBackward(dev(x), [37]))
-    assert np.array_equal(gb, oracle.linear_bias_backward(x))
+    gb = host(nncl.LinearBiasBackward(dev(x[:1]), [37]))
+    assert np.array_equal(gb, oracle.linear_bias_backward(x[:1]))
+
+
+def blocked_sum_bound(x2d, rows=256):
+    """Error bound of the chunked sum over axis 0 of x2d: (rows - 1 + chunks - 1) * u * sum|x|
+    (recursive summation within a chunk, then over the chunk sums; u = 2^-24)."""
+    n = x2d.shape[0]
+    chunks = -(-n // rows)
+    steps = min(n, rows) - 1 + chunks - 1
+    return steps * 2.0 ** -24 * np.abs(x2d.astype(np.float64)).sum(axis=0)
+
+
+@pytest.mark.parametrize("rows,N", [(12000, 6565), (1000, 37), (257, 512), (70000, 3)])
+def test_chunked_column_sum(nncl, rows, N):
+    """Longer axes are summed in 256-row chunks, combined in chunk order. Small integers make
+    every order exact (bit-identical to the reference's chain); random data stays within
+    the blocked-summation bound of the fp64 sum."""
+    say("chunked column sum", rows, N)
+    xi = small_int_matrix(rows, N, 17)
+    gb = host(nncl.LinearBiasBackward(dev(xi), [N]))
+    assert np.array_equal(gb, oracle.linear_bias_backward(xi))
+    x = oracle.normal((rows, N), 17, 1)
+    gb = host(nncl.LinearBiasBackward(dev(x), [N])).astype(np.float64)
+    ref = x.astype(np.float64).sum(axis=0)
+    assert np.all(np.abs(gb - ref) <= blocked_sum_bound(x))
+    got = host(nncl.Sum(dev(x.reshape(1, rows, N)), 1, keepDims=True)).reshape(N)
+    assert np.array_equal(got.astype(np.float64), gb)  # same kernel, same order
+
+
+def small_int_matrix(rows, N, seed):
+    rng = np.random.default_rng(seed)
+    return rng.integers(-8, 9, size=(rows, N)).astype(np.float32)
+
+
+def test_linear_500_to_6565_end_to_end(nncl):
+    """The largest real caller of the path: Linear(500 -> 6565) on [8, 1500, 500]
+    (cs/TestLSTMRealTrain/EncoderDecoder.cs:29,75): forward with the bias epilogue, then
+    LinearOp.Backward (cs/core/LinearOp.cs:16-49): dX = dY W^T (NT), dW = sum_b X_b^T dY_b
+    (one TN GEMM over 12000 rows), db = column sum of dY."""
+    from my_pytchon_opencl_lib_amd.autograd import LinearOp
+    batch, M, K, N = 8, 1500, 500, 6565
+    X = oracle.normal((batch, M, K), 18, 0)
+    W = oracle.uniform((1, K, N), 18, 1, -1 / 22, 1 / 22)
+    bias = oracle.uniform((N,), 18, 2, -1 / 22, 1 / 22)
+    G = oracle.normal((batch, M, N), 18, 3, 0.0, 1.0 / 64)
+    say("Linear(500->6565) forward")
+    y = nncl.LinearForward(dev(X), dev(W), dev(bias))
+    rows = sample_rows(M, 16)
+    check_gemm(host(y), X, W, 0, 0, bias=bias, M=M, N=N, K=K, lda=K, ldb=N, sA=M * K, sB=0,
+               batch=batch, rows=rows)
+    say("Linear(500->6565) backward")
+    node = LinearOp(dev(X), dev(W), dev(bias), y, nncl)
+    gX, gW, gb = [host(t) for t in node.Backward(dev(G))]
+    check_gemm(gX, G, W, 0, 1, M=M, N=K, K=N, lda=N, ldb=N, sA=M * N, sB=0, batch=batch,
+               rows=rows)
+    Xf = X.reshape(batch * M, K)
+    Gf = G.reshape(batch * M, N)
+    check_gemm(gW.reshape(K, N), Xf, Gf, 1, 0, M=K, N=N, K=batch * M, lda=K, ldb=N,
+               rows=sample_rows(K, 16))
+    ref = Gf.astype(np.float64).sum(axis=0)
+    assert np.all(np.abs(gb.astype(np.float64) - ref) <= blocked_sum_bound(Gf))
 
 
 def test_shape_errors_before_launch(nncl):
