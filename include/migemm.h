@@ -78,6 +78,18 @@ int migemm_gemm_strided_batched(void *stream, int transA, int transB,
                                 float *C, int64_t ldc, int64_t strideC,
                                 int batch);
 
+/* The same with flags. MIGEMM_GEMM_ACCUMULATE: C_b = C_b + (opA(A_b) * opB(B_b) + bias),
+ * the "+=" epilogue of the reference's gradient kernels (cs/cl_kernels/lstm.cl:546-560,
+ * 621-632: grad_W / grad_U = old value + tile sum). Other bits are rejected. */
+#define MIGEMM_GEMM_ACCUMULATE 1
+int migemm_gemm_strided_batched_ex(void *stream, int transA, int transB,
+                                   int M, int N, int K,
+                                   const float *A, int64_t lda, int64_t strideA,
+                                   const float *B, int64_t ldb, int64_t strideB,
+                                   const float *bias,
+                                   float *C, int64_t ldc, int64_t strideC,
+                                   int batch, int flags);
+
 /* ------------------------------------------------------------------------------- */
 /* (2) Reference-shaped entry points: same argument lists and meaning as the OpenCL
  *     kernels (plus the stream, and the batch count that the reference passes as the
@@ -120,6 +132,25 @@ int migemm_lstm_gemm_xw(void *stream, const float *X, const float *W,
                         const float *bias, float *XW_out,
                         int total_tokens, int in_features, int total_gates);
 
+/* Replaces kernel lstm_gemm_grad_x, cs/cl_kernels/lstm.cl:372-376, enqueued by
+ * NnClGlob.LstmBackward (cs/compiler/NnClGlob.cs:967-994):
+ * grad_X[T,F] = all_grad_gates[T,G] * W^T with W stored [F,G] (G = 4 * hidden). */
+int migemm_lstm_gemm_grad_x(void *stream, const float *all_grad_gates, const float *W,
+                            float *grad_X, int total_tokens, int in_features, int total_gates);
+
+/* Replaces kernel lstm_gemm_grad_weights, cs/cl_kernels/lstm.cl:459-468, enqueued by
+ * NnClGlob.LstmBackward (cs/compiler/NnClGlob.cs:996-1024). Tokens are ordered
+ * [batch_size][seq_len], T = batch_size * seq_len, G = 4 * hidden_size. Accumulates:
+ *   grad_W[F,G]  += X[T,F]^T * all_grad_gates[T,G]
+ *   grad_U[H,G]  += H_prev[T,H]^T * all_grad_gates, H_prev[t] = H_out[t-1] when
+ *                   t % seq_len > 0, else 0 (each sequence's first step has no h_{t-1})
+ *   grad_bias[G] += column sums of all_grad_gates
+ * The three outputs must not overlap each other or the inputs. */
+int migemm_lstm_gemm_grad_weights(void *stream, const float *X, const float *H_out,
+                                  const float *all_grad_gates, float *grad_W, float *grad_U,
+                                  float *grad_bias, int batch_size, int seq_len,
+                                  int in_features, int hidden_size);
+
 /* Replaces kernel tensor_permute, cl_kernels/permute.cl:11-18, enqueued by
  * NnClGlob.Permute (cs/compiler/NnClGlob.cs:382-424) and nncl_glob.py:148-174.
  * dst = src.permute(axes); src_dims and axes are HOST int arrays of length num_dims
@@ -130,13 +161,16 @@ int migemm_tensor_permute(void *stream, const float *src, float *dst,
 
 /* Replaces kernel linear_bias_backward, cs/cl_kernels/linear.cl:149-153, enqueued by
  * NnClGlob.LinearBiasBackward (cs/compiler/NnClGlob.cs:1557-1584):
- * grad_bias[n] = sum over r < total_rows of grad_output[r*N + n], r ascending. */
+ * grad_bias[n] = sum over r < total_rows of grad_output[r*N + n]. Summed r ascending
+ * within chunks of 256 rows, the chunk sums added in chunk order: the reference's single
+ * ascending chain (bit-identical) when total_rows <= 256, deterministic beyond. */
 int migemm_linear_bias_backward(void *stream, const float *grad_output, float *grad_bias,
                                 int total_rows, int N);
 
 /* Replaces kernel reduce_sum_axis, cs/cl_kernels/reduce_sum_axis.cl:3-8, enqueued by
  * NnClGlob.Sum (cs/compiler/NnClGlob.cs:1595-1664):
- * Y[o, i] = sum over a < axis_size of X[(o*axis_size + a)*inner_size + i], a ascending. */
+ * Y[o, i] = sum over a < axis_size of X[(o*axis_size + a)*inner_size + i], in the order
+ * of migemm_linear_bias_backward (the reference's ascending chain up to 256). */
 int migemm_reduce_sum_axis(void *stream, const float *X, float *Y,
                            int outer_size, int axis_size, int inner_size);
 

@@ -19,6 +19,8 @@ MIGEMM_ERR_NO_DEVICE = 4
 MIGEMM_ERR_WORKSPACE = 5
 MIGEMM_ERR_UNSUPPORTED = 6
 
+MIGEMM_GEMM_ACCUMULATE = 1  # migemm_gemm_strided_batched_ex flag: C += result
+
 # Kernel-family policies (migemm_set_gemm_policy)
 MIGEMM_POLICY_AUTO = 0
 MIGEMM_POLICY_TILED = 1
@@ -64,11 +66,16 @@ _ip = ctypes.POINTER(ctypes.c_int)
 SIGNATURES = {
     "migemm_gemm_strided_batched": ([_vp, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _vp,
                                      _i64, _i64, _vp, _vp, _i64, _i64, _i32], _i32),
+    "migemm_gemm_strided_batched_ex": ([_vp, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64,
+                                        _vp, _i64, _i64, _vp, _vp, _i64, _i64, _i32, _i32],
+                                       _i32),
     "migemm_matmul_tiled": ([_vp, _vp, _vp, _vp, _i32, _i32, _i32], _i32),
     "migemm_bmm_tiled": ([_vp, _vp, _vp, _vp] + [_i32] * 7, _i32),
     "migemm_bmm_permute_tiled": ([_vp, _vp, _vp, _vp] + [_i32] * 9, _i32),
     "migemm_linear_forward": ([_vp, _vp, _vp, _vp, _vp] + [_i32] * 6, _i32),
     "migemm_lstm_gemm_xw": ([_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32], _i32),
+    "migemm_lstm_gemm_grad_x": ([_vp, _vp, _vp, _vp, _i32, _i32, _i32], _i32),
+    "migemm_lstm_gemm_grad_weights": ([_vp] * 7 + [_i32] * 4, _i32),
     "migemm_tensor_permute": ([_vp, _vp, _vp, _ip, _ip, _i32], _i32),
     "migemm_linear_bias_backward": ([_vp, _vp, _vp, _i32, _i32], _i32),
     "migemm_reduce_sum_axis": ([_vp, _vp, _vp, _i32, _i32, _i32], _i32),

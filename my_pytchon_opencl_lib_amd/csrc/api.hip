@@ -71,20 +71,25 @@ int hip_check(hipError_t e, const char *what) {
     return set_error(MIGEMM_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-// One growing buffer per device. A buffer that is outgrown is retired, not freed: work
-// already queued, or a HIP graph captured earlier, may still refer to it, so retired
+// One growing buffer per device and slot. A buffer that is outgrown is retired, not freed:
+// work already queued, or a HIP graph captured earlier, may still refer to it, so retired
 // buffers live until the process ends. Calls that use the workspace must be ordered on
 // one stream (they share the buffer).
-void *workspace(size_t bytes, int *status) {
+void *workspace(size_t bytes, int *status, int slot) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) {
         *status = hip_check(e, "hipGetDevice");
         return nullptr;
     }
+    if (slot < 0 || slot >= kWorkspaceSlots) {
+        *status = set_error(MIGEMM_ERR_WORKSPACE, "workspace slot %d", slot);
+        return nullptr;
+    }
     std::lock_guard<std::mutex> lock(g_ws_mutex);
-    if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
-    DeviceWorkspace &w = g_ws[dev];
+    if ((int)g_ws.size() <= dev * kWorkspaceSlots + slot)
+        g_ws.resize((dev + 1) * kWorkspaceSlots);
+    DeviceWorkspace &w = g_ws[dev * kWorkspaceSlots + slot];
     if (w.bytes < bytes) {
         size_t want = bytes < ((size_t)8 << 20) ? ((size_t)8 << 20) : bytes;
         if (want < 2 * w.bytes) want = 2 * w.bytes;
@@ -154,6 +159,7 @@ static int validate_gemm(int transA, int transB, int M, int N, int K, const floa
     d->batch = batch;
     d->transA = transA != 0;
     d->transB = transB != 0;
+    d->accumulate = false;
     return MIGEMM_OK;
 }
 
@@ -186,6 +192,21 @@ int migemm_gemm_strided_batched(void *stream, int transA, int transB, int M, int
     int rc = validate_gemm(transA, transB, M, N, K, A, lda, strideA, B, ldb, strideB, bias, C,
                            ldc, strideC, batch, &d);
     if (rc != MIGEMM_OK) return rc;
+    return run_gemm(static_cast<hipStream_t>(stream), d);
+}
+
+int migemm_gemm_strided_batched_ex(void *stream, int transA, int transB, int M, int N, int K,
+                                   const float *A, int64_t lda, int64_t strideA, const float *B,
+                                   int64_t ldb, int64_t strideB, const float *bias, float *C,
+                                   int64_t ldc, int64_t strideC, int batch, int flags) {
+    clear_error();
+    if ((flags & ~MIGEMM_GEMM_ACCUMULATE) != 0)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "gemm_ex: unknown flags 0x%x", flags);
+    GemmDesc d;
+    int rc = validate_gemm(transA, transB, M, N, K, A, lda, strideA, B, ldb, strideB, bias, C,
+                           ldc, strideC, batch, &d);
+    if (rc != MIGEMM_OK) return rc;
+    d.accumulate = (flags & MIGEMM_GEMM_ACCUMULATE) != 0;
     return run_gemm(static_cast<hipStream_t>(stream), d);
 }
 
@@ -244,6 +265,75 @@ int migemm_lstm_gemm_xw(void *stream, const float *X, const float *W, const floa
     return migemm_gemm_strided_batched(stream, 0, 0, total_tokens, total_gates, in_features, X,
                                        in_features, 0, W, total_gates, 0, bias, XW_out,
                                        total_gates, 0, 1);
+}
+
+int migemm_lstm_gemm_grad_x(void *stream, const float *all_grad_gates, const float *W,
+                            float *grad_X, int total_tokens, int in_features, int total_gates) {
+    clear_error();
+    // grad_X[T, F] = G[T, 4H] * W^T, W stored [F, 4H] (B transposed: element (k, f) at
+    // W[f * total_gates + k]).
+    return migemm_gemm_strided_batched(stream, 0, 1, total_tokens, in_features, total_gates,
+                                       all_grad_gates, total_gates, 0, W, total_gates, 0,
+                                       nullptr, grad_X, in_features, 0, 1);
+}
+
+int migemm_lstm_gemm_grad_weights(void *stream, const float *X, const float *H_out,
+                                  const float *all_grad_gates, float *grad_W, float *grad_U,
+                                  float *grad_bias, int batch_size, int seq_len,
+                                  int in_features, int hidden_size) {
+    clear_error();
+    if (X == nullptr || H_out == nullptr || all_grad_gates == nullptr || grad_W == nullptr ||
+        grad_U == nullptr || grad_bias == nullptr)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "lstm_gemm_grad_weights: null pointer argument");
+    if (batch_size < 1 || seq_len < 1 || in_features < 1 || hidden_size < 1)
+        return set_error(MIGEMM_ERR_INVALID_ARG,
+                         "lstm_gemm_grad_weights: sizes must be >= 1 (batch=%d seq=%d in=%d "
+                         "hidden=%d)",
+                         batch_size, seq_len, in_features, hidden_size);
+    const int64_t tokens = (int64_t)batch_size * seq_len;
+    const int64_t gates = (int64_t)4 * hidden_size;
+    if (tokens > INT32_MAX || gates > INT32_MAX)
+        return set_error(MIGEMM_ERR_INVALID_ARG,
+                         "lstm_gemm_grad_weights: batch*seq or 4*hidden exceeds 2^31-1");
+    const int T = (int)tokens, G = (int)gates;
+    // the three accumulated outputs must be disjoint from each other and from the inputs
+    const struct {
+        const void *p;
+        int64_t n;
+    } out[3] = {{grad_W, (int64_t)in_features * G},
+                {grad_U, (int64_t)hidden_size * G},
+                {grad_bias, G}},
+      in[3] = {{X, tokens * in_features}, {H_out, tokens * hidden_size}, {all_grad_gates, tokens * G}};
+    for (int i = 0; i < 3; ++i) {
+        for (int j = 0; j < 3; ++j)
+            if (ranges_overlap(out[i].p, out[i].n, in[j].p, in[j].n))
+                return set_error(MIGEMM_ERR_ALIAS,
+                                 "lstm_gemm_grad_weights: an output overlaps an input");
+        for (int j = i + 1; j < 3; ++j)
+            if (ranges_overlap(out[i].p, out[i].n, out[j].p, out[j].n))
+                return set_error(MIGEMM_ERR_ALIAS, "lstm_gemm_grad_weights: outputs overlap");
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // grad_W[F, 4H] += X^T * G (A transposed: X is stored [T, F])
+    int rc = migemm_gemm_strided_batched_ex(stream, 1, 0, in_features, G, T, X, in_features, 0,
+                                            all_grad_gates, G, 0, nullptr, grad_W, G, 0, 1,
+                                            MIGEMM_GEMM_ACCUMULATE);
+    if (rc != MIGEMM_OK) return rc;
+    // grad_bias[4H] += column sums of G
+    rc = launch_column_sum(st, all_grad_gates, grad_bias, 1, T, G, true);
+    if (rc != MIGEMM_OK) return rc;
+    // grad_U[H, 4H] += H_prev^T * G; H_prev is zero at every sequence's first step, so a
+    // single-step sequence adds nothing
+    if (seq_len == 1) return MIGEMM_OK;
+    int st_ws = MIGEMM_OK;
+    float *hprev = static_cast<float *>(
+        workspace((size_t)tokens * hidden_size * sizeof(float), &st_ws, 1));
+    if (hprev == nullptr) return st_ws;
+    rc = launch_shift_rows(st, H_out, hprev, T, seq_len, hidden_size);
+    if (rc != MIGEMM_OK) return rc;
+    return migemm_gemm_strided_batched_ex(stream, 1, 0, hidden_size, G, T, hprev, hidden_size, 0,
+                                          all_grad_gates, G, 0, nullptr, grad_U, G, 0, 1,
+                                          MIGEMM_GEMM_ACCUMULATE);
 }
 
 int migemm_linear_weight_grad(void *stream, const float *X, const float *dY, float *dW, int M,

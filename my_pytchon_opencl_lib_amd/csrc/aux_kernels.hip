@@ -74,13 +74,15 @@ __global__ void __launch_bounds__(256) transpose_kernel(const float *__restrict_
 // rows) this is exactly the reference's order; otherwise the chunk sums are added in
 // chunk order by reduce_slices_kernel (deterministic, and within the blocked-summation
 // error bound (rows - 1 + chunks - 1) * 2^-24 * sum |x|). Each thread owns VW consecutive i
-// (128-bit loads when VW = 4) and keeps CS_INFLIGHT rows of loads in flight.
+// (128-bit loads when VW = 4) and keeps CS_INFLIGHT rows of loads in flight. With
+// `accumulate` (one chunk only) the sum is added to the output's value: out += sum.
 constexpr int CS_INFLIGHT = 16;
 
 template <int VW>
 __global__ void __launch_bounds__(256) column_sum_kernel(const float *__restrict__ X,
                                                            float *__restrict__ out, int outer,
-                                                           int axis, int inner, int rows) {
+                                                           int axis, int inner, int rows,
+                                                           int accumulate) {
     typedef float vec __attribute__((ext_vector_type(VW)));
     const int vecs = (inner + VW - 1) / VW;
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -114,7 +116,27 @@ __global__ void __launch_bounds__(256) column_sum_kernel(const float *__restrict
     float *y = out + ((int64_t)c * outer + o) * inner + i0;
 #pragma unroll
     for (int e = 0; e < VW; ++e)
-        if (e < cnt) y[e] = sum[e];
+        if (e < cnt) y[e] = accumulate ? y[e] + sum[e] : sum[e];
+}
+
+// Hp[t][h] = H[t - 1][h] when step t % seq_len > 0 of its sequence, else 0: the previous
+// hidden state of the same sequence, the left operand of grad_U += H_prev^T * grad_gates
+// (cs/cl_kernels/lstm.cl:582-590, tokens ordered [batch][seq_len]). VW consecutive h per
+// thread (hidden % VW == 0).
+template <int VW>
+__global__ void __launch_bounds__(256) shift_rows_kernel(const float *__restrict__ H,
+                                                           float *__restrict__ Hp,
+                                                           int64_t total, int seq_len,
+                                                           int hidden) {
+    typedef float vec __attribute__((ext_vector_type(VW)));
+    const int64_t step = (int64_t)gridDim.x * blockDim.x * VW;
+    for (int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * VW; i < total;
+         i += step) {
+        const int64_t t = i / hidden;
+        vec v = {};
+        if (t % seq_len != 0) __builtin_memcpy(&v, H + i - hidden, sizeof(vec));
+        __builtin_memcpy(Hp + i, &v, sizeof(vec));
+    }
 }
 
 }  // namespace
@@ -160,7 +182,7 @@ int launch_permute(hipStream_t stream, const float *src, float *dst, const int *
 }
 
 int launch_column_sum(hipStream_t stream, const float *X, float *Y, int outer, int axis,
-                      int inner) {
+                      int inner, bool accumulate) {
     // Chunks of 256 rows: 12000 x 6565 (the Linear(500 -> 6565) bias gradient) is 47 chunks
     // of 7 work-groups, each thread with 16 rows of 128-bit loads in flight.
     int rows = 256;
@@ -178,13 +200,29 @@ int launch_column_sum(hipStream_t stream, const float *X, float *Y, int outer, i
     const dim3 grid((unsigned)((threads + 255) / 256), (unsigned)chunks);
     if (vec)
         hipLaunchKernelGGL(column_sum_kernel<4>, grid, dim3(256), 0, stream, X, dst, outer,
-                           axis, inner, rows);
+                           axis, inner, rows, (int)(accumulate && chunks == 1));
     else
         hipLaunchKernelGGL(column_sum_kernel<1>, grid, dim3(256), 0, stream, X, dst, outer,
-                           axis, inner, rows);
+                           axis, inner, rows, (int)(accumulate && chunks == 1));
     const int rc = hip_check(hipGetLastError(), "column_sum_kernel launch");
     if (rc != MIGEMM_OK || chunks == 1) return rc;
-    return launch_reduce_slices(stream, dst, chunks, outer, 1, inner, nullptr, Y, inner, inner);
+    return launch_reduce_slices(stream, dst, chunks, outer, 1, inner, nullptr, Y, inner, inner,
+                                accumulate);
+}
+
+int launch_shift_rows(hipStream_t stream, const float *H, float *Hp, int total_tokens,
+                      int seq_len, int hidden) {
+    const int64_t total = (int64_t)total_tokens * hidden;
+    const bool vec = hidden % 4 == 0;
+    int64_t blocks = ((vec ? total / 4 : total) + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (vec)
+        hipLaunchKernelGGL(shift_rows_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream, H,
+                           Hp, total, seq_len, hidden);
+    else
+        hipLaunchKernelGGL(shift_rows_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream, H,
+                           Hp, total, seq_len, hidden);
+    return hip_check(hipGetLastError(), "shift_rows_kernel launch");
 }
 
 }  // namespace migemm

@@ -37,6 +37,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "migemm_internal.h"
 
 namespace migemm {
@@ -59,6 +61,7 @@ struct TiledArgs {
     int splits;            // split-K ranges (1 = no split)
     int kt_per_split;      // k-tiles per range
     float *partial;        // [splits][batch][M][N] partial sums when splits > 1
+    int accumulate;        // C += result instead of C = result
 };
 
 constexpr int PAD_K = 4;  // pad of a K-contiguous LDS tile row [i][BK + 4]
@@ -392,25 +395,37 @@ gemm_mfma_kernel(TiledArgs p) {
         return;
     }
     float *Cb = p.C + (int64_t)b * p.sC;
+    // Two copies of the store loop behind a uniform branch, so the plain store never
+    // carries a (speculated) load of C.
+    auto store = [&](auto accumulate) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-        const int col = n0 + wn * WTN + j * 32 + lo;
-        const bool cok = col < p.N;
-        float bv = 0.f;
-        if (p.bias != nullptr && cok) bv = p.bias[col];
+        for (int j = 0; j < FN; ++j) {
+            const int col = n0 + wn * WTN + j * 32 + lo;
+            const bool cok = col < p.N;
+            float bv = 0.f;
+            if (p.bias != nullptr && cok) bv = p.bias[col];
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
+            for (int i = 0; i < FM; ++i) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
-                if (cok && row < p.M) {
-                    float v = acc[i][j][r];
-                    if (p.bias != nullptr) v = v + bv;
-                    Cb[(int64_t)row * p.ldc + col] = v;
+                for (int r = 0; r < 16; ++r) {
+                    const int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+                    if (cok && row < p.M) {
+                        float v = acc[i][j][r];
+                        if (p.bias != nullptr) v = v + bv;
+                        float *c = Cb + (int64_t)row * p.ldc + col;
+                        if constexpr (decltype(accumulate)::value)
+                            *c = *c + v;
+                        else
+                            *c = v;
+                    }
                 }
             }
         }
-    }
+    };
+    if (p.accumulate)
+        store(std::true_type{});
+    else
+        store(std::false_type{});
 }
 
 // C_b[m, n] = partial[0][b][m][n] + ... + partial[S-1][b][m][n] (+ bias[n]), added in
@@ -425,7 +440,7 @@ template <int VW>
 __global__ void __launch_bounds__(256)
 reduce_slices_kernel(const float *__restrict__ partial, int slices, int batch, int M, int N,
                      const float *__restrict__ bias, float *__restrict__ C, int64_t ldc,
-                     int64_t strideC) {
+                     int64_t strideC, int accumulate) {
     typedef float vec __attribute__((ext_vector_type(VW)));
     const int64_t total = (int64_t)batch * M * N;
     const int64_t nvec = (total + VW - 1) / VW;
@@ -462,7 +477,8 @@ reduce_slices_kernel(const float *__restrict__ partial, int slices, int batch, i
                 const int m = (int)(row - b * M);
                 float o = v[e];
                 if (bias != nullptr) o = o + bias[n];
-                C[b * strideC + (int64_t)m * ldc + n] = o;
+                float *c = C + b * strideC + (int64_t)m * ldc + n;
+                *c = accumulate ? *c + o : o;
             }
             if (++n == N) {
                 n = 0;
@@ -533,7 +549,7 @@ int launch_tiles(hipStream_t s, TiledArgs &a, bool akc, bool bkc, bool av, bool 
 
 int launch_reduce_slices(hipStream_t stream, const float *partial, int slices, int batch,
                          int M, int N, const float *bias, float *C, int64_t ldc,
-                         int64_t strideC) {
+                         int64_t strideC, bool accumulate) {
     const int64_t total = (int64_t)batch * M * N;
     // 4 outputs per thread once that still gives every CU a work-group
     const bool wide = total >= 4 * 256 * 256;
@@ -541,10 +557,10 @@ int launch_reduce_slices(hipStream_t stream, const float *partial, int slices, i
     if (blocks > 16384) blocks = 16384;
     if (wide)
         hipLaunchKernelGGL(reduce_slices_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream,
-                           partial, slices, batch, M, N, bias, C, ldc, strideC);
+                           partial, slices, batch, M, N, bias, C, ldc, strideC, (int)accumulate);
     else
         hipLaunchKernelGGL(reduce_slices_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream,
-                           partial, slices, batch, M, N, bias, C, ldc, strideC);
+                           partial, slices, batch, M, N, bias, C, ldc, strideC, (int)accumulate);
     return hip_check(hipGetLastError(), "reduce_slices_kernel launch");
 }
 
@@ -586,6 +602,7 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     a.N = d.N;
     a.K = d.K;
     a.batch = d.batch;
+    a.accumulate = d.accumulate;
 
     auto tiles = [&](int bm, int bn) {
         return (int64_t)((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn) * d.batch;
@@ -692,7 +709,7 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     splits = a.splits;
     if (rc != MIGEMM_OK || splits == 1) return rc;
     return launch_reduce_slices(stream, a.partial, splits, d.batch, d.M, d.N, d.bias, d.C,
-                                d.ldc, d.sC);
+                                d.ldc, d.sC, d.accumulate);
 }
 
 }  // namespace migemm

@@ -43,6 +43,7 @@ struct SkinnyArgs {
     int cblocks;   // ceil(N / 256)
     float *partial;  // [slices][batch][M][N] when slices > 1
     int batch;
+    int accumulate;  // C += result instead of C = result
 };
 
 template <int MR, bool VEC, bool NTL>
@@ -129,7 +130,7 @@ __global__ void __launch_bounds__(SK_THREADS) gemm_skinny_kernel(SkinnyArgs p) {
                     if (n + e < p.N) {
                         float v = tot[m][e];
                         if (p.bias != nullptr) v = v + p.bias[n + e];
-                        crow[n + e] = v;
+                        crow[n + e] = p.accumulate ? crow[n + e] + v : v;
                     }
                 }
             }
@@ -208,6 +209,7 @@ int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {
     }
     a.partial = nullptr;
     a.batch = d.batch;
+    a.accumulate = d.accumulate;
     if (a.slices > 1) {
         const size_t part_bytes = (size_t)a.slices * d.batch * d.M * d.N * sizeof(float);
         int st = MIGEMM_OK;
@@ -226,7 +228,7 @@ int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {
     }
     if (rc != MIGEMM_OK || a.slices == 1) return rc;
     return launch_reduce_slices(stream, a.partial, a.slices, d.batch, d.M, d.N, d.bias, d.C,
-                                d.ldc, d.sC);
+                                d.ldc, d.sC, d.accumulate);
 }
 
 }  // namespace migemm

@@ -50,6 +50,7 @@ struct SmallArgs {
     int splits;            // k ranges over work-groups (1 = none)
     int groups_per_split;  // 16-wide k-groups per range
     float *partial;        // [splits][batch][M][N] when splits > 1
+    int accumulate;        // C += result instead of C = result
 };
 
 constexpr int KG = 16;       // k values per k-group (4 MFMA steps of 4)
@@ -257,7 +258,8 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(SmallArgs p) {
         if (m < p.M && n < p.N) {
             if (p.splits == 1) {
                 if (p.bias != nullptr) v = v + p.bias[n];
-                p.C[(int64_t)b * p.sC + (int64_t)m * p.ldc + n] = v;
+                float *c = p.C + (int64_t)b * p.sC + (int64_t)m * p.ldc + n;
+                *c = p.accumulate ? *c + v : v;
             } else {
                 p.partial[(((int64_t)split * p.batch + b) * p.M + m) * p.N + n] = v;
             }
@@ -347,6 +349,7 @@ int launch_gemm_small(hipStream_t stream, const GemmDesc &d) {
     a.M = d.M;
     a.N = d.N;
     a.K = d.K;
+    a.accumulate = d.accumulate;
     a.tiles_m = (int)cdiv(d.M, 16 * pl.mb);
     a.tiles_n = (int)cdiv(d.N, 16);
     a.batch = d.batch;
@@ -375,7 +378,7 @@ int launch_gemm_small(hipStream_t stream, const GemmDesc &d) {
     }
     if (rc != MIGEMM_OK || a.splits == 1) return rc;
     return launch_reduce_slices(stream, a.partial, a.splits, d.batch, d.M, d.N, d.bias, d.C,
-                                d.ldc, d.sC);
+                                d.ldc, d.sC, d.accumulate);
 }
 
 }  // namespace migemm

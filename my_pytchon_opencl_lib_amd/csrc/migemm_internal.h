@@ -32,6 +32,7 @@ struct GemmDesc {
     int64_t sA, sB, sC;
     int M, N, K, batch;
     bool transA, transB;
+    bool accumulate;  // C = C + (op(A) op(B) + bias) instead of C = op(A) op(B) + bias
 };
 
 // Launchers. They assume a validated descriptor and only enqueue work.
@@ -42,18 +43,27 @@ int launch_gemm_small(hipStream_t stream, const GemmDesc &d);
 // True when C has too few 64x64 tiles to occupy the 256 CUs (gemm_small_kernel).
 bool small_preferred(const GemmDesc &d);
 
-// Device workspace owned by the library (one growing buffer per device), used by
-// split-K partial sums. Returns nullptr and records MIGEMM_ERR_WORKSPACE on failure.
-void *workspace(size_t bytes, int *status);
+// Device workspace owned by the library: one growing buffer per device and slot. Slot 0
+// holds split-K partial sums (GEMM, column sums); slot 1 holds operands staged by an entry
+// point for the GEMMs it then runs (which may use slot 0). Returns nullptr and records
+// MIGEMM_ERR_WORKSPACE on failure.
+constexpr int kWorkspaceSlots = 2;
+void *workspace(size_t bytes, int *status, int slot = 0);
 
-// C_b[m, n] = sum over s = 0..S-1 (in order) of partial[s][b][m][n] (+ bias[n]).
+// C_b[m, n] = sum over s = 0..S-1 (in order) of partial[s][b][m][n] (+ bias[n]); with
+// `accumulate`, C_b[m, n] += that value.
 int launch_reduce_slices(hipStream_t stream, const float *partial, int slices, int batch,
                          int M, int N, const float *bias, float *C, int64_t ldc,
-                         int64_t strideC);
+                         int64_t strideC, bool accumulate = false);
 
 int launch_permute(hipStream_t stream, const float *src, float *dst,
                    const int *src_dims, const int *axes, int num_dims, int64_t total);
+// Y[o, i] (+)= sum over a of X[o][a][i] (accumulate: Y += sum).
 int launch_column_sum(hipStream_t stream, const float *X, float *Y,
-                      int outer, int axis, int inner);
+                      int outer, int axis, int inner, bool accumulate = false);
+
+// Hp[t] = H[t - 1] when t % seq_len > 0, else 0 (rows of `hidden` floats).
+int launch_shift_rows(hipStream_t stream, const float *H, float *Hp, int total_tokens,
+                      int seq_len, int hidden);
 
 }  // namespace migemm

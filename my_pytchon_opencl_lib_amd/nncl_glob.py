@@ -149,6 +149,61 @@ class NnClGlob:
                      _ptr(gb), rows, n)
         return gb
 
+    # ---- LSTM GEMM stages (NnClGlob.Lstm / LstmBackward, cs/compiler/NnClGlob.cs:850-1061).
+    # The recurrent kernels between them (lstm_recurrent_forward / _backward) are not part
+    # of the matmul path; these are the three GEMM launches of those two methods.
+    def LstmGemmXW(self, x, w, bias):
+        """XW[T, 4H] = x[B, S, F] (as [T, F]) @ w[F, 4H] + bias[4H]: stage 1 of NnClGlob.Lstm
+        (NnClGlob.cs:877-899, lstm_gemm_xw lstm.cl:273-367)."""
+        _check_tensor("x", x)
+        _check_tensor("w", w)
+        _check_tensor("bias", bias)
+        f = x.shape[-1]
+        t = x.numel() // f
+        _require(w.dim() == 2 and w.shape[0] == f, f"w must be [{f}, 4*hidden] (got {list(w.shape)})")
+        g = w.shape[1]
+        _require(bias.numel() == g, f"bias must have {g} elements (got {bias.numel()})")
+        xw = torch.empty((t, g), dtype=torch.float32, device=x.device)
+        _native.call("migemm_lstm_gemm_xw", _stream(x), _ptr(x), _ptr(w), _ptr(bias), _ptr(xw),
+                     t, f, g)
+        return xw
+
+    def LstmGemmGradX(self, allGradGates, w, xShape):
+        """grad_X (shape xShape) = allGradGates[T, 4H] @ w[F, 4H]^T: stage 2 of
+        NnClGlob.LstmBackward (NnClGlob.cs:967-994, lstm_gemm_grad_x lstm.cl:372-457)."""
+        _check_tensor("allGradGates", allGradGates)
+        _check_tensor("w", w)
+        _require(w.dim() == 2, f"w must be [in_features, 4*hidden] (got {list(w.shape)})")
+        f, g = w.shape
+        _require(allGradGates.shape[-1] == g,
+                 f"allGradGates must end in {g} gates (got {list(allGradGates.shape)})")
+        t = allGradGates.numel() // g
+        gx = torch.empty(list(xShape), dtype=torch.float32, device=w.device)
+        _require(gx.numel() == t * f, f"xShape {list(xShape)} does not hold [{t}, {f}]")
+        _native.call("migemm_lstm_gemm_grad_x", _stream(w), _ptr(allGradGates), _ptr(w),
+                     _ptr(gx), t, f, g)
+        return gx
+
+    def LstmGemmGradWeights(self, x, hOut, allGradGates, gradW, gradU, gradBias):
+        """Stage 3 of NnClGlob.LstmBackward (NnClGlob.cs:996-1024, lstm_gemm_grad_weights
+        lstm.cl:459-636), accumulating in place like w.Grad / u.Grad / bias.Grad there:
+        gradW += X^T G, gradU += H_prev^T G (h_{t-1} of the same sequence, 0 at its first
+        step), gradBias += sum over tokens of G. x is [B, S, F], hOut [B, S, H]."""
+        for name, t in (("x", x), ("hOut", hOut), ("allGradGates", allGradGates),
+                        ("gradW", gradW), ("gradU", gradU), ("gradBias", gradBias)):
+            _check_tensor(name, t)
+        _require(x.dim() == 3 and hOut.dim() == 3, "x and hOut must be [Batch, Seq, *]")
+        b, s_, f = x.shape
+        h = hOut.shape[2]
+        _require(hOut.shape[0] == b and hOut.shape[1] == s_, "x and hOut batch/seq differ")
+        _require(allGradGates.numel() == b * s_ * 4 * h, "allGradGates must be [B*S, 4*hidden]")
+        _require(gradW.numel() == f * 4 * h, f"gradW must hold [{f}, {4 * h}]")
+        _require(gradU.numel() == h * 4 * h, f"gradU must hold [{h}, {4 * h}]")
+        _require(gradBias.numel() == 4 * h, f"gradBias must hold {4 * h} values")
+        _native.call("migemm_lstm_gemm_grad_weights", _stream(x), _ptr(x), _ptr(hOut),
+                     _ptr(allGradGates), _ptr(gradW), _ptr(gradU), _ptr(gradBias), b, s_, f, h)
+        return gradW, gradU, gradBias
+
     def Sum(self, x, axis, keepDims=False):
         """Sum over one axis, ascending order (NnClGlob.cs:1595-1664)."""
         _check_tensor("x", x)

@@ -49,6 +49,8 @@ def lib():
         L.oracle_bmm_permute_tiled.argtypes = [f, f, f] + [i32] * 9
         L.oracle_linear_forward_tiled.argtypes = [f, f, f, f] + [i32] * 6
         L.oracle_lstm_gemm_xw.argtypes = [f, f, f, f, i32, i32, i32]
+        L.oracle_lstm_gemm_grad_x.argtypes = [f, f, f, i32, i32, i32]
+        L.oracle_lstm_gemm_grad_weights.argtypes = [f] * 6 + [i32] * 4
         L.oracle_tensor_permute.argtypes = [f, f, i, i, i32]
         L.oracle_reduce_sum_axis.argtypes = [f, f, i32, i32, i32]
         L.oracle_linear_bias_backward.argtypes = [f, f, i32, i32]
@@ -189,6 +191,28 @@ def lstm_gemm_xw(X, W, bias):
     Y = np.empty((T, G), dtype=np.float32)
     lib().oracle_lstm_gemm_xw(_fp(X), _fp(W), _fp(bias), _fp(Y), T, F, G)
     return Y
+
+
+def lstm_gemm_grad_x(G, W):
+    """lstm.cl:372-457: grad_X[T, F] = G[T, 4H] * W^T, W stored [F, 4H]."""
+    T, Gt = G.shape
+    F = W.shape[0]
+    gX = np.empty((T, F), dtype=np.float32)
+    lib().oracle_lstm_gemm_grad_x(_fp(G), _fp(W), _fp(gX), T, F, Gt)
+    return gX
+
+
+def lstm_gemm_grad_weights(X, H_out, G, grad_W, grad_U, grad_bias, batch_size, seq_len):
+    """lstm.cl:459-636: returns (grad_W + X^T G, grad_U + H_prev^T G, grad_bias + sum G)
+    with the reference's per-output fp32 arithmetic; the inputs are not modified."""
+    T, F = X.shape
+    H = H_out.shape[-1]
+    gW = np.array(grad_W, dtype=np.float32, copy=True)
+    gU = np.array(grad_U, dtype=np.float32, copy=True)
+    gB = np.array(grad_bias, dtype=np.float32, copy=True)
+    lib().oracle_lstm_gemm_grad_weights(_fp(X), _fp(H_out), _fp(G), _fp(gW), _fp(gU), _fp(gB),
+                                        batch_size, seq_len, F, H)
+    return gW, gU, gB
 
 
 def tensor_permute(x, axes):

@@ -22,6 +22,13 @@
  *  - oracle_linear_forward_tiled / oracle_lstm_gemm_xw follow cs/cl_kernels/linear.cl:14-144
  *    and cs/cl_kernels/lstm.cl:273-367: the fma chain, then ONE fp32 add of bias[n] after
  *    the k loop (linear.cl:119-122, lstm.cl:356). Pinned by == bmm + row-broadcast add.
+ *  - oracle_lstm_gemm_grad_x / oracle_lstm_gemm_grad_weights follow cs/cl_kernels/lstm.cl:
+ *    372-457 / 459-636: fma chains over 16-wide zero-padded tiles, the weight gradients
+ *    accumulated onto the old value (old + chain), grad_U's left operand the previous
+ *    step's hidden state of the same sequence (zero at each sequence's first step). Pinned
+ *    by the reference kernels themselves on the GPU (tests/test_reference_gpu.py), by exact
+ *    small-integer products against independent numpy constructions, and by
+ *    grad_x == bmm_permute_tiled(G, W, transB) bit for bit.
  *  - oracle_tensor_permute follows cl_kernels/permute.cl:11-50. Pinned by numpy.transpose.
  *  - oracle_reduce_sum_axis / oracle_linear_bias_backward follow
  *    cs/cl_kernels/reduce_sum_axis.cl:3-24 and cs/cl_kernels/linear.cl:149-168: sequential
@@ -170,6 +177,56 @@ void oracle_linear_forward_tiled(const float *X, const float *W, const float *bi
 void oracle_lstm_gemm_xw(const float *X, const float *W, const float *bias, float *XW,
                          int total_tokens, int in_features, int total_gates) {
     oracle_linear_forward_tiled(X, W, bias, XW, total_tokens, in_features, total_gates, 0, 0, 1);
+}
+
+/* lstm.cl:372-457 (lstm_gemm_grad_x): grad_X[t][f] = fma chain over the gates k in
+ * ascending, zero-padded 16-wide tiles of G[t][k] * W[f][k] (the tile WTsub[k][f] is read
+ * from W[f*G + k], :413-419): the bmm_permute_tiled arithmetic with B transposed. */
+void oracle_lstm_gemm_grad_x(const float *Gr, const float *W, float *gX, int total_tokens,
+                             int in_features, int total_gates) {
+    for (int t = 0; t < total_tokens; ++t)
+        for (int f = 0; f < in_features; ++f)
+            gX[(int64_t)t * in_features + f] =
+                permute_chain(Gr, W, total_tokens, total_gates, in_features, t, f, 0, 1);
+}
+
+/* lstm.cl:459-636 (lstm_gemm_grad_weights), tokens t = b*seq_len + s in ascending,
+ * zero-padded 16-wide tiles (:484, :497-517), each output its own fp32 chain from +0.0f:
+ *   grad_W[f][c] = grad_W[f][c] + (fma chain of X[t][f] * G[t][c])              :518-560
+ *   grad_bias[c] = grad_bias[c] + (plain sum of G[t][c], padded zeros included)  :524-575
+ *   grad_U[h][c] = grad_U[h][c] + (fma chain of Hprev[t][h] * G[t][c]),
+ *                  Hprev[t][h] = H_out[(t-1)*H + h] if t % seq_len > 0 else 0    :579-632 */
+void oracle_lstm_gemm_grad_weights(const float *X, const float *Hout, const float *Gr,
+                                   float *gW, float *gU, float *gB, int batch_size,
+                                   int seq_len, int in_features, int hidden) {
+    const int T = batch_size * seq_len, Gt = 4 * hidden;
+    const int Tp = (T + REF_TILE - 1) / REF_TILE * REF_TILE;
+    for (int f = 0; f < in_features; ++f)
+        for (int c = 0; c < Gt; ++c) {
+            float acc = 0.0f;
+            for (int t = 0; t < Tp; ++t) {
+                const float x = t < T ? X[(int64_t)t * in_features + f] : 0.0f;
+                const float g = t < T ? Gr[(int64_t)t * Gt + c] : 0.0f;
+                acc = fmaf(x, g, acc);
+            }
+            gW[(int64_t)f * Gt + c] = gW[(int64_t)f * Gt + c] + acc;
+        }
+    for (int c = 0; c < Gt; ++c) {
+        float acc = 0.0f;
+        for (int t = 0; t < Tp; ++t) acc = acc + (t < T ? Gr[(int64_t)t * Gt + c] : 0.0f);
+        gB[c] = gB[c] + acc;
+    }
+    for (int h = 0; h < hidden; ++h)
+        for (int c = 0; c < Gt; ++c) {
+            float acc = 0.0f;
+            for (int t = 0; t < Tp; ++t) {
+                const float hv =
+                    (t < T && t % seq_len > 0) ? Hout[(int64_t)(t - 1) * hidden + h] : 0.0f;
+                const float g = t < T ? Gr[(int64_t)t * Gt + c] : 0.0f;
+                acc = fmaf(hv, g, acc);
+            }
+            gU[(int64_t)h * Gt + c] = gU[(int64_t)h * Gt + c] + acc;
+        }
 }
 
 /* permute.cl:11-50: dst[tid] = src[src_index(permuted coords)], up to 10 dimensions. */

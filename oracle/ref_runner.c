@@ -16,10 +16,20 @@
  *                      NnClGlob.cs:1722-1748
  *   linear_forward_tiled  as bmm_permute_tiled                      NnClGlob.cs:1505-1543
  *   tensor_permute     global (total) local chosen by the driver    NnClGlob.cs:407-420
+ *   lstm_gemm_xw       global (ceil(N/64)*16, ceil(M/64)*16) local (16,16)  NnClGlob.cs:891-899
+ *   lstm_gemm_grad_x   global (ceil(F/64)*16, ceil(T/64)*16) local (16,16)  NnClGlob.cs:986-994
+ *   lstm_gemm_grad_weights  global (ceil(4H/64)*16, ceil(max(F,H)/64)*16) local (16,16)
+ *                      NnClGlob.cs:1017-1024
  *
  * Usage: ref_runner <code_object> <kernel> <M> <K> <N> <batch> <sA> <sB> <sC> <transA>
  *                   <transB> <A.f32> <B.f32|-> <bias.f32|-> <out.f32> [reps]
- * (tensor_permute: M = num_dims, A = src, B = int32 file "dims then axes", K/N unused.)
+ * (tensor_permute: M = num_dims, A = src, B = int32 file "dims then axes", K/N unused.
+ *  lstm_gemm_xw: M = tokens, K = in_features, N = gates, A = X, B = W, bias.
+ *  lstm_gemm_grad_x: M = tokens, K = gates, N = in_features, A = grad_gates, B = W.
+ *  lstm_gemm_grad_weights: M = batch_size, K = seq_len, N = in_features, batch = hidden;
+ *  A = X, B = H_out, bias = grad_gates; <out>.init holds the initial grad_W | grad_U |
+ *  grad_bias, which are re-uploaded before every repetition (the kernel accumulates), and
+ *  <out> receives the three concatenated.)
  * Inputs are raw little-endian float32 files; the output file receives the kernel's output
  * buffer. One JSON line on stdout reports the median kernel time from OpenCL profiling
  * events. Exit status 3 means no OpenCL GPU device or the binary was refused (the caller
@@ -129,9 +139,24 @@ int main(int argc, char **argv) {
     }
 
     const int is_permute = strcmp(kname, "tensor_permute") == 0;
+    const int is_gw = strcmp(kname, "lstm_gemm_grad_weights") == 0;
     size_t out_elems;
+    /* lstm_gemm_grad_weights: sizes of grad_W, grad_U, grad_bias */
+    const size_t gw_n[3] = {(size_t)N * 4 * (size_t)batch, (size_t)batch * 4 * (size_t)batch,
+                            4 * (size_t)batch};
+    void *hinit = NULL;
     if (is_permute) {
         out_elems = a_size / sizeof(float);
+    } else if (is_gw) {
+        out_elems = gw_n[0] + gw_n[1] + gw_n[2];
+        char init_path[4096];
+        snprintf(init_path, sizeof(init_path), "%s.init", out_path);
+        size_t init_size = 0;
+        hinit = read_file(init_path, &init_size);
+        if (!hinit || init_size != out_elems * sizeof(float)) {
+            fprintf(stderr, "ref_runner: bad %s\n", init_path);
+            return 1;
+        }
     } else {
         out_elems = (size_t)(batch - 1) * (size_t)sC + (size_t)M * (size_t)N;
     }
@@ -150,6 +175,7 @@ int main(int argc, char **argv) {
     cl_mem dc = clCreateBuffer(ctx, CL_MEM_READ_WRITE, out_elems * sizeof(float), NULL, &err);
     CHECK(err, "buffer C");
 
+    cl_mem gw_bufs[3] = {NULL, NULL, NULL};
     size_t gsz[3], lsz[3];
     cl_uint dims = 3;
     size_t *lptr = lsz;
@@ -212,6 +238,56 @@ int main(int argc, char **argv) {
         gsz[2] = (size_t)batch;
         lsz[0] = lsz[1] = 16;
         lsz[2] = 1;
+    } else if (strcmp(kname, "lstm_gemm_xw") == 0) {
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &da);
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &db);
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &dbias);
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &dc);
+        clSetKernelArg(kern, t++, sizeof(int), &M);
+        clSetKernelArg(kern, t++, sizeof(int), &K);
+        clSetKernelArg(kern, t++, sizeof(int), &N);
+        dims = 2;
+        gsz[0] = (size_t)((N + 63) / 64) * 16;
+        gsz[1] = (size_t)((M + 63) / 64) * 16;
+        lsz[0] = lsz[1] = 16;
+    } else if (strcmp(kname, "lstm_gemm_grad_x") == 0) {
+        /* (all_grad_gates, W, grad_X, total_tokens, in_features, total_gates) */
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &da);
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &db);
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &dc);
+        clSetKernelArg(kern, t++, sizeof(int), &M);
+        clSetKernelArg(kern, t++, sizeof(int), &N);
+        clSetKernelArg(kern, t++, sizeof(int), &K);
+        dims = 2;
+        gsz[0] = (size_t)((N + 63) / 64) * 16;
+        gsz[1] = (size_t)((M + 63) / 64) * 16;
+        lsz[0] = lsz[1] = 16;
+    } else if (is_gw) {
+        /* (X, H_out, all_grad_gates, grad_W, grad_U, grad_bias, batch, seq, in, hidden) */
+        const int hidden = batch;
+        /* grad_W lives in the output buffer C; grad_U and grad_bias get buffers of their own */
+        cl_mem dgu = clCreateBuffer(ctx, CL_MEM_READ_WRITE, gw_n[1] * sizeof(float), NULL, &err);
+        CHECK(err, "buffer grad_U");
+        cl_mem dgb = clCreateBuffer(ctx, CL_MEM_READ_WRITE, gw_n[2] * sizeof(float), NULL, &err);
+        CHECK(err, "buffer grad_bias");
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &da);
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &db);
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &dbias);
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &dc);
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &dgu);
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &dgb);
+        clSetKernelArg(kern, t++, sizeof(int), &M);
+        clSetKernelArg(kern, t++, sizeof(int), &K);
+        clSetKernelArg(kern, t++, sizeof(int), &N);
+        clSetKernelArg(kern, t++, sizeof(int), &hidden);
+        gw_bufs[0] = dc;
+        gw_bufs[1] = dgu;
+        gw_bufs[2] = dgb;
+        const int rows = N > hidden ? N : hidden;
+        dims = 2;
+        gsz[0] = (size_t)((4 * hidden + 63) / 64) * 16;
+        gsz[1] = (size_t)((rows + 63) / 64) * 16;
+        lsz[0] = lsz[1] = 16;
     } else if (is_permute) {
         /* B file holds int32 dims[M] then axes[M]; M = num_dims */
         const int nd = M;
@@ -250,6 +326,17 @@ int main(int argc, char **argv) {
     double times[64];
     int nrep = reps < 1 ? 1 : (reps > 64 ? 64 : reps);
     for (int r = 0; r < nrep; ++r) {
+        if (is_gw) {
+            /* the kernel accumulates: every repetition starts from the initial values */
+            const float *init = (const float *)hinit;
+            size_t off = 0;
+            for (int i = 0; i < 3; ++i) {
+                CHECK(clEnqueueWriteBuffer(q, gw_bufs[i], CL_TRUE, 0, gw_n[i] * sizeof(float),
+                                           init + off, 0, NULL, NULL),
+                      "upload init");
+                off += gw_n[i];
+            }
+        }
         cl_event ev;
         CHECK(clEnqueueNDRangeKernel(q, kern, dims, NULL, gsz, lptr, 0, NULL, &ev), "enqueue");
         CHECK(clFinish(q), "clFinish");
@@ -261,8 +348,19 @@ int main(int argc, char **argv) {
     }
     qsort(times, (size_t)nrep, sizeof(double), cmp_double);
     float *hc = malloc(out_elems * sizeof(float));
-    CHECK(clEnqueueReadBuffer(q, dc, CL_TRUE, 0, out_elems * sizeof(float), hc, 0, NULL, NULL),
-          "read C");
+    if (is_gw) {
+        size_t off = 0;
+        for (int i = 0; i < 3; ++i) {
+            CHECK(clEnqueueReadBuffer(q, gw_bufs[i], CL_TRUE, 0, gw_n[i] * sizeof(float),
+                                      hc + off, 0, NULL, NULL),
+                  "read grads");
+            off += gw_n[i];
+        }
+    } else {
+        CHECK(clEnqueueReadBuffer(q, dc, CL_TRUE, 0, out_elems * sizeof(float), hc, 0, NULL,
+                                  NULL),
+              "read C");
+    }
     FILE *f = fopen(out_path, "wb");
     if (!f || fwrite(hc, sizeof(float), out_elems, f) != out_elems) {
         fprintf(stderr, "ref_runner: cannot write %s\n", out_path);

@@ -24,6 +24,9 @@ CODE_OBJECT = {
     "bmm_permute_tiled": "bmm_permute_tiled.co",
     "linear_forward_tiled": "linear.co",
     "tensor_permute": "permute.co",
+    "lstm_gemm_xw": "lstm.co",
+    "lstm_gemm_grad_x": "lstm.co",
+    "lstm_gemm_grad_weights": "lstm.co",
 }
 
 
@@ -37,7 +40,7 @@ def available():
 
 
 def run(kernel, A, B=None, bias=None, M=0, K=0, N=0, batch=1, sA=0, sB=0, sC=0, transA=0,
-        transB=0, reps=3, out_elems=None):
+        transB=0, reps=3, out_elems=None, init=None):
     """Run one reference kernel; returns (flat float32 output, info dict)."""
     if not available():
         raise Unavailable("oracle/_ref is not built (needs the reference sources at build time)")
@@ -53,6 +56,8 @@ def run(kernel, A, B=None, bias=None, M=0, K=0, N=0, batch=1, sA=0, sB=0, sC=0, 
         b = dump("b.bin", B, np.int32 if kernel == "tensor_permute" else np.float32)
         bi = dump("bias.bin", bias)
         out = os.path.join(td, "out.bin")
+        if init is not None:
+            np.ascontiguousarray(init, dtype=np.float32).tofile(out + ".init")
         cmd = [RUNNER, os.path.join(REF_DIR, CODE_OBJECT[kernel]), kernel, str(M), str(K),
                str(N), str(batch), str(sA), str(sB), str(sC), str(int(transA)),
                str(int(transB)), a, b, bi, out, str(reps)]
@@ -66,3 +71,17 @@ def run(kernel, A, B=None, bias=None, M=0, K=0, N=0, batch=1, sA=0, sB=0, sC=0, 
     if out_elems is not None:
         res = res[:out_elems]
     return res, info
+
+
+def lstm_gemm_grad_weights(X, H_out, G, grad_W, grad_U, grad_bias, batch_size, seq_len,
+                           reps=1):
+    """Runs the reference lstm_gemm_grad_weights (cs/cl_kernels/lstm.cl:459) on the given
+    initial gradients; returns (grad_W, grad_U, grad_bias) after one accumulation."""
+    F = X.shape[1]
+    H = H_out.shape[-1]
+    init = np.concatenate([np.ravel(grad_W), np.ravel(grad_U), np.ravel(grad_bias)])
+    res, info = run("lstm_gemm_grad_weights", X, H_out, G, M=batch_size, K=seq_len, N=F,
+                    batch=H, reps=reps, init=init)
+    nW, nU = F * 4 * H, H * 4 * H
+    return (res[:nW].reshape(F, 4 * H), res[nW:nW + nU].reshape(H, 4 * H),
+            res[nW + nU:].reshape(4 * H)), info

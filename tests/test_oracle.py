@@ -237,3 +237,68 @@ def test_known_answer_tests_catch_planted_mistakes():
     twice = oracle.linear_forward(X, W, bias) + bias
     assert not np.array_equal(twice[0], (X[0] @ W) + bias)
     assert np.array_equal(oracle.linear_forward(X, W, bias)[0], (X[0] @ W) + bias)
+
+
+# ------------------------------------------------------------- LSTM gradient GEMMs
+def hprev_numpy(H, batch, seq):
+    """Independent construction of the grad_U operand: within each sequence the previous
+    step's hidden state, zero at the first step."""
+    Hs = H.reshape(batch, seq, -1)
+    P = np.zeros_like(Hs)
+    P[:, 1:] = Hs[:, :-1]
+    return P.reshape(batch * seq, -1)
+
+
+def test_lstm_gemm_grad_x_exact_and_identity():
+    G = small_ints((37, 20), 40)
+    W = small_ints((19, 20), 41)
+    exact = (G.astype(np.int64) @ W.T.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(oracle.lstm_gemm_grad_x(G, W), exact)
+    Gn = oracle.normal((37, 20), 42, 0)
+    Wn = oracle.normal((19, 20), 42, 1)
+    assert np.array_equal(oracle.lstm_gemm_grad_x(Gn, Wn),
+                          oracle.bmm_permute(Gn[None], Wn[None], transB=True)[0])
+
+
+@pytest.mark.parametrize("batch,seq,F,H", [(3, 7, 10, 5), (2, 1, 4, 3), (1, 33, 17, 9)])
+def test_lstm_gemm_grad_weights_exact(batch, seq, F, H):
+    """Exact small-integer known answers: grad_W += X^T G, grad_U += H_prev^T G with the
+    per-sequence shift, grad_bias += sum G, each added onto a non-zero old value."""
+    T, Gt = batch * seq, 4 * H
+    X = small_ints((T, F), 43)
+    Hout = small_ints((T, H), 44)
+    G = small_ints((T, Gt), 45)
+    gW0, gU0, gB0 = small_ints((F, Gt), 46), small_ints((H, Gt), 47), small_ints((Gt,), 48)
+    gW, gU, gB = oracle.lstm_gemm_grad_weights(X, Hout, G, gW0, gU0, gB0, batch, seq)
+    i64 = lambda a: a.astype(np.int64)  # noqa: E731
+    assert np.array_equal(gW, (i64(gW0) + i64(X).T @ i64(G)).astype(np.float32))
+    P = hprev_numpy(Hout, batch, seq)
+    assert np.array_equal(gU, (i64(gU0) + i64(P).T @ i64(G)).astype(np.float32))
+    assert np.array_equal(gB, (i64(gB0) + i64(G).sum(axis=0)).astype(np.float32))
+    # planted mistakes the known answers tell apart: a shift that crosses sequences, and
+    # overwriting instead of accumulating
+    if batch > 1 and seq > 1:
+        crossing = np.zeros_like(Hout)
+        crossing[1:] = Hout[:-1]
+        assert not np.array_equal(gU, (i64(gU0) + i64(crossing).T @ i64(G)).astype(np.float32))
+    assert not np.array_equal(gW, (i64(X).T @ i64(G)).astype(np.float32))
+    assert not np.array_equal(gB, i64(G).sum(axis=0).astype(np.float32))
+
+
+def test_lstm_gemm_grad_weights_vs_fp64():
+    batch, seq, F, H = 4, 9, 24, 8
+    T, Gt = batch * seq, 4 * H
+    X = oracle.normal((T, F), 49, 0)
+    Hout = oracle.normal((T, H), 49, 1)
+    G = oracle.normal((T, Gt), 49, 2)
+    z = np.zeros
+    gW, gU, gB = oracle.lstm_gemm_grad_weights(X, Hout, G, z((F, Gt), np.float32),
+                                               z((H, Gt), np.float32), z(Gt, np.float32),
+                                               batch, seq)
+    P = hprev_numpy(Hout, batch, seq).astype(np.float64)
+    G64 = G.astype(np.float64)
+    tol = oracle.tolerance(T)
+    for got, ref, den in [(gW, X.astype(np.float64).T @ G64, np.abs(X).T.astype(np.float64) @ np.abs(G64)),
+                          (gU, P.T @ G64, np.abs(P).T @ np.abs(G64))]:
+        assert np.max(np.abs(got - ref) / np.maximum(den, 1e-30)) <= tol
+    assert np.max(np.abs(gB - G64.sum(axis=0)) / np.abs(G64).sum(axis=0)) <= tol

@@ -143,3 +143,54 @@ def test_config4_nn_4096_reference(nncl):
         assert np.array_equal(ours, R[r]), f"row {r}: restatement differs"
     C = host(nncl.gemm(dev(A), dev(B)))
     check_gemm(C, A, B, 0, 0, M=n, N=n, K=n, lda=n, ldb=n, rows=rows, ref=R)
+
+
+def test_lstm_gemm_kernels_reference(nncl):
+    """lstm.cl's three GEMM kernels (lstm_gemm_xw, lstm_gemm_grad_x, lstm_gemm_grad_weights)
+    run by the reference geometry: the restatement is bit-identical to them, the HIP path
+    within tolerance. grad_weights accumulates onto non-zero initial gradients."""
+    import torch
+    batch, seq, F, H = 3, 37, 70, 33  # T = 111 tokens, 132 gates: ragged everywhere
+    T, G = batch * seq, 4 * H
+    X = oracle.normal((T, F), 31, 0)
+    W = oracle.uniform((F, G), 31, 1, -0.2, 0.2)
+    bias = oracle.uniform((G,), 31, 2, -0.2, 0.2)
+    say("reference lstm_gemm_xw")
+    R, _ = run_ref("lstm_gemm_xw", X, W, bias, M=T, K=F, N=G)
+    assert np.array_equal(oracle.lstm_gemm_xw(X, W, bias).ravel(), R)
+    XW = host(nncl.LstmGemmXW(dev(X.reshape(batch, seq, F)), dev(W), dev(bias)))
+    ap = oracle.gemm_absprod(X, W, 0, 0, bias, M=T, N=G, K=F, lda=F, ldb=G)[0]
+    assert rel_distance(XW, R.reshape(T, G), ap) <= oracle.tolerance(F)
+
+    Gr = oracle.normal((T, G), 31, 3)
+    say("reference lstm_gemm_grad_x")
+    R, _ = run_ref("lstm_gemm_grad_x", Gr, W, M=T, K=G, N=F)
+    assert np.array_equal(oracle.lstm_gemm_grad_x(Gr, W).ravel(), R)
+    gX = host(nncl.LstmGemmGradX(dev(Gr), dev(W), (batch, seq, F))).reshape(T, F)
+    ap = oracle.gemm_absprod(Gr, W, 0, 1, None, M=T, N=F, K=G, lda=G, ldb=G)[0]
+    assert rel_distance(gX, R.reshape(T, F), ap) <= oracle.tolerance(G)
+
+    Hout = oracle.normal((T, H), 31, 4)
+    gW0 = oracle.normal((F, G), 31, 5)
+    gU0 = oracle.normal((H, G), 31, 6)
+    gB0 = oracle.normal((G,), 31, 7)
+    say("reference lstm_gemm_grad_weights")
+    try:
+        (rW, rU, rB), _ = ref.lstm_gemm_grad_weights(X, Hout, Gr, gW0, gU0, gB0, batch, seq)
+    except ref.Unavailable as e:
+        pytest.skip(f"reference OpenCL kernels unavailable: {e}")
+    oW, oU, oB = oracle.lstm_gemm_grad_weights(X, Hout, Gr, gW0, gU0, gB0, batch, seq)
+    assert np.array_equal(oW, rW) and np.array_equal(oU, rU) and np.array_equal(oB, rB)
+    tW, tU, tB = dev(gW0), dev(gU0), dev(gB0)
+    nncl.LstmGemmGradWeights(dev(X.reshape(batch, seq, F)), dev(Hout.reshape(batch, seq, H)),
+                             dev(Gr), tW, tU, tB)
+    torch.cuda.synchronize()
+    P = Hout.reshape(batch, seq, H).copy()
+    P[:, 1:] = P[:, :-1].copy()
+    P[:, 0] = 0
+    P = P.reshape(T, H)
+    for got, ref_, A_, K_ in [(host(tW), rW, X, F), (host(tU), rU, P, H)]:
+        den = np.abs(A_.astype(np.float64)).T @ np.abs(Gr.astype(np.float64)) + np.abs(ref_)
+        assert rel_distance(got, ref_, den) <= oracle.tolerance(T), K_
+    denb = np.abs(Gr.astype(np.float64)).sum(axis=0) + np.abs(gB0)
+    assert rel_distance(host(tB), rB, denb) <= oracle.tolerance(T)
