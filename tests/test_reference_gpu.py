@@ -194,3 +194,46 @@ def test_lstm_gemm_kernels_reference(nncl):
         assert rel_distance(got, ref_, den) <= oracle.tolerance(T), K_
     denb = np.abs(Gr.astype(np.float64)).sum(axis=0) + np.abs(gB0)
     assert rel_distance(host(tB), rB, denb) <= oracle.tolerance(T)
+
+
+def test_lstm_gemm_kernels_reference_at_baseline_size(nncl):
+    """lstm.cl's GEMM kernels at the LSTM of BASELINE config 3 (input 512, hidden 1024) over
+    64 sequences of 100 steps: the restatement reproduces sampled rows of lstm_gemm_xw and
+    lstm_gemm_grad_x bit for bit (matmul_rows is the same fma chain); the HIP path is within
+    tolerance of the reference. Prints the reference kernels' times on this GPU."""
+    batch, seq, F, H = 64, 100, 512, 1024
+    T, G = batch * seq, 4 * H
+    X = oracle.normal((T, F), 32, 0)
+    W = oracle.uniform((F, G), 32, 1, -1 / 32, 1 / 32)
+    bias = oracle.uniform((G,), 32, 2, -1 / 32, 1 / 32)
+    Gr = oracle.normal((T, G), 32, 4, 0.0, 1.0 / 64)
+    rows = sample_rows(T, 8)
+    say("reference lstm_gemm_xw", T, F, G)
+    R, info = run_ref("lstm_gemm_xw", X, W, bias, M=T, K=F, N=G)
+    say(info)
+    R = R.reshape(T, G)
+    for r in rows:
+        ours = oracle.matmul_rows(X, W, r, r + 1, threads=8)[0] + bias
+        assert np.array_equal(ours, R[r]), f"row {r}"
+    C = host(nncl.LstmGemmXW(dev(X.reshape(batch, seq, F)), dev(W), dev(bias)))
+    check_gemm(C, X, W, 0, 0, bias=bias, M=T, N=G, K=F, lda=F, ldb=G, rows=rows, ref=R)
+    say("reference lstm_gemm_grad_x", T, F, G)
+    R, info = run_ref("lstm_gemm_grad_x", Gr, W, M=T, K=G, N=F)
+    say(info)
+    R = R.reshape(T, F)
+    Wt = np.ascontiguousarray(W.T)
+    for r in rows:
+        assert np.array_equal(oracle.matmul_rows(Gr, Wt, r, r + 1, threads=8)[0], R[r]), r
+    C = host(nncl.LstmGemmGradX(dev(Gr), dev(W), (T, F)))
+    check_gemm(C, Gr, W, 0, 1, M=T, N=F, K=G, lda=G, ldb=G, rows=rows, ref=R)
+    Hout = oracle.uniform((T, H), 32, 3, -1.0, 1.0)
+    say("reference lstm_gemm_grad_weights", batch, seq, F, H)
+    z = np.zeros
+    try:
+        (rW, rU, rB), info = ref.lstm_gemm_grad_weights(
+            X, Hout, Gr, z((F, G), np.float32), z((H, G), np.float32), z(G, np.float32), batch,
+            seq, reps=3)
+    except ref.Unavailable as e:
+        pytest.skip(f"reference OpenCL kernels unavailable: {e}")
+    say(info)
+    check_gemm(rW, X, Gr, 1, 0, M=F, N=G, K=T, lda=F, ldb=G, rows=sample_rows(F, 6))
