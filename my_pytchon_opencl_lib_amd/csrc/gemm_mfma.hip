@@ -529,7 +529,9 @@ int launch_layout(hipStream_t s, const TiledArgs &a, bool akc, bool bkc, bool av
 // Sets the tile grid for a BM x BN tile and the split-K ranges (a.splits requested on
 // entry; on return the number of non-empty ranges, each of kt_per_split BK-wide k-tiles),
 // then launches.
-template <int BM, int BN, int BK, int WM, int WN>
+// ONLY: -1 instantiates every operand layout; 0..3 only the layout (akc = ONLY >> 1,
+// bkc = ONLY & 1), for tile shapes that one form alone uses.
+template <int BM, int BN, int BK, int WM, int WN, int ONLY = -1>
 int launch_tiles(hipStream_t s, TiledArgs &a, bool akc, bool bkc, bool av, bool bv) {
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
@@ -542,7 +544,10 @@ int launch_tiles(hipStream_t s, TiledArgs &a, bool akc, bool bkc, bool av, bool 
         return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm: %lld tiles exceed one launch",
                          (long long)total);
     a.total = (int)total;
-    return launch_layout<BM, BN, BK, WM, WN>(s, a, akc, bkc, av, bv);
+    if constexpr (ONLY >= 0)
+        return launch_vec<BM, BN, BK, WM, WN, (ONLY >> 1) != 0, (ONLY & 1) != 0>(s, a, av, bv);
+    else
+        return launch_layout<BM, BN, BK, WM, WN>(s, a, akc, bkc, av, bv);
 }
 
 }  // namespace
@@ -695,7 +700,18 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
                 // 141.4 / 145.4 / 144.6; 128x256 with 8: 141.2 / 140.5 / 141.5; 128x128 with
                 // 4: 140.2 / 136.1 / 140.3; 128x128 with 2x2 wavefronts of 64x64: 140.1 /
                 // 125.9 / 140.2.
-                if (big == 2)
+                // NT (both operands K-contiguous) runs BK = 32: half the barriers, 144 KB of
+                // LDS; measured NT 146.3 against 144.1 TFLOP/s at 4096^3, 148.6 against 145.5
+                // at 8192^3. With an I-contiguous operand BK = 32 spills and is slower (NN
+                // 133.0 against 143.5), so NN / TN keep BK = 16. TN (both operands
+                // I-contiguous) runs 8 wavefronts of 64x128 (2 per SIMD, ~220 VGPRs): 143.2
+                // against 142.5 at 4096^3, 145.9 against 144.3 at 8192^3; NN and NT are
+                // slower that way (142.7 / 143.0).
+                if (big == 2 && akc && bkc)
+                    rc = launch_tiles<256, 256, 32, 8, 2, 3>(stream, a, akc, bkc, av, bv);
+                else if (big == 2 && !akc && !bkc)
+                    rc = launch_tiles<256, 256, 16, 4, 2, 0>(stream, a, akc, bkc, av, bv);
+                else if (big == 2)
                     rc = launch_tiles<256, 256, 16, 8, 2>(stream, a, akc, bkc, av, bv);
                 else if (big == 1)
                     rc = launch_tiles<128, 256, 16, 4, 2>(stream, a, akc, bkc, av, bv);

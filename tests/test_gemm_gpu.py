@@ -327,8 +327,9 @@ def forced_tile(request):
 
 
 @pytest.mark.parametrize("forced_tile", ["128", "128x256", "256"], indirect=True)
-@pytest.mark.parametrize("M,K,N", [(2000, 50, 3980), (3000, 70, 2900), (1000, 300, 1100)])
-@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+@pytest.mark.parametrize("M,K,N", [(2000, 50, 3980), (3000, 70, 2900), (1000, 300, 1100),
+                                   (1001, 301, 1103)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_large_tile_shapes_exact(nncl, forced_tile, M, K, N, ta, tb):
     """Ragged shapes through each large macro-tile (128x128, 128x256, 256x256), with a
     zero-filled K tail; exact small-integer products."""
