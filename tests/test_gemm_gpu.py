@@ -356,3 +356,21 @@ def test_long_k_split_tiles_exact(nncl, M, K, N, ta, tb):
     expect = (Aop @ Bop).astype(np.float32)  # exact: |sums| <= 4*K << 2^24
     got = gemm_gpu(nncl, A, B, bool(ta), bool(tb))
     assert np.array_equal(got, expect)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("K,N", [(333, 8195), (4096, 11008), (7, 8192)])
+def test_gemv_wide_exact(nncl, M, K, N):
+    """M <= 4 on wide outputs (the sliced kernel with its ordered reduce): exact
+    small-integer products with and without bias, A in both layouts; N % 4 != 0 reads
+    columns one by one."""
+    say("gemv wide", M, K, N)
+    A = small_ints((M, K), M * 5 + K)
+    B = small_ints((K, N), N + K)
+    bias = small_ints((N,), N)
+    expect = A.astype(np.int64) @ B.astype(np.int64)
+    assert np.array_equal(gemm_gpu(nncl, A, B), expect.astype(np.float32))
+    assert np.array_equal(gemm_gpu(nncl, A, B, bias=bias),
+                          (expect + bias.astype(np.int64)).astype(np.float32))
+    At = np.ascontiguousarray(A.T)
+    assert np.array_equal(gemm_gpu(nncl, At, B, transA=True), expect.astype(np.float32))

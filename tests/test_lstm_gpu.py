@@ -38,7 +38,8 @@ def gemm_ex(A, B, C, M, N, K, transA, transB, lda, ldb, ldc, bias=None, flags=1)
                  ctypes.c_void_p(C.data_ptr()), ldc, 0, 1, flags)
 
 
-@pytest.mark.parametrize("M,K,N", [(1, 300, 257), (3, 64, 1030), (64, 1536, 300), (100, 70, 90),
+@pytest.mark.parametrize("M,K,N", [(1, 300, 257), (3, 64, 1030), (2, 300, 8200), (64, 1536, 300),
+                                   (100, 70, 90),
                                    (64, 5000, 64), (300, 5000, 200), (1000, 50, 1100)])
 def test_accumulate_epilogue_exact(nncl, policy, M, K, N):
     """C += A B (+ bias) with a non-zero C on every kernel family, the split-K and sliced
