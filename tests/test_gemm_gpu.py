@@ -374,3 +374,99 @@ def test_gemv_wide_exact(nncl, M, K, N):
                           (expect + bias.astype(np.int64)).astype(np.float32))
     At = np.ascontiguousarray(A.T)
     assert np.array_equal(gemm_gpu(nncl, At, B, transA=True), expect.astype(np.float32))
+
+
+# ------------------------------------------------------------- seeded random strided cases
+def _random_case(rng):
+    """One strided-batched request: shape class, layouts, padded leading dimensions, batch
+    strides (stride 0 = broadcast), bias and the accumulate flag."""
+    cls = int(rng.integers(0, 4))
+    if cls == 0:    # tiny: every dimension below one 16-wide tile
+        M, N, K = (int(v) for v in rng.integers(1, 41, 3))
+    elif cls == 1:  # skinny rows, wide and long (the GEMV family)
+        M, N, K = int(rng.integers(1, 5)), int(rng.integers(1, 5000)), int(rng.integers(1, 3000))
+    elif cls == 2:  # medium ragged
+        M, N = (int(v) for v in rng.integers(40, 600, 2))
+        K = int(rng.integers(1, 900))
+    else:           # long K (split over work-groups)
+        M, N = (int(v) for v in rng.integers(1, 200, 2))
+        K = int(rng.integers(2000, 6000))
+    ta, tb = (int(v) for v in rng.integers(0, 2, 2))
+    batch = int(rng.integers(1, 4)) if M * N * K < 30_000_000 else 1
+    c = dict(M=M, N=N, K=K, ta=ta, tb=tb, batch=batch,
+             bias=bool(rng.random() < 0.4), acc=bool(rng.random() < 0.3))
+    a_rows, a_cols = (K, M) if ta else (M, K)
+    b_rows, b_cols = (N, K) if tb else (K, N)
+    c["lda"] = a_cols + int(rng.integers(0, 4)) * int(rng.random() < 0.5)
+    c["ldb"] = b_cols + int(rng.integers(0, 4)) * int(rng.random() < 0.5)
+    c["ldc"] = N + int(rng.integers(0, 4)) * int(rng.random() < 0.5)
+    bcast_a = batch > 1 and rng.random() < 0.25
+    bcast_b = batch > 1 and not bcast_a and rng.random() < 0.25
+    c["sA"] = 0 if bcast_a else a_rows * c["lda"] + int(rng.integers(0, 6))
+    c["sB"] = 0 if bcast_b else b_rows * c["ldb"] + int(rng.integers(0, 6))
+    c["sC"] = M * c["ldc"] + int(rng.integers(0, 6))
+    c["a_shape"], c["b_shape"] = (a_rows, a_cols), (b_rows, b_cols)
+    return c
+
+
+def _strided(rows, cols, ld, stride, batch, rng, lo, hi):
+    """A flat buffer holding `batch` windows of [rows x cols] (leading dimension ld, batch
+    stride `stride`, 0 = one shared window) of small integers; everything else is NaN."""
+    count = 1 if stride == 0 else batch
+    size = (count - 1) * stride + rows * ld
+    buf = np.full(size, np.nan, np.float32)
+    wins = []
+    for z in range(count):
+        w = rng.integers(lo, hi + 1, size=(rows, cols)).astype(np.float32)
+        buf[z * stride:z * stride + rows * ld].reshape(rows, ld)[:, :cols] = w
+        wins.append(w)
+    return buf, [wins[0 if stride == 0 else z] for z in range(batch)]
+
+
+def test_random_strided_batched_exact(nncl, policy):
+    """180 seeded requests through migemm_gemm_strided_batched_ex over every kernel family:
+    random shapes (tiny, skinny, medium ragged, long K), all four layouts, padded leading
+    dimensions, batch strides with gaps and stride-0 broadcast, bias and the accumulating
+    epilogue. Small-integer operands make the answer exact in any summation order, so each
+    result must equal the float64 product bit-for-bit. The padding of A and B is NaN, so a
+    kernel that multiplies anything outside the [rows x cols] windows poisons its output;
+    C's padding is NaN as well and must stay NaN (no write outside [M x N])."""
+    import ctypes
+    from my_pytchon_opencl_lib_amd import _native
+    rng = np.random.default_rng(20260 + sorted(("auto", "small", "tiled")).index(policy))
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for i in range(60):
+        c = _random_case(rng)
+        M, N, K, batch = c["M"], c["N"], c["K"], c["batch"]
+        say("random", policy, i, {k: v for k, v in c.items() if not k.endswith("shape")})
+        lo, hi = (-2, 2) if K > 2000 else (-4, 4)
+        abuf, As = _strided(*c["a_shape"], c["lda"], c["sA"], batch, rng, lo, hi)
+        bbuf, Bs = _strided(*c["b_shape"], c["ldb"], c["sB"], batch, rng, lo, hi)
+        bias = rng.integers(-20, 21, size=N).astype(np.float32) if c["bias"] else None
+        cbuf = np.full((batch - 1) * c["sC"] + M * c["ldc"] + 16, np.nan, np.float32)
+        C0 = [rng.integers(-50, 51, size=(M, N)).astype(np.float32) for _ in range(batch)]
+        if c["acc"]:
+            for z in range(batch):
+                cbuf[z * c["sC"]:z * c["sC"] + M * c["ldc"]].reshape(M, c["ldc"])[:, :N] = C0[z]
+        a, b, cc = dev(abuf), dev(bbuf), dev(cbuf)
+        bt = dev(bias) if bias is not None else None
+        _native.call("migemm_gemm_strided_batched_ex", stream, c["ta"], c["tb"], M, N, K,
+                     ctypes.c_void_p(a.data_ptr()), c["lda"], c["sA"],
+                     ctypes.c_void_p(b.data_ptr()), c["ldb"], c["sB"],
+                     None if bt is None else ctypes.c_void_p(bt.data_ptr()),
+                     ctypes.c_void_p(cc.data_ptr()), c["ldc"], c["sC"], batch, int(c["acc"]))
+        out = host(cc)
+        inside = np.zeros(out.shape, bool)
+        for z in range(batch):
+            Aop = As[z].T if c["ta"] else As[z]
+            Bop = Bs[z].T if c["tb"] else Bs[z]
+            expect = Aop.astype(np.float64) @ Bop.astype(np.float64)
+            if bias is not None:
+                expect = expect + bias
+            if c["acc"]:
+                expect = expect + C0[z]
+            s = z * c["sC"]
+            got = out[s:s + M * c["ldc"]].reshape(M, c["ldc"])[:, :N]
+            assert np.array_equal(got, expect.astype(np.float32)), (i, z, c)
+            inside[s:s + M * c["ldc"]].reshape(M, c["ldc"])[:, :N] = True
+        assert np.all(np.isnan(out[~inside])), (i, "write outside [M x N]", c)
