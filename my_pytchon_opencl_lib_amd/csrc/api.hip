@@ -10,8 +10,9 @@
 #include <string.h>
 
 #include <atomic>
+#include <map>
 #include <mutex>
-#include <vector>
+#include <tuple>
 
 #include "migemm_internal.h"
 
@@ -51,7 +52,8 @@ struct DeviceWorkspace {
     size_t bytes = 0;
 };
 std::mutex g_ws_mutex;
-std::vector<DeviceWorkspace> g_ws;
+// keyed by (device, stream, slot)
+std::map<std::tuple<int, uintptr_t, int>, DeviceWorkspace> g_ws;
 }  // namespace
 
 int set_error(int code, const char *fmt, ...) {
@@ -71,11 +73,17 @@ int hip_check(hipError_t e, const char *what) {
     return set_error(MIGEMM_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-// One growing buffer per device and slot. A buffer that is outgrown is retired, not freed:
+// One growing buffer per device, stream and slot: calls on one stream run in order, so
+// they can share a buffer, and calls on different streams (the reference host keeps one
+// queue per thread) never share one. A buffer that is outgrown is retired, not freed:
 // work already queued, or a HIP graph captured earlier, may still refer to it, so retired
-// buffers live until the process ends. Calls that use the workspace must be ordered on
-// one stream (they share the buffer).
-void *workspace(size_t bytes, int *status, int slot) {
+// buffers live until the process ends.
+// Nothing is allocated while the stream is being captured into a HIP graph (an allocation
+// would invalidate the capture). A capturing stream whose own buffer is too small (torch,
+// for one, captures on a stream of its own) takes the smallest large-enough buffer that
+// eager calls on the device have sized; the graph then shares it with that buffer's
+// stream.
+void *workspace(hipStream_t stream, size_t bytes, int *status, int slot) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) {
@@ -86,23 +94,46 @@ void *workspace(size_t bytes, int *status, int slot) {
         *status = set_error(MIGEMM_ERR_WORKSPACE, "workspace slot %d", slot);
         return nullptr;
     }
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &capture);
+    if (e != hipSuccess) {
+        *status = hip_check(e, "hipStreamIsCapturing");
+        return nullptr;
+    }
     std::lock_guard<std::mutex> lock(g_ws_mutex);
-    if ((int)g_ws.size() <= dev * kWorkspaceSlots + slot)
-        g_ws.resize((dev + 1) * kWorkspaceSlots);
-    DeviceWorkspace &w = g_ws[dev * kWorkspaceSlots + slot];
-    if (w.bytes < bytes) {
-        size_t want = bytes < ((size_t)8 << 20) ? ((size_t)8 << 20) : bytes;
-        if (want < 2 * w.bytes) want = 2 * w.bytes;
-        void *p = nullptr;
-        e = hipMalloc(&p, want);
-        if (e != hipSuccess) {
-            *status = set_error(MIGEMM_ERR_WORKSPACE, "workspace of %zu bytes: %s", want,
-                                hipGetErrorString(e));
+    const auto key = std::make_tuple(dev, reinterpret_cast<uintptr_t>(stream), slot);
+    auto it = g_ws.find(key);
+    if (it != g_ws.end() && it->second.bytes >= bytes) {
+        *status = MIGEMM_OK;
+        return it->second.ptr;
+    }
+    if (capture != hipStreamCaptureStatusNone) {
+        const DeviceWorkspace *best = nullptr;
+        for (const auto &kv : g_ws)
+            if (std::get<0>(kv.first) == dev && std::get<2>(kv.first) == slot &&
+                kv.second.bytes >= bytes && (best == nullptr || kv.second.bytes < best->bytes))
+                best = &kv.second;
+        if (best == nullptr) {
+            *status = set_error(MIGEMM_ERR_WORKSPACE,
+                                "workspace of %zu bytes is needed during HIP graph capture: "
+                                "run the same call once outside the capture first", bytes);
             return nullptr;
         }
-        w.ptr = p;  // the previous buffer (if any) is retired, never freed
-        w.bytes = want;
+        *status = MIGEMM_OK;
+        return best->ptr;
     }
+    DeviceWorkspace &w = g_ws[key];
+    size_t want = bytes < ((size_t)8 << 20) ? ((size_t)8 << 20) : bytes;
+    if (want < 2 * w.bytes) want = 2 * w.bytes;
+    void *p = nullptr;
+    e = hipMalloc(&p, want);
+    if (e != hipSuccess) {
+        *status = set_error(MIGEMM_ERR_WORKSPACE, "workspace of %zu bytes: %s", want,
+                            hipGetErrorString(e));
+        return nullptr;
+    }
+    w.ptr = p;  // the previous buffer (if any) is retired, never freed
+    w.bytes = want;
     *status = MIGEMM_OK;
     return w.ptr;
 }
@@ -327,7 +358,7 @@ int migemm_lstm_gemm_grad_weights(void *stream, const float *X, const float *H_o
     if (seq_len == 1) return MIGEMM_OK;
     int st_ws = MIGEMM_OK;
     float *hprev = static_cast<float *>(
-        workspace((size_t)tokens * hidden_size * sizeof(float), &st_ws, 1));
+        workspace(st, (size_t)tokens * hidden_size * sizeof(float), &st_ws, 1));
     if (hprev == nullptr) return st_ws;
     rc = launch_shift_rows(st, H_out, hprev, T, seq_len, hidden_size);
     if (rc != MIGEMM_OK) return rc;

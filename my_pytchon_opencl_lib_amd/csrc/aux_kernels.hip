@@ -192,7 +192,7 @@ int launch_column_sum(hipStream_t stream, const float *X, float *Y, int outer, i
     if (chunks > 1) {
         int st = MIGEMM_OK;
         dst = static_cast<float *>(
-            workspace((size_t)chunks * outer * inner * sizeof(float), &st));
+            workspace(stream, (size_t)chunks * outer * inner * sizeof(float), &st));
         if (dst == nullptr) return st;
     }
     const bool vec = inner % 4 == 0;

@@ -676,7 +676,7 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     if (splits > 1) {
         int st = MIGEMM_OK;
         a.partial = static_cast<float *>(
-            workspace((size_t)splits * d.batch * d.M * d.N * sizeof(float), &st));
+            workspace(stream, (size_t)splits * d.batch * d.M * d.N * sizeof(float), &st));
         if (a.partial == nullptr) return st;
     }
     int rc;

@@ -213,7 +213,7 @@ int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {
     if (a.slices > 1) {
         const size_t part_bytes = (size_t)a.slices * d.batch * d.M * d.N * sizeof(float);
         int st = MIGEMM_OK;
-        a.partial = static_cast<float *>(workspace(part_bytes, &st));
+        a.partial = static_cast<float *>(workspace(stream, part_bytes, &st));
         if (a.partial == nullptr) return st;
     }
     // 4-column groups never straddle N when N % 4 == 0 (16-byte loads need only 4-byte

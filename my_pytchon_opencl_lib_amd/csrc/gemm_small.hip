@@ -364,7 +364,7 @@ int launch_gemm_small(hipStream_t stream, const GemmDesc &d) {
     if (a.splits > 1) {
         int st = MIGEMM_OK;
         a.partial = static_cast<float *>(
-            workspace((size_t)a.splits * d.batch * d.M * d.N * sizeof(float), &st));
+            workspace(stream, (size_t)a.splits * d.batch * d.M * d.N * sizeof(float), &st));
         if (a.partial == nullptr) return st;
     }
     const bool akc = !d.transA;

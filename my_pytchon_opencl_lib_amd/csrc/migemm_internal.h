@@ -43,12 +43,12 @@ int launch_gemm_small(hipStream_t stream, const GemmDesc &d);
 // True when C has too few 64x64 tiles to occupy the 256 CUs (gemm_small_kernel).
 bool small_preferred(const GemmDesc &d);
 
-// Device workspace owned by the library: one growing buffer per device and slot. Slot 0
-// holds split-K partial sums (GEMM, column sums); slot 1 holds operands staged by an entry
-// point for the GEMMs it then runs (which may use slot 0). Returns nullptr and records
-// MIGEMM_ERR_WORKSPACE on failure.
+// Device workspace owned by the library: one growing buffer per device, stream and slot.
+// Slot 0 holds split-K partial sums (GEMM, column sums); slot 1 holds operands staged by
+// an entry point for the GEMMs it then runs (which may use slot 0). Returns nullptr and
+// records MIGEMM_ERR_WORKSPACE on failure.
 constexpr int kWorkspaceSlots = 2;
-void *workspace(size_t bytes, int *status, int slot = 0);
+void *workspace(hipStream_t stream, size_t bytes, int *status, int slot = 0);
 
 // C_b[m, n] = sum over s = 0..S-1 (in order) of partial[s][b][m][n] (+ bias[n]); with
 // `accumulate`, C_b[m, n] += that value.

@@ -283,6 +283,41 @@ def test_graph_capture_replays_match_eager(nncl):
         del noise
 
 
+def test_split_k_on_two_streams_concurrently(nncl):
+    """The reference host keeps one command queue per thread (DeviceQueueRegistry.cs:14).
+    GEMMs that keep partial sums in the library workspace (split-K, sliced GEMV, chunked
+    column sum) run on two streams at once, with no synchronisation between the streams,
+    and each result must be exact."""
+    say("two streams: split-K 64x8192x1536, GEMV 1x4096x11008, column sum 12000x300")
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    W = small_ints((8192, 1536), 61, -2, 2)
+    Bv = small_ints((4096, 11008), 62, -2, 2)
+    G = small_ints((12000, 300), 63, -2, 2)
+    xs = [small_ints((64, 8192), 70 + i, -2, 2) for i in range(6)]
+    vs = [small_ints((1, 4096), 80 + i, -2, 2) for i in range(6)]
+    w, bv, g = dev(W), dev(Bv), dev(G)
+    dxs, dvs = [dev(x) for x in xs], [dev(v) for v in vs]
+    torch.cuda.synchronize()
+    outs = []
+    for i in range(6):
+        with torch.cuda.stream(s1 if i % 2 == 0 else s2):
+            outs.append(("gemm", i, nncl.gemm(dxs[i], w)))
+        with torch.cuda.stream(s2 if i % 2 == 0 else s1):
+            outs.append(("gemv", i, nncl.gemm(dvs[i], bv)))
+            outs.append(("sum", i, nncl.Sum(g, 0)))
+    torch.cuda.synchronize()
+    colsum = G.astype(np.float64).sum(axis=0).astype(np.float32)
+    for kind, i, t in outs:
+        got = host(t)
+        if kind == "gemm":
+            expect = (xs[i].astype(np.float64) @ W.astype(np.float64)).astype(np.float32)
+        elif kind == "gemv":
+            expect = (vs[i].astype(np.float64) @ Bv.astype(np.float64)).astype(np.float32)
+        else:
+            expect = colsum
+        assert np.array_equal(got.reshape(expect.shape), expect), (kind, i)
+
+
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_unaligned_bases_and_leading_dims(nncl, policy, ta, tb):
     """Operands that start 4 bytes past a 16-byte boundary with leading dimensions that
