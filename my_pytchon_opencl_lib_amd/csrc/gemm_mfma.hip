@@ -614,15 +614,21 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     };
     const int nk32 = (d.K + 31) / 32;
     // Largest tile that still gives the 256 CUs two work-groups each. Below that, a long K
-    // (>= 4096) with M, N >= 128 keeps 128x128 tiles and splits K until there are >= 1024
-    // work-groups (an even number of ranges, at most 8). Otherwise 64x64 tiles, split along
-    // K when K is long enough for every range to keep >= 4 k-tiles. Measured (graph replay,
-    // us): the Linear(500 -> 6565) gradients dX 12000x500x6565 (NT) 128x128 / 4 ranges 664,
-    // 64x64 767; dW 500x6565x12000 (TN) 128x128 / 6 ranges 691, 64x64 916.
+    // (>= 4096) with M, N >= 128 and at least 128 tiles of 128x128 keeps 128x128 tiles and
+    // splits K until there are >= 1024 work-groups (an even number of ranges, at most 8).
+    // Otherwise 64x64 tiles. A long K over 48-128 of them is split into 8 ranges: the XCD
+    // remap in the kernel then gives each XCD one k-range of every tile, so the A and B
+    // panels of that range are shared in its L2. Other splits aim at 640 work-groups, at
+    // most 32 ranges of >= 8 k-tiles of 32. Measured (graph replay, us): the Linear(500 ->
+    // 6565) gradients dX 12000x500x6565 (NT) 128x128 / 4 ranges 664, 64x64 767; dW
+    // 500x6565x12000 (TN) 128x128 / 6 ranges 691, 64x64 916. With few 128x128 tiles, 8
+    // ranges leave most CUs idle: 256x4096x256 41.5 against 64x64 / 16 ranges 14.1;
+    // 128x4096x4096 64x64 with 4 / 5 / 8 / 16 ranges: 49.2 / 55.0 / 47.9 / 51.5;
+    // 512x16384x512 TN with 5 / 8 / 10: 119.9 / 78.4 / 91.0.
     int cfg, splits = 1;
     if (tiles(128, 128) >= 512) {
         cfg = 128;
-    } else if (d.K >= 4096 && d.M >= 128 && d.N >= 128) {
+    } else if (d.K >= 4096 && d.M >= 128 && d.N >= 128 && tiles(128, 128) >= 128) {
         cfg = 128;
         int64_t want = (1024 + tiles(128, 128) - 1) / tiles(128, 128);
         want += want & 1;
@@ -631,10 +637,15 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         cfg = tiles(64, 64) >= 256 ? 64 : 32;
     } else {
         cfg = 64;
-        const int64_t want = (512 + tiles(64, 64) - 1) / tiles(64, 64);
-        const int64_t cap = nk32 / 4 < 16 ? nk32 / 4 : 16;
-        splits = (int)(want < cap ? want : cap);
-        if (splits < 1) splits = 1;
+        const int64_t t64 = tiles(64, 64);
+        if (d.K >= 4096 && t64 >= 48 && t64 <= 128) {
+            splits = 8;
+        } else {
+            const int64_t want = (640 + t64 - 1) / t64;
+            const int64_t cap = nk32 / 8 < 32 ? nk32 / 8 : 32;
+            splits = (int)(want < cap ? want : cap);
+            if (splits < 1) splits = 1;
+        }
     }
     // Large outputs: pick the macro-tile by the busiest CU's share of the work. The work-
     // groups are dealt over the 256 CUs, so a CU carries ceil(tiles / 256) tiles of area x K
