@@ -201,9 +201,12 @@ static int run_gemm(hipStream_t stream, const GemmDesc &d) {
     switch (g_policy.load(std::memory_order_relaxed)) {
         case MIGEMM_POLICY_TILED: return launch_gemm_tiled(stream, d);
         case MIGEMM_POLICY_SMALL: return launch_gemm_small(stream, d);
+        case MIGEMM_POLICY_SKINNY:
+            if (skinny_supported(d)) return launch_gemm_skinny(stream, d);
+            break;
         default: break;
     }
-    if (skinny_applicable(d)) return launch_gemm_skinny(stream, d);
+    if (skinny_preferred(d)) return launch_gemm_skinny(stream, d);
     if (small_preferred(d)) return launch_gemm_small(stream, d);
     return launch_gemm_tiled(stream, d);
 }

@@ -167,8 +167,18 @@ int launch_mr(hipStream_t st, const SkinnyArgs &a, bool vec, int batch) {
 
 }  // namespace
 
-bool skinny_applicable(const GemmDesc &d) {
+bool skinny_supported(const GemmDesc &d) {
     return d.M <= SK_MAXM && !d.transB && d.N >= 4 && d.batch <= 65535;
+}
+
+// Streaming B pays once B is too large to sit in the caches, for one or two rows: from
+// 64 MB of B the kernel reads 4.8-6.4 TB/s at M = 1-2 (1 x 11008 x 4096: 32.7 us against
+// 60.9 in the small kernel; 1 x 32000 x 4096: 83.6 against 128.6; 2 x 4096 x 16384: 51.3
+// against 106.3). With 32 MB of B, or three or four rows, the small kernel is as fast or
+// faster (1 x 4096 x 2048: 15.3 against 12.1 us; 4 x 1024 x 8192: 24.2 against 14.2;
+// 4 x 11008 x 4096: 65.6 against 61.3).
+bool skinny_preferred(const GemmDesc &d) {
+    return skinny_supported(d) && d.M <= 2 && (int64_t)d.K * d.N * d.batch >= ((int64_t)16 << 20);
 }
 
 int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {

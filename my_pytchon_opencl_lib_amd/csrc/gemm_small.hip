@@ -321,13 +321,30 @@ SmallPlan plan_small(const GemmDesc &d) {
 
 }  // namespace
 
-// Chosen when C has fewer 64x64 tiles than CUs and K is at most 2048. Measured (graph
-// replay, us, small / tiled split-K): 256^3 3.3 / 8.2; 32 x 128x128x64 4.7 / 5.9; 64 x 4096
-// x 1536 15.6 / 19.0; at K = 4096 the tiled kernel wins: 64 x 1536 x 4096 23.8 / 18.9,
-// 128 x 4096 x 4096 64 / 49, 256 x 256 x 4096 13.4 / 13.1.
+// Where the small kernel beats the tiled one (graph replay over a grid of M, N in 1..6000
+// and K in 16..8192, NN and TN; us, small / tiled):
+//  * M or N <= 4 (unless B is large enough for the skinny kernel): the tiled kernel's
+//    64-wide tiles would be almost empty (6000 x 1 x 8192 48 / 63; 3 x 300 x 300 4.5 / 10.0).
+//  * fewer 64x64 tiles than CUs, and then
+//    - a thin output (M or N <= 32) or K <= 64 (17 x 1024 x 8192 14.4 / 18.5);
+//    - K <= 1024 with < 128 tiles (777 x 300 x 300 9.7 / 11.7; 2048 x 300 x 300 takes the
+//      tiled kernel, 16.3 / 12.2);
+//    - K <= 2048 with < 12 tiles, or < 80 tiles that give the small kernel >= 128 work-
+//      groups without a k split (64 x 4096 x 1536 15.6 / 19.0; 200 x 300 x 2048, 76 work-
+//      groups, 15.3 / 12.8; 6000 x 64 x 2048 33.0 / 28.6);
+//    - longer K with at most 4 tiles (128 x 8192 x 128 11.7 / 13.4; 256 x 4096 x 256 takes
+//      the tiled split, 14.2 / 13.6).
 bool small_preferred(const GemmDesc &d) {
+    if (d.M <= 4 || d.N <= 4) return true;
     const int64_t tiles64 = cdiv(d.M, 64) * cdiv(d.N, 64) * d.batch;
-    return tiles64 < 256 && d.K <= 2048;
+    if (tiles64 >= 256) return false;
+    if ((d.M < d.N ? d.M : d.N) <= 32 || d.K <= 64) return true;
+    if (d.K <= 1024) return tiles64 < 128;
+    if (d.K <= 2048) {
+        const int64_t wgs = cdiv(d.M, 64) * cdiv(d.N, 16) * d.batch;  // row blocks of 4
+        return tiles64 < 12 || (wgs >= 128 && tiles64 < 80);
+    }
+    return tiles64 <= 4;
 }
 
 int launch_gemm_small(hipStream_t stream, const GemmDesc &d) {

@@ -38,7 +38,10 @@ struct GemmDesc {
 // Launchers. They assume a validated descriptor and only enqueue work.
 int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d);
 int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d);
-bool skinny_applicable(const GemmDesc &d);
+// M <= 4 and B not transposed (the shapes gemm_skinny_kernel handles).
+bool skinny_supported(const GemmDesc &d);
+// Supported, M <= 2 and B large enough (>= 64 MB) for the streaming kernel to beat the others.
+bool skinny_preferred(const GemmDesc &d);
 int launch_gemm_small(hipStream_t stream, const GemmDesc &d);
 // True when C has too few 64x64 tiles to occupy the 256 CUs (gemm_small_kernel).
 bool small_preferred(const GemmDesc &d);
