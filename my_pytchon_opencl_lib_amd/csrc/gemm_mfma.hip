@@ -616,13 +616,14 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     // Largest tile that still gives the 256 CUs two work-groups each. Below that, a long K
     // (>= 4096) with M, N >= 128 and at least 128 tiles of 128x128 keeps 128x128 tiles and
     // splits K until there are >= 1024 work-groups (an even number of ranges, at most 8).
-    // Otherwise 64x64 tiles. A long K over 48-128 of them is split into 8 ranges: the XCD
-    // remap in the kernel then gives each XCD one k-range of every tile, so the A and B
-    // panels of that range are shared in its L2. Other splits aim at 640 work-groups, at
-    // most 32 ranges of >= 8 k-tiles of 32. Measured (graph replay, us): the Linear(500 ->
-    // 6565) gradients dX 12000x500x6565 (NT) 128x128 / 4 ranges 664, 64x64 767; dW
-    // 500x6565x12000 (TN) 128x128 / 6 ranges 691, 64x64 916. With few 128x128 tiles, 8
-    // ranges leave most CUs idle: 256x4096x256 41.5 against 64x64 / 16 ranges 14.1;
+    // Otherwise 64x64 tiles, mostly whole when there are >= 256 of them (a split then mostly
+    // adds the reduce: 1024^3 in 2 ranges 62.7 TFLOP/s, whole 75.7). A long K over 48-128 is
+    // split into 8 ranges: the XCD remap in the kernel then gives each XCD one k-range of
+    // every tile, so the A and B panels of that range are shared in its L2. Other splits aim
+    // at 640 work-groups, at most 32 ranges of >= 8 k-tiles of 32. Measured (graph replay,
+    // us): the Linear(500 -> 6565) gradients dX 12000x500x6565 (NT) 128x128 / 4 ranges 664,
+    // 64x64 767; dW 500x6565x12000 (TN) 128x128 / 6 ranges 691, 64x64 916. With few 128x128
+    // tiles, 8 ranges leave most CUs idle: 256x4096x256 41.5 against 64x64 / 16 ranges 14.1;
     // 128x4096x4096 64x64 with 4 / 5 / 8 / 16 ranges: 49.2 / 55.0 / 47.9 / 51.5;
     // 512x16384x512 TN with 5 / 8 / 10: 119.9 / 78.4 / 91.0.
     int cfg, splits = 1;
@@ -633,8 +634,15 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         int64_t want = (1024 + tiles(128, 128) - 1) / tiles(128, 128);
         want += want & 1;
         splits = (int)(want < 8 ? want : 8);
-    } else if (tiles(64, 64) >= 512 || nk32 < 8) {
+    } else if (tiles(64, 64) >= 256 || nk32 < 8) {
         cfg = tiles(64, 64) >= 256 ? 64 : 32;
+        // About one tile per CU (one wavefront per SIMD) with a long k loop, or a few tiles
+        // left over for a second round: 3 ranges fill the CUs (1024x2048x1024 NT 77.3 ->
+        // 89.6 TFLOP/s, 1100x1100x900 49.6 -> 57.2; 1024^3, balanced and short, stays whole)
+        const int64_t t64 = tiles(64, 64);
+        if (t64 >= 256 && t64 < 320 && nk32 >= 24 &&
+            (d.K >= 2048 || (t64 % 256 != 0 && d.K >= 768)))
+            splits = 3;
     } else {
         cfg = 64;
         const int64_t t64 = tiles(64, 64);
