@@ -54,6 +54,18 @@ def _stream(t):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
+def _launch(name, tensors, *args):
+    """Calls C-ABI entry `name` on the current stream of the tensors' device, with that
+    device current (the library launches on the current HIP device). All tensors of one
+    call must live on one device."""
+    devices = {t.device for t in tensors}
+    _require(len(devices) == 1,
+             f"all operands must be on one device (got {sorted(map(str, devices))})")
+    dev = tensors[0].device
+    with torch.cuda.device(dev):
+        _native.call(name, _stream(tensors[0]), *args)
+
+
 def _check_tensor(name, t):
     _require(isinstance(t, torch.Tensor), f"{name} must be a torch.Tensor")
     _require(t.dtype == torch.float32, f"{name} must be float32 (got {t.dtype})")
@@ -83,8 +95,8 @@ class NnClGlob:
         n = b.shape[2]
         c = torch.empty((batch, m, n), dtype=torch.float32, device=a.device)
         sB = 0 if b.shape[0] == 1 else k * n
-        _native.call("migemm_bmm_tiled", _stream(a), _ptr(a), _ptr(b), _ptr(c), m, k, n,
-                     m * k, sB, m * n, batch)
+        _launch("migemm_bmm_tiled", (a, b, c), _ptr(a), _ptr(b), _ptr(c), m, k, n, m * k, sB,
+                m * n, batch)
         torch.cuda.current_stream(a.device).synchronize()
         return c
 
@@ -105,8 +117,8 @@ class NnClGlob:
         c = torch.empty((batch, m, n), dtype=torch.float32, device=a.device)
         sA = 0 if a.shape[0] == 1 else a.shape[1] * a.shape[2]
         sB = 0 if b.shape[0] == 1 else b.shape[1] * b.shape[2]
-        _native.call("migemm_bmm_permute_tiled", _stream(a), _ptr(a), _ptr(b), _ptr(c), m, kA,
-                     n, sA, sB, m * n, int(bool(transA)), int(bool(transB)), batch)
+        _launch("migemm_bmm_permute_tiled", (a, b, c), _ptr(a), _ptr(b), _ptr(c), m, kA, n, sA,
+                sB, m * n, int(bool(transA)), int(bool(transB)), batch)
         return c
 
     def Permute(self, x, axes):
@@ -118,7 +130,7 @@ class NnClGlob:
         y = torch.empty([x.shape[i] for i in axes], dtype=torch.float32, device=x.device)
         dims = (ctypes.c_int * x.dim())(*x.shape)
         ax = (ctypes.c_int * x.dim())(*axes)
-        _native.call("migemm_tensor_permute", _stream(x), _ptr(x), _ptr(y), dims, ax, x.dim())
+        _launch("migemm_tensor_permute", (x, y), _ptr(x), _ptr(y), dims, ax, x.dim())
         return y
 
     def LinearForward(self, x, w, bias):
@@ -134,8 +146,8 @@ class NnClGlob:
                  f"w must be [1, {k}, N] (got {list(w.shape)})")
         _require(bias.numel() == n, f"bias must have {n} elements (got {bias.numel()})")
         y = torch.empty((batch, m, n), dtype=torch.float32, device=x.device)
-        _native.call("migemm_linear_forward", _stream(x), _ptr(x), _ptr(w), _ptr(bias), _ptr(y),
-                     m, k, n, m * k, m * n, batch)
+        _launch("migemm_linear_forward", (x, w, bias, y), _ptr(x), _ptr(w), _ptr(bias), _ptr(y),
+                m, k, n, m * k, m * n, batch)
         return y
 
     def LinearBiasBackward(self, gradOutput, biasShape):
@@ -145,8 +157,8 @@ class NnClGlob:
         rows = gradOutput.numel() // n
         gb = torch.empty(list(biasShape), dtype=torch.float32, device=gradOutput.device)
         _require(gb.numel() == n, f"bias shape {list(biasShape)} does not hold {n} values")
-        _native.call("migemm_linear_bias_backward", _stream(gradOutput), _ptr(gradOutput),
-                     _ptr(gb), rows, n)
+        _launch("migemm_linear_bias_backward", (gradOutput, gb), _ptr(gradOutput), _ptr(gb),
+                rows, n)
         return gb
 
     # ---- LSTM GEMM stages (NnClGlob.Lstm / LstmBackward, cs/compiler/NnClGlob.cs:850-1061).
@@ -160,12 +172,13 @@ class NnClGlob:
         _check_tensor("bias", bias)
         f = x.shape[-1]
         t = x.numel() // f
-        _require(w.dim() == 2 and w.shape[0] == f, f"w must be [{f}, 4*hidden] (got {list(w.shape)})")
+        _require(w.dim() == 2 and w.shape[0] == f,
+                 f"w must be [{f}, 4*hidden] (got {list(w.shape)})")
         g = w.shape[1]
         _require(bias.numel() == g, f"bias must have {g} elements (got {bias.numel()})")
         xw = torch.empty((t, g), dtype=torch.float32, device=x.device)
-        _native.call("migemm_lstm_gemm_xw", _stream(x), _ptr(x), _ptr(w), _ptr(bias), _ptr(xw),
-                     t, f, g)
+        _launch("migemm_lstm_gemm_xw", (x, w, bias, xw), _ptr(x), _ptr(w), _ptr(bias), _ptr(xw),
+                t, f, g)
         return xw
 
     def LstmGemmGradX(self, allGradGates, w, xShape):
@@ -180,8 +193,8 @@ class NnClGlob:
         t = allGradGates.numel() // g
         gx = torch.empty(list(xShape), dtype=torch.float32, device=w.device)
         _require(gx.numel() == t * f, f"xShape {list(xShape)} does not hold [{t}, {f}]")
-        _native.call("migemm_lstm_gemm_grad_x", _stream(w), _ptr(allGradGates), _ptr(w),
-                     _ptr(gx), t, f, g)
+        _launch("migemm_lstm_gemm_grad_x", (w, allGradGates, gx), _ptr(allGradGates), _ptr(w),
+                _ptr(gx), t, f, g)
         return gx
 
     def LstmGemmGradWeights(self, x, hOut, allGradGates, gradW, gradU, gradBias):
@@ -200,8 +213,9 @@ class NnClGlob:
         _require(gradW.numel() == f * 4 * h, f"gradW must hold [{f}, {4 * h}]")
         _require(gradU.numel() == h * 4 * h, f"gradU must hold [{h}, {4 * h}]")
         _require(gradBias.numel() == 4 * h, f"gradBias must hold {4 * h} values")
-        _native.call("migemm_lstm_gemm_grad_weights", _stream(x), _ptr(x), _ptr(hOut),
-                     _ptr(allGradGates), _ptr(gradW), _ptr(gradU), _ptr(gradBias), b, s_, f, h)
+        _launch("migemm_lstm_gemm_grad_weights", (x, hOut, allGradGates, gradW, gradU, gradBias),
+                _ptr(x), _ptr(hOut), _ptr(allGradGates), _ptr(gradW), _ptr(gradU),
+                _ptr(gradBias), b, s_, f, h)
         return gradW, gradU, gradBias
 
     def Sum(self, x, axis, keepDims=False):
@@ -224,8 +238,7 @@ class NnClGlob:
         else:
             shape = [s for i, s in enumerate(x.shape) if i != ax]
         y = torch.empty(shape, dtype=torch.float32, device=x.device)
-        _native.call("migemm_reduce_sum_axis", _stream(x), _ptr(x), _ptr(y), outer,
-                     x.shape[ax], inner)
+        _launch("migemm_reduce_sum_axis", (x, y), _ptr(x), _ptr(y), outer, x.shape[ax], inner)
         return y
 
     # -------------------------------------------------------------- Python names
@@ -264,8 +277,8 @@ class NnClGlob:
                  "x and grad_output must share [Batch, M]")
         n = grad_output.shape[2]
         dw = torch.empty((1, k, n), dtype=torch.float32, device=x.device)
-        _native.call("migemm_linear_weight_grad", _stream(x), _ptr(x), _ptr(grad_output),
-                     _ptr(dw), m, k, n, batch)
+        _launch("migemm_linear_weight_grad", (x, grad_output, dw), _ptr(x), _ptr(grad_output),
+                _ptr(dw), m, k, n, batch)
         return dw
 
     def gemm(self, a, b, transA=False, transB=False, bias=None, out=None):
@@ -291,7 +304,8 @@ class NnClGlob:
             _require(out.numel() == batch * m * n, "out has the wrong size")
         sA = 0 if a3.shape[0] == 1 else a3.shape[1] * a3.shape[2]
         sB = 0 if b3.shape[0] == 1 else b3.shape[1] * b3.shape[2]
-        _native.call("migemm_gemm_strided_batched", _stream(a), int(transA), int(transB), m, n,
-                     k, _ptr(a3), a3.shape[2], sA, _ptr(b3), b3.shape[2], sB,
-                     _ptr(bias) if bias is not None else None, _ptr(out), n, m * n, batch)
+        _launch("migemm_gemm_strided_batched", (a, b, out) + ((bias,) if bias is not None else ()),
+                int(transA), int(transB), m, n, k, _ptr(a3), a3.shape[2], sA, _ptr(b3),
+                b3.shape[2], sB, _ptr(bias) if bias is not None else None, _ptr(out), n, m * n,
+                batch)
         return out.view(m, n) if squeeze else out

@@ -298,7 +298,8 @@ def test_lstm_gemm_grad_weights_vs_fp64():
     P = hprev_numpy(Hout, batch, seq).astype(np.float64)
     G64 = G.astype(np.float64)
     tol = oracle.tolerance(T)
-    for got, ref, den in [(gW, X.astype(np.float64).T @ G64, np.abs(X).T.astype(np.float64) @ np.abs(G64)),
+    X64 = X.astype(np.float64)
+    for got, ref, den in [(gW, X64.T @ G64, np.abs(X64).T @ np.abs(G64)),
                           (gU, P.T @ G64, np.abs(P).T @ np.abs(G64))]:
         assert np.max(np.abs(got - ref) / np.maximum(den, 1e-30)) <= tol
     assert np.max(np.abs(gB - G64.sum(axis=0)) / np.abs(G64).sum(axis=0)) <= tol
