@@ -3,10 +3,10 @@
 // is therefore bound by HBM bandwidth (0.5 FLOP/byte at M = 1), not by the matrix cores.
 //
 // Work split: a work-group of 4 wavefronts owns 256 consecutive columns (one float4 of
-// B per lane) and a slice of KC rows of K; wavefront w accumulates the w-th quarter of
-// the slice with fp32 FMA chains, 16 rows of loads in flight at a time, and the 4
-// wavefronts are combined through LDS. With
-// S = ceil(K / KC) > 1 slices, each slice writes its partial sums to the library
+// B per lane) and a slice of KC rows of K; the slice of A is staged in LDS, wavefront w
+// accumulates the w-th quarter of the slice with fp32 FMA chains, 16 rows of loads in
+// flight at a time (8 for 3-4 rows of C), and the 4 wavefronts are combined through LDS.
+// With S = ceil(K / KC) > 1 slices, each slice writes its partial sums to the library
 // workspace and a second kernel (reduce_slices_kernel, gemm_mfma.hip) adds the S partials
 // of every output in slice order, then the bias. The result is deterministic: the
 // association order depends only on (K, KC), never on timing. (A single-kernel
@@ -27,7 +27,13 @@ typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
 constexpr int SK_THREADS = 256;
 constexpr int SK_COLS = 256;  // columns per work-group (64 lanes x float4)
 constexpr int SK_MAXM = 4;
-constexpr int SK_UNROLL = 16;  // rows of B in flight per wavefront
+// rows of B in flight per wavefront: 16, or 8 for 3-4 rows of C, whose A values and
+// accumulators would otherwise hold 256 VGPRs (one wavefront per SIMD)
+template <int MR>
+struct SkUnroll {
+    static constexpr int value = MR <= 2 ? 16 : 8;
+};
+constexpr int SK_KC_MAX = 512;  // rows of K per slice at most (A's slice is staged in LDS)
 
 struct SkinnyArgs {
     const float *A;
@@ -49,6 +55,7 @@ struct SkinnyArgs {
 template <int MR, bool VEC, bool NTL>
 __global__ void __launch_bounds__(SK_THREADS) gemm_skinny_kernel(SkinnyArgs p) {
     __shared__ f4 red[4][MR][64];
+    __shared__ float a_s[MR][SK_KC_MAX];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -67,6 +74,17 @@ __global__ void __launch_bounds__(SK_THREADS) gemm_skinny_kernel(SkinnyArgs p) {
     const int k_lo = min(ke, kb + w * per_wave);
     const int k_hi = min(ke, k_lo + per_wave);
 
+    // The slice of A (MR x (ke - kb) values) goes to LDS once: every lane reads all of it,
+    // and as per-element global loads it took 4 vector-memory instructions per row of B at
+    // M = 4, more than the B stream itself.
+    const int span = ke - kb;
+    for (int i = tid; i < MR * span; i += SK_THREADS) {
+        const int m = i / span;
+        const int kk = i - m * span;
+        a_s[m][kk] = Ab[m * p.a_rs + (int64_t)(kb + kk) * p.a_ks];
+    }
+    __syncthreads();
+
     // Columns beyond N read a clamped, in-bounds column; their sums are never stored.
     const float *colp = Bb + (VEC ? (n < p.N ? n : p.N - 4) : 0);
     int nc[4];
@@ -78,33 +96,48 @@ __global__ void __launch_bounds__(SK_THREADS) gemm_skinny_kernel(SkinnyArgs p) {
     for (int m = 0; m < MR; ++m) acc[m] = f4{0.f, 0.f, 0.f, 0.f};
 
     // Batches of SK_UNROLL rows: every load of a batch is issued before its FMAs, so each
-    // wavefront keeps SK_UNROLL x 1 KiB of B in flight.
-    for (int k0 = k_lo; k0 < k_hi; k0 += SK_UNROLL) {
+    // wavefront keeps SK_UNROLL x 1 KiB of B in flight. Full batches carry no bounds
+    // checks; the last, partial batch re-reads its final row and multiplies it by zero.
+    constexpr int SK_UNROLL = SkUnroll<MR>::value;
+    auto load_row = [&](int k) {
+        const float *rowp = colp + (int64_t)k * p.ldb;
+        f4 v;
+        if constexpr (VEC && NTL)
+            v = __builtin_nontemporal_load(reinterpret_cast<const f4u *>(rowp));
+        else if constexpr (VEC)
+            __builtin_memcpy(&v, rowp, sizeof(f4));
+        else
+            v = f4{rowp[nc[0]], rowp[nc[1]], rowp[nc[2]], rowp[nc[3]]};
+        return v;
+    };
+    int k0 = k_lo;
+    for (; k0 + SK_UNROLL <= k_hi; k0 += SK_UNROLL) {
         f4 v[SK_UNROLL];
 #pragma unroll
-        for (int u = 0; u < SK_UNROLL; ++u) {
-            const int k = min(k0 + u, k_hi - 1);
-            const float *rowp = colp + (int64_t)k * p.ldb;
-            if constexpr (VEC && NTL)
-                v[u] = __builtin_nontemporal_load(reinterpret_cast<const f4u *>(rowp));
-            else if constexpr (VEC)
-                __builtin_memcpy(&v[u], rowp, sizeof(f4));
-            else
-                v[u] = f4{rowp[nc[0]], rowp[nc[1]], rowp[nc[2]], rowp[nc[3]]};
-        }
+        for (int u = 0; u < SK_UNROLL; ++u) v[u] = load_row(k0 + u);
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            const float *ap = Ab + m * p.a_rs;
+        for (int u = 0; u < SK_UNROLL; ++u)
 #pragma unroll
-            for (int u = 0; u < SK_UNROLL; ++u) {
+            for (int m = 0; m < MR; ++m) {
+                const float a = a_s[m][k0 + u - kb];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[m][e] = __builtin_fmaf(a, v[u][e], acc[m][e]);
+            }
+    }
+    if (k0 < k_hi) {
+        f4 v[SK_UNROLL];
+#pragma unroll
+        for (int u = 0; u < SK_UNROLL; ++u) v[u] = load_row(min(k0 + u, k_hi - 1));
+#pragma unroll
+        for (int u = 0; u < SK_UNROLL; ++u)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
                 const bool ok = k0 + u < k_hi;
-                const int k = ok ? k0 + u : k_lo;
-                const float a = ok ? ap[(int64_t)k * p.a_ks] : 0.f;
+                const float a = ok ? a_s[m][k0 + u - kb] : 0.f;
                 const f4 vv = ok ? v[u] : f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[m][e] = __builtin_fmaf(a, vv[e], acc[m][e]);
             }
-        }
     }
 
 #pragma unroll
@@ -168,17 +201,18 @@ int launch_mr(hipStream_t st, const SkinnyArgs &a, bool vec, int batch) {
 }  // namespace
 
 bool skinny_supported(const GemmDesc &d) {
-    return d.M <= SK_MAXM && !d.transB && d.N >= 4 && d.batch <= 65535;
+    return d.M <= SK_MAXM && !d.transB && d.N >= 4 && d.batch <= 65535 &&
+           (int64_t)d.K <= (int64_t)65535 * 256;
 }
 
-// Streaming B pays once B is too large to sit in the caches, for one or two rows: from
-// 64 MB of B the kernel reads 4.8-6.4 TB/s at M = 1-2 (1 x 11008 x 4096: 32.7 us against
-// 60.9 in the small kernel; 1 x 32000 x 4096: 83.6 against 128.6; 2 x 4096 x 16384: 51.3
-// against 106.3). With 32 MB of B, or three or four rows, the small kernel is as fast or
-// faster (1 x 4096 x 2048: 15.3 against 12.1 us; 4 x 1024 x 8192: 24.2 against 14.2;
-// 4 x 11008 x 4096: 65.6 against 61.3).
+// Streaming B pays once B is too large to sit in the caches: from 64 MB of B the kernel
+// beats the small kernel at every M <= 4 (graph replay, rotating copies of B, us, skinny /
+// small: 1 x 11008 x 4096 32.2 / 60.6; 4 x 11008 x 4096 38.9 / 61.4; 2 x 8192 x 2048
+// 19.1 / 27.0; 3 x 4096 x 4096 16.7 / 23.9). At 32 MB they tie (1 x 4096 x 2048 12.0 /
+// 12.1; 4 x 4096 x 2048 14.9 / 12.3) and below that the small kernel wins (3 x 6565 x 500
+// 20.1 / 7.7).
 bool skinny_preferred(const GemmDesc &d) {
-    return skinny_supported(d) && d.M <= 2 && (int64_t)d.K * d.N * d.batch >= ((int64_t)16 << 20);
+    return skinny_supported(d) && (int64_t)d.K * d.N * d.batch >= ((int64_t)16 << 20);
 }
 
 int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {
@@ -209,14 +243,13 @@ int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {
         const char *v = getenv("MIGEMM_GEMV_KC");
         return v != nullptr ? atoi(v) : 0;
     }();
-    if (force_kc >= 4) kc = force_kc / 4 * 4;
+    if (force_kc >= 4) kc = (force_kc < SK_KC_MAX ? force_kc : SK_KC_MAX) / 4 * 4;
     if (kc >= d.K) kc = (d.K + 3) / 4 * 4;
     a.kc = kc;
     a.slices = (d.K + kc - 1) / kc;
-    if (a.slices > 65535) {
-        a.kc = ((d.K + 65534) / 65535 + 3) / 4 * 4;
-        a.slices = (d.K + a.kc - 1) / a.kc;
-    }
+    if (a.slices > 65535)  // K <= 65535 * SK_KC_MAX is part of skinny_supported
+        return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm_skinny: K=%d needs %d slices", d.K,
+                         a.slices);
     a.partial = nullptr;
     a.batch = d.batch;
     a.accumulate = d.accumulate;

@@ -40,7 +40,7 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d);
 int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d);
 // M <= 4 and B not transposed (the shapes gemm_skinny_kernel handles).
 bool skinny_supported(const GemmDesc &d);
-// Supported, M <= 2 and B large enough (>= 64 MB) for the streaming kernel to beat the others.
+// Supported and B large enough (>= 64 MB) for the streaming kernel to beat the others.
 bool skinny_preferred(const GemmDesc &d);
 int launch_gemm_small(hipStream_t stream, const GemmDesc &d);
 // True when C has too few 64x64 tiles to occupy the 256 CUs (gemm_small_kernel).
