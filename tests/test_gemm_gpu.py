@@ -505,3 +505,61 @@ def test_random_strided_batched_exact(nncl, policy):
             assert np.array_equal(got, expect.astype(np.float32)), (i, z, c)
             inside[s:s + M * c["ldc"]].reshape(M, c["ldc"])[:, :N] = True
         assert np.all(np.isnan(out[~inside])), (i, "write outside [M x N]", c)
+
+
+# ------------------------------------------------------------------- non-finite inputs
+def _special_pattern(A, B):
+    """IEEE classes of C = A B for small-integer A, B holding a few +-Inf / NaN entries:
+    (nan, +inf, -inf) masks and the exact finite values. A product is NaN when a factor is
+    NaN or an infinity meets a zero; a sum is NaN when it holds a NaN product or infinities
+    of both signs. The zero padding of partial tiles is 0 x 0 and changes nothing."""
+    M, K = A.shape
+    N = B.shape[1]
+    specA = ~np.isfinite(A)
+    specB = ~np.isfinite(B)
+    fin = (np.where(specA, 0, A).astype(np.float64) @ np.where(specB, 0, B).astype(np.float64))
+    nan = np.zeros((M, N), bool)
+    pos = np.zeros((M, N), bool)
+    neg = np.zeros((M, N), bool)
+
+    def add(i, j, a, b):  # a * b with at least one non-finite factor
+        if np.isnan(a) or np.isnan(b) or (np.isinf(a) and b == 0) or (np.isinf(b) and a == 0):
+            nan[i, j] = True
+        elif np.sign(a) * np.sign(b) > 0:
+            pos[i, j] = True
+        else:
+            neg[i, j] = True
+
+    for i, k in zip(*np.nonzero(specA)):
+        for j in range(N):
+            add(i, j, A[i, k], B[k, j])
+    for k, j in zip(*np.nonzero(specB)):
+        for i in range(M):
+            if not specA[i, k]:
+                add(i, j, A[i, k], B[k, j])
+    nan |= pos & neg
+    return nan, pos & ~nan, neg & ~nan, fin
+
+
+@pytest.mark.parametrize("M,K,N", [(3, 300, 40), (37, 45, 29), (200, 300, 260), (129, 4099, 131)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+def test_nonfinite_inputs_propagate(nncl, policy, M, K, N, ta, tb):
+    """+-Inf and NaN in A and B reach exactly the outputs IEEE arithmetic says they reach,
+    with the right class, on every kernel family (edge tiles, zero-filled k tails, k
+    splits); every other output is the exact small-integer product."""
+    say("nonfinite", policy, M, K, N, ta, tb)
+    rng = np.random.default_rng(M * 1000 + K + N)
+    A = rng.integers(-3, 4, size=(M, K)).astype(np.float32)
+    B = rng.integers(-3, 4, size=(K, N)).astype(np.float32)
+    for X, count in ((A, 3), (B, 3)):
+        idx = rng.choice(X.size, size=count, replace=False)
+        X.flat[idx] = np.array([np.inf, -np.inf, np.nan], np.float32)[:count]
+    nan, pos, neg, fin = _special_pattern(A, B)
+    An = np.ascontiguousarray(A.T) if ta else A
+    Bn = np.ascontiguousarray(B.T) if tb else B
+    got = gemm_gpu(nncl, An, Bn, bool(ta), bool(tb))
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(np.isposinf(got), pos)
+    assert np.array_equal(np.isneginf(got), neg)
+    ok = ~(nan | pos | neg)
+    assert np.array_equal(got[ok], fin[ok].astype(np.float32))
