@@ -278,6 +278,7 @@ void oracle_linear_bias_backward(const float *grad_output, float *grad_bias, int
 void oracle_gemm_f64(int transA, int transB, int M, int N, int K, const float *A, int64_t lda,
                      int64_t sA, const float *B, int64_t ldb, int64_t sB, const float *bias,
                      double *C, int batch, int row0, int row1) {
+    (void)M; /* rows come from [row0, row1) */
     for (int z = 0; z < batch; ++z) {
         const float *a = A + (int64_t)z * sA;
         const float *b = B + (int64_t)z * sB;
@@ -304,6 +305,7 @@ void oracle_gemm_f64(int transA, int transB, int M, int N, int K, const float *A
 void oracle_gemm_absprod(int transA, int transB, int M, int N, int K, const float *A,
                          int64_t lda, int64_t sA, const float *B, int64_t ldb, int64_t sB,
                          const float *bias, double *C, int batch, int row0, int row1) {
+    (void)M; /* rows come from [row0, row1) */
     for (int z = 0; z < batch; ++z) {
         const float *a = A + (int64_t)z * sA;
         const float *b = B + (int64_t)z * sB;

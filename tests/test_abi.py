@@ -161,3 +161,12 @@ def test_host_api_rejects_cpu_tensors_loudly():
         g.Bmm(a, b)
     with pytest.raises(AssertionError):  # the Python reference asserts
         g.bmm(a, b)
+
+
+def test_c_caller_compiles_and_validates_without_gpu():
+    """include/migemm.h compiles as strict C99 and a C program linked against libmigemm.so
+    gets the argument errors, with messages, without a GPU (tests/c_abi_check.c)."""
+    import c_abi
+    r = c_abi.run("validate")
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "c_abi_check validate: ok" in r.stdout

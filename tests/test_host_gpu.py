@@ -229,3 +229,14 @@ def test_shape_errors_before_launch(nncl):
         nncl.BmmPermute(a, dev(np.zeros((2, 5, 3), np.float32)), transB=True)
     with pytest.raises(ShapeError):
         nncl.Permute(a, [0, 1])
+
+
+def test_c_caller_on_the_gpu():
+    """A plain C99 program (no torch, no Python: the way the C# host would call the library)
+    allocates, copies, runs the GEMM entry points on GPU 0 and checks them exactly
+    (tests/c_abi_check.c). It runs as a child process."""
+    import c_abi
+    say("c_abi_check gpu")
+    r = c_abi.run("gpu")
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "c_abi_check gpu: ok" in r.stdout
