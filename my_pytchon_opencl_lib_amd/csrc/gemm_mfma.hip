@@ -627,13 +627,24 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     // 128x4096x4096 64x64 with 4 / 5 / 8 / 16 ranges: 49.2 / 55.0 / 47.9 / 51.5;
     // 512x16384x512 TN with 5 / 8 / 10: 119.9 / 78.4 / 91.0.
     int cfg, splits = 1;
+    int big = 0;  // 128x128 tiles; 1: 128x256, 2: 256x256 (see below)
     if (tiles(128, 128) >= 512) {
         cfg = 128;
     } else if (d.K >= 4096 && d.M >= 128 && d.N >= 128 && tiles(128, 128) >= 128) {
         cfg = 128;
-        int64_t want = (1024 + tiles(128, 128) - 1) / tiles(128, 128);
-        want += want & 1;
-        splits = (int)(want < 8 ? want : 8);
+        const int64_t t256 = tiles(256, 256);
+        if (av && bv && (t256 == 32 || t256 == 64)) {
+            // 256x256 tiles split into exactly one work-group per CU (512 x 6400 x 4096 TN
+            // 225.7 -> 213.2 us, 1024 x 6400 x 4096 TN 425.3 -> 395.8, 4096 x 4096 x 1024
+            // 278.6 -> 265.8); with fewer tiles, or a count that does not divide the CUs,
+            // the 128x128 split stays faster (768 x 4096 x 3072: 182.3 against 264.2)
+            big = 2;
+            splits = (int)(256 / t256);
+        } else {
+            int64_t want = (1024 + tiles(128, 128) - 1) / tiles(128, 128);
+            want += want & 1;
+            splits = (int)(want < 8 ? want : 8);
+        }
     } else if (tiles(64, 64) >= 256 || nk32 < 8) {
         cfg = tiles(64, 64) >= 256 ? 64 : 32;
         // About one tile per CU (one wavefront per SIMD) with a long k loop, or a few tiles
@@ -662,7 +673,6 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     // fills its CU alone, so its prologue and epilogue (the C store) are not overlapped by
     // another work-group: they cost about 32 k-steps' worth per tile (16 for 128x256, 2 per
     // CU), which decides short K: 12000 x 6565 x 500 runs 729 us at 128x128, 747 at 256x256.
-    int big = 0;  // 0: 128x128, 1: 128x256, 2: 256x256
     if (cfg == 128 && splits == 1) {
         const double k = d.K;
         const double c0 = (double)((tiles(128, 128) + 255) / 256) * 16384.0 * k / 0.966;

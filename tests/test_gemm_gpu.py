@@ -378,11 +378,13 @@ def test_large_tile_shapes_exact(nncl, forced_tile, M, K, N, ta, tb):
     assert np.array_equal(got, expect)
 
 
-@pytest.mark.parametrize("M,K,N", [(300, 5000, 200), (129, 4099, 131), (500, 12000, 700)])
+@pytest.mark.parametrize("M,K,N", [(300, 5000, 200), (129, 4099, 131), (500, 12000, 700),
+                                   (512, 4100, 4096), (1024, 4108, 2048), (768, 4096, 3072)])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_long_k_split_tiles_exact(nncl, M, K, N, ta, tb):
-    """Long K with few 128x128 tiles: 128x128 tiles with K split into ranges (ragged M, N
-    and a K tail in the last range); exact small-integer products."""
+    """Long K with few tiles, split into k ranges: 64x64 tiles (ragged M, N and a K tail in
+    the last range), 256x256 tiles with one work-group per CU (512 x 4100 x 4096, 1024 x
+    4108 x 2048) and 128x128 tiles (768 x 4096 x 3072); exact small-integer products."""
     say("long-K split exact", M, K, N, ta, tb)
     A = small_ints((K, M) if ta else (M, K), M + 2 * K, -2, 2)
     B = small_ints((N, K) if tb else (K, N), N + 2 * K, -2, 2)
