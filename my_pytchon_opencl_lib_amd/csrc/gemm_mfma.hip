@@ -37,6 +37,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "migemm_internal.h"
@@ -667,18 +668,36 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         }
     }
     // Large outputs: pick the macro-tile by the busiest CU's share of the work. The work-
-    // groups are dealt over the 256 CUs, so a CU carries ceil(tiles / 256) tiles of area x K
-    // multiply-adds; the factor is each shape's measured MFMA efficiency at 4096^3 (256x256:
-    // 143.8, 128x256: 141.1, 128x128: 138.9 TFLOP/s over NN / NT / TN). A 256x256 work-group
-    // fills its CU alone, so its prologue and epilogue (the C store) are not overlapped by
-    // another work-group: they cost about 32 k-steps' worth per tile (16 for 128x256, 2 per
-    // CU), which decides short K: 12000 x 6565 x 500 runs 729 us at 128x128, 747 at 256x256.
+    // groups are dealt over the 256 CUs, so a CU carries ceil(tiles / 256) tiles of area x
+    // (K + a per-tile overhead), at each tile's own rate. With 128-bit loads of both operands
+    // the rates and overheads are fitted to NN at 4096 x K x 4096, K = 512 .. 4096 (TFLOP/s
+    // x K / (K + o)): 256x256 147.2, o = 73; 128x256 140.6, o = 99; 128x128 138.9, o = 78;
+    // 64x64 134.2, o = 75. The tile count's quantization then decides: 3072 x 1024 x 3072
+    // runs 119.4 TFLOP/s in 64x64 tiles (9 per CU) against 96.7 in 128x128 (2.25 per CU);
+    // 4096 x 512 x 4096 128.9 in 256x256 against 120.6. Element-wise loads (M, N or K not a
+    // multiple of 4) keep the earlier three-shape model: 256x256 work-groups fill a CU alone,
+    // their prologue and C store not overlapped (about 32 k-steps per tile, 16 for 128x256),
+    // which decides short K: 12000 x 6565 x 500 runs 729 us at 128x128, 747 at 256x256.
     if (cfg == 128 && splits == 1) {
         const double k = d.K;
-        const double c0 = (double)((tiles(128, 128) + 255) / 256) * 16384.0 * k / 0.966;
-        const double c1 = (double)((tiles(128, 256) + 255) / 256) * 32768.0 * (k + 16) / 0.981;
-        const double c2 = (double)((tiles(256, 256) + 255) / 256) * 65536.0 * (k + 32);
-        big = c2 <= c1 && c2 <= c0 ? 2 : (c1 <= c0 ? 1 : 0);
+        auto cost = [&](int bm, int bn, double rate, double over) {
+            return (double)((tiles(bm, bn) + 255) / 256) * bm * bn * (k + over) / rate;
+        };
+        if (av && bv) {
+            const double c64 = cost(64, 64, 134.2, 75), c0 = cost(128, 128, 138.9, 78);
+            const double c1 = cost(128, 256, 140.6, 99), c2 = cost(256, 256, 147.2, 73);
+            const double best = std::min(std::min(c64, c0), std::min(c1, c2));
+            if (best == c2)
+                big = 2;
+            else if (best == c1)
+                big = 1;
+            else if (best == c64)
+                cfg = 64;
+        } else {
+            const double c0 = cost(128, 128, 0.966, 0), c1 = cost(128, 256, 0.981, 16);
+            const double c2 = cost(256, 256, 1.0, 32);
+            big = c2 <= c1 && c2 <= c0 ? 2 : (c1 <= c0 ? 1 : 0);
+        }
     }
     // read per call, so a tuning sweep can change them between calls in one process;
     // MIGEMM_TILE = 32 | 64 | 128 | 128x256 | 256
