@@ -185,7 +185,7 @@ def main():
                    "M": n, "N": n, "K": n, "forms": per_form,
                    "pct_of_fp32_matrix_peak": round(100 * value / PEAK_FP32_MFMA_TFLOPS, 2),
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": f"gemm_mfma_kernel ({dominant} form)",
+        "roofline": {"bound": "mfma", "kernel": f"{tiled_kernel_name()} ({dominant} form)",
                      "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
                      "traffic": load_traffic(dominant)},
@@ -213,11 +213,20 @@ def pmc_target(torch, nncl):
     print("pmc target done", flush=True)
 
 
+def tiled_kernel_name():
+    """The kernel that runs the 4096^3 forms: 256x256 tiles with operands loaded straight
+    into LDS, unless MIGEMM_DIRECT=0 selects the register-staged kernel."""
+    return "gemm_mfma_kernel" if os.environ.get("MIGEMM_DIRECT", "1") == "0" else \
+        "gemm_direct_kernel"
+
+
 def load_traffic(kernel_substr):
     """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, each
     scaled by the copy-kernel factor) for the dominant kernel, from the committed profile
     summary; None when no summary covers that kernel."""
-    path = os.path.join(ROOT, "profiles", "gemm_mfma_4096_pmc.md")
+    name = "gemm_mfma_4096_pmc.md" if tiled_kernel_name() == "gemm_mfma_kernel" else \
+        "gemm_direct_4096_pmc.md"
+    path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
     for line in open(path):

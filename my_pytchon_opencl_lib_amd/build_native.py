@@ -11,7 +11,7 @@ import sys
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_PATH = os.path.join(PKG_DIR, "libmigemm.so")
-SOURCES = ["api.hip", "gemm_mfma.hip", "gemm_small.hip", "gemm_skinny.hip", "aux_kernels.hip"]
+SOURCES = ["api.hip", "gemm_mfma.hip", "gemm_direct.hip", "gemm_small.hip", "gemm_skinny.hip", "aux_kernels.hip"]
 ARCH = "gfx950"
 
 

@@ -1,0 +1,369 @@
+// Tiled fp32 GEMM for gfx950 with operands loaded straight from global memory into LDS.
+//
+// The same product as gemm_mfma_kernel (matmul.cl:8-135 NN, bmm_permute_tiled.cl NT / TN,
+// the bias epilogue of linear.cl:119-122) for 256x256 output tiles whose operands allow
+// 128-bit loads everywhere (every contiguous extent a multiple of 4). It differs in how the
+// operands reach LDS:
+//  * global_load_lds_dwordx4 (gfx950) moves each lane's 16 bytes from global memory to LDS
+//    without passing through registers. One wavefront instruction fills 1 KB of LDS: lane L's
+//    bytes land at M0 + 16 L. The kernel holds no staging registers, which leaves room for
+//    BK = 32 k-tiles (the register-staged kernel spills at BK = 32 with an I-contiguous
+//    operand) and for the next k-group's fragments.
+//  * S LDS stages, loads D tiles ahead (shipped: BK = 32, S = D = 2; 2 x 130 KB). Every
+//    fragment read of a tile's stage is issued before the tile's one barrier, so the
+//    barrier (1) publishes tile kt+1, for which each wavefront first waits with
+//    s_waitcnt vmcnt (the compiler does not track these loads), and (2) retires the stage
+//    just read, which the loads of tile kt+D then reuse. The last k-group's MFMAs follow the
+//    barrier, and the first MFMAs of tile kt+1 follow them without a barrier in between.
+//  * LDS layouts (per stage, unpadded where a wavefront's 1 KB write must be contiguous):
+//      K-contiguous operand (A not transposed, B transposed): 256 rows x BK k, row r at
+//        BK r floats. Chunk c (4 floats) of row r is stored in slot c ^ kc_swz(r), so a
+//        16-lane phase of an MFMA fragment read (16 consecutive rows, one chunk each) hits
+//        16 distinct 16-byte bank groups. A load instruction covers 64 / (BK / 4) whole rows
+//        and each lane fetches the chunk that belongs in its slot.
+//      I-contiguous operand (A transposed, B not transposed): BK k-rows of 256 floats, row k
+//        at k * 264 floats (one load instruction per k-row; the 8-float pad keeps the two
+//        half-wavefronts of a fragment read, k-rows 4 apart, on different banks).
+//  * Edges: rows / columns beyond M / N are clamped on load (they feed outputs that are not
+//    stored); the k tail (K % BK != 0) is fetched through registers with k >= K zero-filled
+//    (matmul.cl:39-52) into the same layout, after the pipelined loop.
+//  * K order within an MFMA step, split-K ranges, the XCD-aware raster and the epilogue are
+//    those of gemm_mfma_kernel (tiled_common.h); each output's k sum runs in the same order
+//    as in gemm_mfma_kernel, so both give identical bits for one split.
+#include <stdlib.h>
+
+#include "tiled_common.h"
+
+namespace migemm {
+namespace {
+
+constexpr int DT = 256;      // macro-tile edge (BM = BN)
+constexpr int DPAD_I = 8;    // pad of an I-contiguous LDS row
+
+// s_waitcnt vmcnt(N) with expcnt and lgkmcnt left at their maxima (N < 16).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 16, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+template <int BK, bool KC>
+struct DlTileFloats {
+    static constexpr int value = KC ? DT * BK : BK * (DT + DPAD_I);
+};
+
+typedef __attribute__((address_space(3))) float *lds_ptr_t;
+
+// global_load_lds_dwordx4 in its scalar-base form: each lane's 16 bytes at sbase + voff go
+// to LDS at `dst` + 16 * lane (dst wave-uniform, through M0). Written as inline assembly
+// rather than __builtin_amdgcn_global_load_lds: with the builtin the compiler made every
+// later LDS read wait for all outstanding LDS loads (s_waitcnt vmcnt(0)), which serializes
+// the pipeline. The kernel orders these loads itself: each wavefront waits for its own with
+// s_waitcnt vmcnt before the barrier that publishes them. Nothing else in the kernels of
+// this file uses M0 (checked in the generated code).
+__device__ __forceinline__ void dma16(const char *sbase, uint32_t voff, float *dst) {
+    const uint32_t lds = (uint32_t)(uintptr_t)(lds_ptr_t)dst;
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ f4 dl_load16(const float *p) {
+    f4 v;
+    __builtin_memcpy(&v, p, sizeof(v));
+    return v;
+}
+
+// K-contiguous LDS tile: rows of BK floats (CPR = BK / 4 chunks of 16 bytes), unpadded.
+// Chunk c of row r is stored in slot c ^ kc_swz(r). A fragment read phase covers 16
+// consecutive rows at one chunk; kc_swz spreads them over the 16 bank groups of 16 bytes:
+// BK = 16: (r / 4) % 4, BK = 32: (r / 2) % 8.
+template <int BK>
+__device__ __forceinline__ int kc_swz(int r) {
+    constexpr int CPR = BK / 4;
+    return (r / (16 / CPR)) % CPR;
+}
+
+// One operand of a 256 x BK tile. NS = load instructions (1 KB each) per wavefront per
+// tile. KC: instruction q covers tile rows RPI*q .. RPI*q + RPI - 1 (RPI = 64 / CPR rows of
+// CPR chunks); otherwise k-row q (256 floats). The loads address memory as a wave-uniform
+// base (the tile's first row / column at k-tile 0, advanced per k-tile in scalar registers)
+// plus a 32-bit per-lane byte offset, which keeps the per-lane state to one register per
+// instruction; the launcher checks that the offsets fit.
+template <int NT, bool KC, int BK>
+struct DlOperand {
+    static constexpr int NW = NT / 64;
+    static constexpr int NI = BK;  // load instructions per tile: 256 * BK floats / 256
+    static constexpr int NS = NI / NW;
+    static_assert(NS * NW == NI, "the tile's loads split evenly over the wavefronts");
+    static constexpr int CPR = BK / 4;
+    static constexpr int RPI = 64 / CPR;
+    const char *base;      // wave-uniform: element (i0, 0) of the operand
+    uint32_t voff[NS];     // this lane's byte offset from `base` at k-tile 0
+    int q0;                // first instruction of this wavefront (wave-uniform)
+    int c[NS];             // KC: the logical chunk this lane fetches per instruction
+
+    __device__ __forceinline__ void init(const float *op, int64_t ld, int i0, int rows,
+                                         int wave, int lane) {
+        q0 = wave * NS;
+        base = reinterpret_cast<const char *>(op + (KC ? (int64_t)i0 * ld : (int64_t)i0));
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+            const int q = q0 + j;
+            if constexpr (KC) {
+                const int r = RPI * q + lane / CPR;  // tile row
+                c[j] = (lane % CPR) ^ kc_swz<BK>(r);
+                int gi = i0 + r;
+                gi = gi < rows ? gi : rows - 1;
+                voff[j] = (uint32_t)(((gi - i0) * (uint32_t)ld + 4 * c[j]) * 4);
+            } else {
+                c[j] = 0;
+                int gi = i0 + 4 * lane;
+                gi = gi < rows ? gi : rows - 4;
+                voff[j] = (uint32_t)((q * (uint32_t)ld + (gi - i0)) * 4);
+            }
+        }
+    }
+
+    __device__ __forceinline__ int lds_off(int j) const {
+        return KC ? (q0 + j) * 256 : (q0 + j) * (DT + DPAD_I);
+    }
+
+    __device__ __forceinline__ const char *tile_base(int kt, int64_t ld) const {
+        return base + (KC ? (int64_t)kt * BK * 4 : (int64_t)kt * BK * ld * 4);
+    }
+
+    // Full k-tile kt straight into `stage`.
+    __device__ __forceinline__ void issue(float *stage, int kt, int64_t ld) const {
+        const char *tb = tile_base(kt, ld);
+#pragma unroll
+        for (int j = 0; j < NS; ++j) dma16(tb, voff[j], stage + lds_off(j));
+    }
+
+    // The tail tile kt (k0 = BK kt, k0 + BK > K) through registers, k >= K zero-filled,
+    // written where the direct load would have put it.
+    __device__ __forceinline__ void tail(float *stage, int kt, int K, int64_t ld,
+                                         int lane) const {
+        const int k0 = kt * BK;
+        const char *tb = tile_base(kt, ld);
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+            f4 v = {0.f, 0.f, 0.f, 0.f};
+            const float *src = reinterpret_cast<const float *>(tb + voff[j]);
+            if constexpr (KC) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (k0 + 4 * c[j] + e < K) v[e] = src[e];
+            } else {
+                if (k0 + q0 + j < K) v = dl_load16(src);
+            }
+            *reinterpret_cast<f4 *>(stage + lds_off(j) + 4 * lane) = v;
+        }
+    }
+};
+
+// Fragments of k-group g (8 consecutive k of the tile) for F blocks of 32 rows from `off`:
+// fr[f][s] is this lane's operand for MFMA step s (lanes 0-31: k = 8g + s, lanes 32-63:
+// k = 8g + 4 + s).
+template <bool KC, int BK, int F>
+__device__ __forceinline__ void dl_frags(const float *lds, int off, int g, int lane,
+                                         f4 (&fr)[F]) {
+    const int lo = lane & 31;
+    const int hi = lane >> 5;
+    if constexpr (KC) {
+        const int slot = (2 * g + hi) ^ kc_swz<BK>(lo);  // off + 32 f keeps kc_swz(r)
+#pragma unroll
+        for (int f = 0; f < F; ++f)
+            fr[f] = *reinterpret_cast<const f4 *>(lds + (off + f * 32 + lo) * BK + 4 * slot);
+    } else {
+#pragma unroll
+        for (int f = 0; f < F; ++f)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                fr[f][s] = lds[(8 * g + 4 * hi + s) * (DT + DPAD_I) + off + f * 32 + lo];
+    }
+}
+
+// S LDS stages; tile kt lives in stage (kt - kt0) % S and is loaded D (<= S) tiles ahead.
+template <int WM, int WN, bool AKC, bool BKC, int BK, int S, int D>
+__global__ void __launch_bounds__(WM *WN * 64)
+gemm_direct_kernel(TiledArgs p) {
+    static_assert(D >= 2 && D <= S, "loads run 2..S tiles ahead");
+    constexpr int NT = WM * WN * 64;
+    constexpr int WTM = DT / WM;
+    constexpr int WTN = DT / WN;
+    constexpr int FM = WTM / 32;
+    constexpr int FN = WTN / 32;
+    constexpr int G = BK / 8;  // k-groups per tile
+    static_assert(FM >= 1 && FN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "bad wave tile");
+    constexpr int A_FL = DlTileFloats<BK, AKC>::value;
+    constexpr int B_FL = DlTileFloats<BK, BKC>::value;
+    // One array per operand, so each wavefront reads every stage of an operand from one
+    // base register with immediate offsets (the stages of one operand span < 64 KB).
+    __shared__ __attribute__((aligned(16))) float lds_a[S * A_FL];
+    __shared__ __attribute__((aligned(16))) float lds_b[S * B_FL];
+    typedef DlOperand<NT, AKC, BK> OpA;
+    typedef DlOperand<NT, BKC, BK> OpB;
+    constexpr int LPT = OpA::NS + OpB::NS;  // load instructions per tile per wavefront
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN;
+    const int wn = wave % WN;
+
+    // The tile mapping divides in VALU registers; the results are wave-uniform, and keeping
+    // them (and everything derived from them: k-tile indices, load bases) in scalar
+    // registers leaves the vector registers to the accumulators and fragments.
+    TileCoord tc = tile_coord<DT, DT>(p, blockIdx.x);
+    tc.split = __builtin_amdgcn_readfirstlane(tc.split);
+    tc.b = __builtin_amdgcn_readfirstlane(tc.b);
+    tc.m0 = __builtin_amdgcn_readfirstlane(tc.m0);
+    tc.n0 = __builtin_amdgcn_readfirstlane(tc.n0);
+    const float *Ab = p.A + (int64_t)tc.b * p.sA;
+    const float *Bb = p.B + (int64_t)tc.b * p.sB;
+
+    OpA opa;
+    OpB opb;
+    opa.init(Ab, p.lda, tc.m0, p.M, wave, lane);
+    opb.init(Bb, p.ldb, tc.n0, p.N, wave, lane);
+
+    f16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int K = p.K;
+    const int kt0 = tc.split * p.kt_per_split;
+    const int kt1 = min((K + BK - 1) / BK, kt0 + p.kt_per_split);
+    const int kf = min(kt1, K / BK);  // end of the full k-tiles of this range
+
+    auto issue = [&](int kt, int st) {
+        opa.issue(lds_a + st * A_FL, kt, p.lda);
+        opb.issue(lds_b + st * B_FL, kt, p.ldb);
+    };
+    auto frags = [&](int st, int g, f4(&fa)[FM], f4(&fb)[FN]) {
+        dl_frags<AKC, BK, FM>(lds_a + st * A_FL, wm * WTM, g, lane, fa);
+        dl_frags<BKC, BK, FN>(lds_b + st * B_FL, wn * WTN, g, lane, fb);
+    };
+    auto mfmas = [&](const f4(&fa)[FM], const f4(&fb)[FN]) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s],
+                                                                     acc[i][j], 0, 0, 0);
+    };
+    // Tile kt out of stage ST: every fragment read of the stage is issued before the
+    // barrier, which (1) publishes tile kt+1 (each wavefront first waits for its own loads
+    // of it; the D-2 tiles issued after it may stay in flight) and (2) retires the stage of
+    // tile kt+D-S, so the loads of tile kt+D can go there. The last k-group's MFMAs follow
+    // the barrier, and the first of tile kt+1 follow them with no barrier in between.
+    auto step = [&](int kt, auto st) {
+        constexpr int ST = decltype(st)::value;
+        f4 fa[2][FM], fb[2][FN];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            frags(ST, g, fa[g & 1], fb[g & 1]);
+            if (g > 0) mfmas(fa[(g - 1) & 1], fb[(g - 1) & 1]);
+        }
+        if constexpr (D > 2) {
+            if (kt + D - 1 < kf)
+                wait_vmcnt<(D - 2) * LPT>();
+            else
+                wait_vmcnt<0>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        __syncthreads();
+        if (kt + D < kf) issue(kt + D, (ST + D) % S);
+        mfmas(fa[(G - 1) & 1], fb[(G - 1) & 1]);
+    };
+
+    int kt = kt0;
+    if (kt0 < kf) {
+#pragma unroll
+        for (int t = 0; t < D; ++t)
+            if (kt0 + t < kf) issue(kt0 + t, t);
+        if (kt0 + D - 1 < kf)
+            wait_vmcnt<(D - 1) * LPT>();
+        else
+            wait_vmcnt<0>();
+        __syncthreads();
+        // S steps per pass, so every stage index is a compile-time constant
+        for (; kt + S - 1 < kf; kt += S) {
+            step(kt, std::integral_constant<int, 0>{});
+            step(kt + 1, std::integral_constant<int, 1 % S>{});
+            if constexpr (S > 2) step(kt + 2, std::integral_constant<int, 2 % S>{});
+            if constexpr (S > 3) step(kt + 3, std::integral_constant<int, 3 % S>{});
+        }
+        if (kt < kf) step(kt++, std::integral_constant<int, 0>{});
+        if constexpr (S > 2)
+            if (kt < kf) step(kt++, std::integral_constant<int, 1 % S>{});
+        if constexpr (S > 3)
+            if (kt < kf) step(kt++, std::integral_constant<int, 2 % S>{});
+    }
+    wait_vmcnt<0>();  // no load into LDS outlives the loop
+    if (kt < kt1) {  // the tail tile: k >= K zero-filled in both operands
+        __syncthreads();  // every wavefront is done reading the stages
+        opa.tail(lds_a, kt, K, p.lda, lane);
+        opb.tail(lds_b, kt, K, p.ldb, lane);
+        __syncthreads();
+        f4 fa[FM], fb[FN];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            frags(0, g, fa, fb);
+            mfmas(fa, fb);
+        }
+    }
+    store_tile<FM, FN>(p, tc, tc.m0 + wm * WTM, tc.n0 + wn * WTN, lane, acc);
+}
+
+template <int WM, int WN, bool AKC, bool BKC, int BK, int S, int D>
+int launch_direct(hipStream_t s, TiledArgs &a) {
+    a.tiles_m = (a.M + DT - 1) / DT;
+    a.tiles_n = (a.N + DT - 1) / DT;
+    const int nk = (a.K + BK - 1) / BK;
+    const int want = a.splits < nk ? a.splits : nk;
+    a.kt_per_split = (nk + want - 1) / want;
+    a.splits = (nk + a.kt_per_split - 1) / a.kt_per_split;
+    const int64_t total = (int64_t)a.tiles_m * a.tiles_n * a.batch * a.splits;
+    if (total > INT32_MAX)
+        return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm: %lld tiles exceed one launch",
+                         (long long)total);
+    a.total = (int)total;
+    hipLaunchKernelGGL((gemm_direct_kernel<WM, WN, AKC, BKC, BK, S, D>), dim3(a.total),
+                       dim3(WM * WN * 64), 0, s, a);
+    return hip_check(hipGetLastError(), "gemm_direct_kernel launch");
+}
+
+// Every operand layout (NN, NT, TN, TT) runs 16 wavefronts of 32x128.
+template <int BK, int S, int D>
+int launch_layouts(hipStream_t s, TiledArgs &a, bool akc, bool bkc) {
+    if (akc && bkc) return launch_direct<8, 2, true, true, BK, S, D>(s, a);
+    if (akc) return launch_direct<8, 2, true, false, BK, S, D>(s, a);
+    if (!bkc) return launch_direct<8, 2, false, false, BK, S, D>(s, a);
+    return launch_direct<8, 2, false, true, BK, S, D>(s, a);
+}
+
+}  // namespace
+
+int launch_gemm_direct(hipStream_t stream, TiledArgs &a, bool akc, bool bkc) {
+    // BK = 32 with two stages, loads two tiles ahead (2 x 130 KB of LDS, one barrier per 32
+    // k). Measured at 4096^3 against BK = 16 with three stages (the alternative kept under
+    // MIGEMM_DVAR=1, read per call), interleaved in one process, TFLOP/s NN / NT / TN:
+    // 148.2 / 150.9 / 147.4 against 148.0 / 150.3 / 147.8; with loads three tiles ahead
+    // (three stages) 146.7 / 150.0 / 143.4; four stages 145.9 / 149.9 / 142.9; TN with 8
+    // wavefronts of 64x128 144.3-145.5. The register-staged kernel: 144.6 / 147.7 / 143.0.
+    const char *v = getenv("MIGEMM_DVAR");
+    if (v != nullptr && atoi(v) == 1) return launch_layouts<16, 3, 2>(stream, a, akc, bkc);
+    return launch_layouts<32, 2, 2>(stream, a, akc, bkc);
+}
+
+}  // namespace migemm

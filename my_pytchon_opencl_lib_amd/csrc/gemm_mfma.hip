@@ -40,30 +40,10 @@
 #include <algorithm>
 #include <type_traits>
 
-#include "migemm_internal.h"
+#include "tiled_common.h"
 
 namespace migemm {
 namespace {
-
-typedef float f4 __attribute__((ext_vector_type(4)));
-typedef float f16 __attribute__((ext_vector_type(16)));
-
-struct TiledArgs {
-    const float *A;
-    const float *B;
-    const float *bias;
-    float *C;
-    int64_t lda, ldb, ldc;
-    int64_t sA, sB, sC;
-    int M, N, K;
-    int tiles_m, tiles_n;  // tiles per batch entry
-    int batch;
-    int total;             // tiles_m * tiles_n * batch * splits
-    int splits;            // split-K ranges (1 = no split)
-    int kt_per_split;      // k-tiles per range
-    float *partial;        // [splits][batch][M][N] partial sums when splits > 1
-    int accumulate;        // C += result instead of C = result
-};
 
 constexpr int PAD_K = 4;  // pad of a K-contiguous LDS tile row [i][BK + 4]
 constexpr int PAD_I = 8;  // pad of an I-contiguous LDS tile row [k][T + 8]
@@ -253,24 +233,11 @@ gemm_mfma_kernel(TiledArgs p) {
     const int wm = wave / WN;
     const int wn = wave % WN;
 
-    // ---- work-group -> (batch, tile) with XCD-contiguous chunks and grouped raster ----
-    int pid = blockIdx.x;
-    const int total = p.total;
-    if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
-    const int per_batch = p.tiles_m * p.tiles_n;
-    const int per_split = per_batch * p.batch;
-    const int split = pid / per_split;
-    pid -= split * per_split;
-    const int b = pid / per_batch;
-    const int t = pid - b * per_batch;
-    constexpr int GROUP = 8;
-    const int in_group = GROUP * p.tiles_n;
-    const int first_m = (t / in_group) * GROUP;
-    const int gsz = min(p.tiles_m - first_m, GROUP);
-    const int tm = first_m + (t % in_group) % gsz;
-    const int tn = (t % in_group) / gsz;
-    const int m0 = tm * BM;
-    const int n0 = tn * BN;
+    const TileCoord tc = tile_coord<BM, BN>(p, blockIdx.x);
+    const int split = tc.split;
+    const int b = tc.b;
+    const int m0 = tc.m0;
+    const int n0 = tc.n0;
 
     const float *Ab = p.A + (int64_t)b * p.sA;
     const float *Bb = p.B + (int64_t)b * p.sB;
@@ -376,57 +343,7 @@ gemm_mfma_kernel(TiledArgs p) {
         for (int g = 0; g < BK / 8; ++g) group(smem, g);
     }
 
-    // ---- epilogue: accumulator (i, j) register r holds C row 8*(r/4) + 4*(lane/32) +
-    // r%4, column lane%32 of its 32x32 block; bias is added after the k loop ----
-    const int lo = lane & 31;
-    const int hi = lane >> 5;
-    if (p.splits > 1) {
-        float *Pb = p.partial + ((int64_t)split * p.batch + b) * p.M * p.N;
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int col = n0 + wn * WTN + j * 32 + lo;
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
-                    if (col < p.N && row < p.M) Pb[(int64_t)row * p.N + col] = acc[i][j][r];
-                }
-        }
-        return;
-    }
-    float *Cb = p.C + (int64_t)b * p.sC;
-    // Two copies of the store loop behind a uniform branch, so the plain store never
-    // carries a (speculated) load of C.
-    auto store = [&](auto accumulate) {
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int col = n0 + wn * WTN + j * 32 + lo;
-            const bool cok = col < p.N;
-            float bv = 0.f;
-            if (p.bias != nullptr && cok) bv = p.bias[col];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
-                    if (cok && row < p.M) {
-                        float v = acc[i][j][r];
-                        if (p.bias != nullptr) v = v + bv;
-                        float *c = Cb + (int64_t)row * p.ldc + col;
-                        if constexpr (decltype(accumulate)::value)
-                            *c = *c + v;
-                        else
-                            *c = v;
-                    }
-                }
-            }
-        }
-    };
-    if (p.accumulate)
-        store(std::true_type{});
-    else
-        store(std::false_type{});
+    store_tile<FM, FN>(p, tc, m0 + wm * WTM, n0 + wn * WTN, lane, acc);
 }
 
 // C_b[m, n] = partial[0][b][m][n] + ... + partial[S-1][b][m][n] (+ bias[n]), added in
@@ -580,6 +497,18 @@ int env_int(const char *name) {
 int lds_pad_bytes() {
     static const int pad = env_int("MIGEMM_LDS_PAD");
     return pad > 0 && pad <= 65536 ? pad : 0;
+}
+// 256x256 tiles use gemm_direct_kernel unless MIGEMM_DIRECT=0 (read per call, for
+// interleaved comparisons in one process) when its loads apply: every row and batch entry of
+// both operands starts on a 16-byte boundary (the loads into LDS move aligned 16-byte
+// pieces), and a lane's offset within a 256-row panel fits the loads' 32-bit offsets.
+bool direct_loads(const GemmDesc &d) {
+    const char *v = getenv("MIGEMM_DIRECT");
+    if (v != nullptr && atoi(v) == 0) return false;
+    auto ok = [](const float *p, int64_t ld, int64_t stride) {
+        return ((uintptr_t)p & 15) == 0 && ld % 4 == 0 && stride % 4 == 0 && ld <= (1 << 21);
+    };
+    return ok(d.A, d.lda, d.sA) && ok(d.B, d.ldb, d.sB);
 }
 }  // namespace
 
@@ -755,7 +684,9 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
                 // I-contiguous) runs 8 wavefronts of 64x128 (2 per SIMD, ~220 VGPRs): 143.2
                 // against 142.5 at 4096^3, 145.9 against 144.3 at 8192^3; NN and NT are
                 // slower that way (142.7 / 143.0).
-                if (big == 2 && akc && bkc)
+                if (big == 2 && av && bv && direct_loads(d))
+                    rc = launch_gemm_direct(stream, a, akc, bkc);
+                else if (big == 2 && akc && bkc)
                     rc = launch_tiles<256, 256, 32, 8, 2, 3>(stream, a, akc, bkc, av, bv);
                 else if (big == 2 && !akc && !bkc)
                     rc = launch_tiles<256, 256, 16, 4, 2, 0>(stream, a, akc, bkc, av, bv);

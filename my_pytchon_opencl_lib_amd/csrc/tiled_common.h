@@ -1,0 +1,128 @@
+// Pieces shared by the tiled MFMA GEMM kernels (gemm_mfma.hip: operands staged through
+// registers; gemm_direct.hip: operands loaded straight into LDS): the argument block, the
+// work-group -> tile mapping and the epilogue that writes a wavefront's 32x32 accumulator
+// blocks to C (or to the split-K partial buffer).
+#pragma once
+
+#include <type_traits>
+
+#include "migemm_internal.h"
+
+namespace migemm {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16 __attribute__((ext_vector_type(16)));
+
+struct TiledArgs {
+    const float *A;
+    const float *B;
+    const float *bias;
+    float *C;
+    int64_t lda, ldb, ldc;
+    int64_t sA, sB, sC;
+    int M, N, K;
+    int tiles_m, tiles_n;  // tiles per batch entry
+    int batch;
+    int total;             // tiles_m * tiles_n * batch * splits
+    int splits;            // split-K ranges (1 = no split)
+    int kt_per_split;      // k-tiles per range
+    float *partial;        // [splits][batch][M][N] partial sums when splits > 1
+    int accumulate;        // C += result instead of C = result
+};
+
+struct TileCoord {
+    int split, b, m0, n0;
+};
+
+// Work-group id -> (split range, batch entry, tile origin). The dispatcher deals work-groups
+// round-robin over the 8 XCDs (each with its own L2), so ids are first remapped to give each
+// XCD a contiguous chunk of tiles, then rastered in groups of 8 tile-rows so concurrently
+// running tiles share A and B panels in that L2.
+template <int BM, int BN>
+__device__ __forceinline__ TileCoord tile_coord(const TiledArgs &p, int pid) {
+    const int total = p.total;
+    if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
+    const int per_batch = p.tiles_m * p.tiles_n;
+    const int per_split = per_batch * p.batch;
+    TileCoord tc;
+    tc.split = pid / per_split;
+    pid -= tc.split * per_split;
+    tc.b = pid / per_batch;
+    const int t = pid - tc.b * per_batch;
+    constexpr int GROUP = 8;
+    const int in_group = GROUP * p.tiles_n;
+    const int first_m = (t / in_group) * GROUP;
+    const int gsz = min(p.tiles_m - first_m, GROUP);
+    const int tm = first_m + (t % in_group) % gsz;
+    const int tn = (t % in_group) / gsz;
+    tc.m0 = tm * BM;
+    tc.n0 = tn * BN;
+    return tc;
+}
+
+// Writes FM x FN accumulator blocks of 32x32 whose top-left output is (r0, c0). Register r
+// of block (i, j) holds row r0 + 32i + 8(r/4) + 4(lane/32) + r%4, column c0 + 32j + lane%32.
+// Split ranges write raw partial sums to p.partial (reduce_slices_kernel adds them in range
+// order and applies bias / accumulate); otherwise the bias is added after the k loop
+// (linear.cl:119-122) and C is written, or added to with p.accumulate.
+template <int FM, int FN>
+__device__ __forceinline__ void store_tile(const TiledArgs &p, const TileCoord &tc, int r0,
+                                           int c0, int lane, const f16 (&acc)[FM][FN]) {
+    const int lo = lane & 31;
+    const int hi = lane >> 5;
+    if (p.splits > 1) {
+        float *Pb = p.partial + ((int64_t)tc.split * p.batch + tc.b) * p.M * p.N;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int col = c0 + j * 32 + lo;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = r0 + i * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+                    if (col < p.N && row < p.M) Pb[(int64_t)row * p.N + col] = acc[i][j][r];
+                }
+        }
+        return;
+    }
+    float *Cb = p.C + (int64_t)tc.b * p.sC;
+    // Two copies of the store loop behind a uniform branch, so the plain store never
+    // carries a (speculated) load of C.
+    auto store = [&](auto accumulate) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int col = c0 + j * 32 + lo;
+            const bool cok = col < p.N;
+            float bv = 0.f;
+            if (p.bias != nullptr && cok) bv = p.bias[col];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = r0 + i * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+                    if (cok && row < p.M) {
+                        float v = acc[i][j][r];
+                        if (p.bias != nullptr) v = v + bv;
+                        float *c = Cb + (int64_t)row * p.ldc + col;
+                        if constexpr (decltype(accumulate)::value)
+                            *c = *c + v;
+                        else
+                            *c = v;
+                    }
+                }
+            }
+        }
+    };
+    if (p.accumulate)
+        store(std::true_type{});
+    else
+        store(std::false_type{});
+}
+
+// 256x256 tiles with operands loaded straight into LDS (gemm_direct.hip). Requires every
+// contiguous extent to be a multiple of 4 (K for a K-contiguous operand, M or N otherwise).
+// On entry a.splits is the requested number of split-K ranges; on return `a` holds the grid
+// (tiles_m, tiles_n, kt_per_split in 16-wide k-tiles, total) and the non-empty range count.
+int launch_gemm_direct(hipStream_t stream, TiledArgs &a, bool akc, bool bkc);
+
+}  // namespace migemm

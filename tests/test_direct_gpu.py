@@ -1,0 +1,176 @@
+"""GPU parity of the 256x256 kernel whose operands are loaded straight into LDS
+(gemm_direct_kernel), through the C ABI.
+
+The kernel runs a three-stage LDS pipeline over 16-wide k-tiles: a prologue of one or two
+tiles, a main loop of three tiles per pass, a remainder of one or two, and a zero-filled K
+tail fetched through registers. The shapes below reach each of those paths (K below one
+tile, 1-5 full tiles, K tails) with ragged M and N, in every operand layout, with batch
+strides, bias, the accumulating epilogue and split-K ranges. Small-integer operands make the
+exact answer known in any summation order. On random operands the kernel must equal the
+register-staged 256x256 kernel bit for bit: both sum each output over k in the same order.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from parity import dev, host
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def small_ints(shape, seed, lo=-4, hi=4):
+    rng = np.random.default_rng(seed)
+    return rng.integers(lo, hi + 1, size=shape).astype(np.float32)
+
+
+class _Env:
+    """Sets library tuning variables (read per call) and restores them."""
+
+    def __init__(self):
+        self.saved = {}
+
+    def set(self, **kv):
+        for k, v in kv.items():
+            if k not in self.saved:
+                self.saved[k] = os.environ.get(k)
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = str(v)
+
+    def restore(self):
+        for k, v in self.saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.fixture
+def tiled256():
+    """The TILED policy with 256x256 tiles forced (MIGEMM_TILE), direct loads on."""
+    from my_pytchon_opencl_lib_amd import _native
+    env = _Env()
+    prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_TILED)
+    env.set(MIGEMM_TILE=256, MIGEMM_DIRECT=1, MIGEMM_SPLITK=None)
+    yield env
+    env.restore()
+    _native.set_gemm_policy(prev)
+
+
+def gemm_ex(ta, tb, M, N, K, a, lda, sA, b, ldb, sB, bias, c, ldc, sC, batch, acc=False):
+    from my_pytchon_opencl_lib_amd import _native
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _native.call("migemm_gemm_strided_batched_ex", stream, int(ta), int(tb), M, N, K,
+                 ctypes.c_void_p(a.data_ptr()), lda, sA, ctypes.c_void_p(b.data_ptr()), ldb, sB,
+                 None if bias is None else ctypes.c_void_p(bias.data_ptr()),
+                 ctypes.c_void_p(c.data_ptr()), ldc, sC, batch, int(acc))
+
+
+def run_exact(M, K, N, ta, tb, batch=1, bias=False, acc=False, seed=0):
+    """One strided-batched request on small integers; returns (got, expect)."""
+    rng = np.random.default_rng(seed)
+    lo, hi = (-2, 2) if K > 2000 else (-4, 4)
+    a_rows, a_cols = (K, M) if ta else (M, K)
+    b_rows, b_cols = (N, K) if tb else (K, N)
+    A = rng.integers(lo, hi + 1, size=(batch, a_rows, a_cols)).astype(np.float32)
+    B = rng.integers(lo, hi + 1, size=(batch, b_rows, b_cols)).astype(np.float32)
+    bv = rng.integers(-20, 21, size=N).astype(np.float32) if bias else None
+    C0 = rng.integers(-50, 51, size=(batch, M, N)).astype(np.float32)
+    a, b = dev(A), dev(B)
+    c = dev(C0) if acc else torch.full((batch, M, N), float("nan"), device="cuda")
+    gemm_ex(ta, tb, M, N, K, a, a_cols, a_rows * a_cols, b, b_cols, b_rows * b_cols,
+            None if bv is None else dev(bv), c, N, M * N, batch, acc)
+    Aop = np.swapaxes(A, 1, 2) if ta else A
+    Bop = np.swapaxes(B, 1, 2) if tb else B
+    expect = Aop.astype(np.float64) @ Bop.astype(np.float64)
+    if bv is not None:
+        expect = expect + bv
+    if acc:
+        expect = expect + C0
+    return host(c), expect.astype(np.float32)
+
+
+LAYOUTS = [(0, 0), (0, 1), (1, 0), (1, 1)]
+# (M, K, N): every extent a multiple of 4 (the direct path's condition). K = 4, 8, 12: the
+# tail tile alone; 16, 32, 48: one to three full tiles (prologue and remainder only); 64 and
+# 80: a main-loop pass plus a remainder of one and two; 300 and 1036: long loops with tails.
+SHAPES = [(256, 4, 256), (260, 8, 516), (300, 12, 300), (256, 16, 260), (516, 32, 260),
+          (1000, 48, 1100), (256, 64, 512), (512, 80, 256), (1000, 300, 1100),
+          (520, 1036, 264)]
+
+
+@pytest.mark.parametrize("M,K,N", SHAPES)
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_direct_exact(tiled256, M, K, N, ta, tb):
+    say("direct exact", M, K, N, ta, tb)
+    got, expect = run_exact(M, K, N, ta, tb, seed=M + 3 * K + 7 * N + ta + 2 * tb)
+    assert np.array_equal(got, expect)
+
+
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_direct_batched_bias_accumulate(tiled256, ta, tb):
+    """Batch strides, bias after the k loop and C += result."""
+    for M, K, N, bias, acc in [(300, 100, 520, True, False), (260, 68, 256, False, True),
+                               (512, 36, 300, True, True)]:
+        say("direct batched", M, K, N, ta, tb, "bias", bias, "acc", acc)
+        got, expect = run_exact(M, K, N, ta, tb, batch=3, bias=bias, acc=acc, seed=K)
+        assert np.array_equal(got, expect)
+
+
+@pytest.mark.parametrize("splits", [2, 3, 7])
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_direct_split_ranges(tiled256, splits, ta, tb):
+    """Forced split-K: ranges that start past k-tile 0, ranges of 1-2 tiles, the K tail in
+    the last range; partial sums through the ordered reduce, with bias and accumulate."""
+    tiled256.set(MIGEMM_SPLITK=splits)
+    for M, K, N, bias, acc in [(516, 1036, 260, False, False), (256, 100, 512, True, True),
+                               (300, 4100, 256, True, False)]:
+        say("direct split", splits, M, K, N, ta, tb)
+        got, expect = run_exact(M, K, N, ta, tb, bias=bias, acc=acc, seed=splits + K)
+        assert np.array_equal(got, expect)
+
+
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_direct_equals_staged_kernel(tiled256, ta, tb):
+    """N(0,1) operands: the direct kernel and the register-staged 256x256 kernel (the same
+    MFMA sequence per output) give identical bits. K is not split (the staged NT kernel
+    counts ranges in 32-wide k-tiles, the direct kernel in 16-wide ones)."""
+    tiled256.set(MIGEMM_SPLITK=1)
+    g = torch.Generator(device="cpu").manual_seed(77 + ta + 2 * tb)
+    for M, K, N in [(768, 528, 1024), (1028, 1000, 516), (256, 4100, 768)]:
+        say("direct vs staged", M, K, N, ta, tb)
+        A = torch.randn((K, M) if ta else (M, K), generator=g).cuda()
+        B = torch.randn((N, K) if tb else (K, N), generator=g).cuda()
+        bias = torch.randn(N, generator=g).cuda()
+        outs = []
+        for direct in (1, 0):
+            tiled256.set(MIGEMM_DIRECT=direct)
+            c = torch.empty((M, N), device="cuda")
+            gemm_ex(ta, tb, M, N, K, A, A.shape[1], 0, B, B.shape[1], 0, bias, c, N, 0, 1)
+            outs.append(host(c))
+        assert np.array_equal(outs[0], outs[1])
+
+
+def test_unaligned_rows_use_staged_kernel(tiled256):
+    """Leading dimensions that are not multiples of 4 (rows off 16-byte boundaries) and an
+    operand starting 4 bytes into its buffer take the register-staged kernel; exact."""
+    M, K, N = 300, 100, 260
+    for lda, ldb, off in [(K + 1, N, 0), (K, N + 2, 0), (K, N, 1)]:
+        say("direct unaligned", lda, ldb, off)
+        A = small_ints((M, lda), lda)
+        B = small_ints((K, ldb), ldb)
+        a = dev(np.concatenate([np.zeros(off, np.float32), A.ravel()]))
+        b = dev(B)
+        c = torch.empty((M, N), device="cuda")
+        av = a[off:]
+        gemm_ex(0, 0, M, N, K, av, lda, 0, b, ldb, 0, None, c, N, 0, 1)
+        expect = A[:, :K].astype(np.float64) @ B[:, :N].astype(np.float64)
+        assert np.array_equal(host(c), expect.astype(np.float32))
