@@ -37,20 +37,12 @@
 namespace migemm {
 namespace {
 
-constexpr int DT = 256;      // macro-tile edge (BM = BN)
-constexpr int DPAD_I = 8;    // pad of an I-contiguous LDS row
-
 // s_waitcnt vmcnt(N) with expcnt and lgkmcnt left at their maxima (N < 16).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 16, "vmcnt immediate");
     __builtin_amdgcn_s_waitcnt(0x0F70 | N);
 }
-
-template <int BK, bool KC>
-struct DlTileFloats {
-    static constexpr int value = KC ? DT * BK : BK * (DT + DPAD_I);
-};
 
 typedef __attribute__((address_space(3))) float *lds_ptr_t;
 
@@ -85,20 +77,28 @@ __device__ __forceinline__ int kc_swz(int r) {
     return (r / (16 / CPR)) % CPR;
 }
 
-// One operand of a 256 x BK tile. NS = load instructions (1 KB each) per wavefront per
-// tile. KC: instruction q covers tile rows RPI*q .. RPI*q + RPI - 1 (RPI = 64 / CPR rows of
-// CPR chunks); otherwise k-row q (256 floats). The loads address memory as a wave-uniform
-// base (the tile's first row / column at k-tile 0, advanced per k-tile in scalar registers)
-// plus a 32-bit per-lane byte offset, which keeps the per-lane state to one register per
+// I-contiguous LDS tile: BK k-rows of T floats, unpadded. Column c of k-row k is stored at
+// c ^ ic_swz(k): the two half-wavefronts of a fragment read take k-rows 4 apart (whose
+// starts fall on the same banks) at 32 consecutive columns each; flipping bit 5 of the
+// column on alternate groups of 4 k-rows puts them on complementary halves of the 64 banks.
+__device__ __forceinline__ int ic_swz(int k) { return ((k >> 2) & 1) << 5; }
+
+// One operand of a T x BK tile (T = 128 or 256 rows of the M or N dimension). A load
+// instruction fills 1 KB: KC, 64 / (BK / 4) whole rows; otherwise 256 / T whole k-rows.
+// NS = instructions per wavefront per tile. The loads address memory as a wave-uniform base
+// (the tile's first row / column at k-tile 0, advanced per k-tile in scalar registers) plus
+// a 32-bit per-lane byte offset, which keeps the per-lane state to one register per
 // instruction; the launcher checks that the offsets fit.
-template <int NT, bool KC, int BK>
+template <int NT, bool KC, int BK, int T>
 struct DlOperand {
+    static_assert(T == 128 || T == 256, "tile edge");
     static constexpr int NW = NT / 64;
-    static constexpr int NI = BK;  // load instructions per tile: 256 * BK floats / 256
+    static constexpr int NI = T * BK / 256;  // load instructions per tile
     static constexpr int NS = NI / NW;
-    static_assert(NS * NW == NI, "the tile's loads split evenly over the wavefronts");
+    static_assert(NS >= 1 && NS * NW == NI, "the tile's loads split evenly over the wavefronts");
     static constexpr int CPR = BK / 4;
-    static constexpr int RPI = 64 / CPR;
+    static constexpr int RPI = KC ? 64 / CPR : 256 / T;  // rows (KC) / k-rows per instruction
+    static constexpr int FLOATS = T * BK;
     const char *base;      // wave-uniform: element (i0, 0) of the operand
     uint32_t voff[NS];     // this lane's byte offset from `base` at k-tile 0
     int q0;                // first instruction of this wavefront (wave-uniform)
@@ -118,17 +118,16 @@ struct DlOperand {
                 gi = gi < rows ? gi : rows - 1;
                 voff[j] = (uint32_t)(((gi - i0) * (uint32_t)ld + 4 * c[j]) * 4);
             } else {
+                const int k = RPI * q + lane / (T / 4);  // k-row of the tile
                 c[j] = 0;
-                int gi = i0 + 4 * lane;
+                int gi = i0 + ((4 * (lane % (T / 4))) ^ ic_swz(k));
                 gi = gi < rows ? gi : rows - 4;
-                voff[j] = (uint32_t)((q * (uint32_t)ld + (gi - i0)) * 4);
+                voff[j] = (uint32_t)((k * (uint32_t)ld + (gi - i0)) * 4);
             }
         }
     }
 
-    __device__ __forceinline__ int lds_off(int j) const {
-        return KC ? (q0 + j) * 256 : (q0 + j) * (DT + DPAD_I);
-    }
+    __device__ __forceinline__ int lds_off(int j) const { return (q0 + j) * 256; }
 
     __device__ __forceinline__ const char *tile_base(int kt, int64_t ld) const {
         return base + (KC ? (int64_t)kt * BK * 4 : (int64_t)kt * BK * ld * 4);
@@ -156,7 +155,7 @@ struct DlOperand {
                 for (int e = 0; e < 4; ++e)
                     if (k0 + 4 * c[j] + e < K) v[e] = src[e];
             } else {
-                if (k0 + q0 + j < K) v = dl_load16(src);
+                if (k0 + RPI * (q0 + j) + lane / (T / 4) < K) v = dl_load16(src);
             }
             *reinterpret_cast<f4 *>(stage + lds_off(j) + 4 * lane) = v;
         }
@@ -166,7 +165,7 @@ struct DlOperand {
 // Fragments of k-group g (8 consecutive k of the tile) for F blocks of 32 rows from `off`:
 // fr[f][s] is this lane's operand for MFMA step s (lanes 0-31: k = 8g + s, lanes 32-63:
 // k = 8g + 4 + s).
-template <bool KC, int BK, int F>
+template <bool KC, int BK, int T, int F>
 __device__ __forceinline__ void dl_frags(const float *lds, int off, int g, int lane,
                                          f4 (&fr)[F]) {
     const int lo = lane & 31;
@@ -177,34 +176,37 @@ __device__ __forceinline__ void dl_frags(const float *lds, int off, int g, int l
         for (int f = 0; f < F; ++f)
             fr[f] = *reinterpret_cast<const f4 *>(lds + (off + f * 32 + lo) * BK + 4 * slot);
     } else {
+        // k-row 8g + 4hi + s has ic_swz = 32 hi
 #pragma unroll
         for (int f = 0; f < F; ++f)
 #pragma unroll
             for (int s = 0; s < 4; ++s)
-                fr[f][s] = lds[(8 * g + 4 * hi + s) * (DT + DPAD_I) + off + f * 32 + lo];
+                fr[f][s] = lds[(8 * g + 4 * hi + s) * T + ((off + f * 32 + lo) ^ (hi << 5))];
     }
 }
 
-// S LDS stages; tile kt lives in stage (kt - kt0) % S and is loaded D (<= S) tiles ahead.
-template <int WM, int WN, bool AKC, bool BKC, int BK, int S, int D>
-__global__ void __launch_bounds__(WM *WN * 64)
+// BM x BN tiles, WM x WN wavefronts; S LDS stages; tile kt lives in stage (kt - kt0) % S
+// and is loaded D (<= S) tiles ahead. OCC: wavefronts per SIMD the register allocation must
+// allow (4 for four 4-wavefront work-groups per CU).
+template <int BM, int BN, int WM, int WN, bool AKC, bool BKC, int BK, int S, int D, int OCC>
+__global__ void __launch_bounds__(WM *WN * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
 gemm_direct_kernel(TiledArgs p) {
     static_assert(D >= 2 && D <= S, "loads run 2..S tiles ahead");
     constexpr int NT = WM * WN * 64;
-    constexpr int WTM = DT / WM;
-    constexpr int WTN = DT / WN;
+    constexpr int WTM = BM / WM;
+    constexpr int WTN = BN / WN;
     constexpr int FM = WTM / 32;
     constexpr int FN = WTN / 32;
     constexpr int G = BK / 8;  // k-groups per tile
     static_assert(FM >= 1 && FN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "bad wave tile");
-    constexpr int A_FL = DlTileFloats<BK, AKC>::value;
-    constexpr int B_FL = DlTileFloats<BK, BKC>::value;
+    typedef DlOperand<NT, AKC, BK, BM> OpA;
+    typedef DlOperand<NT, BKC, BK, BN> OpB;
+    constexpr int A_FL = OpA::FLOATS;
+    constexpr int B_FL = OpB::FLOATS;
     // One array per operand, so each wavefront reads every stage of an operand from one
     // base register with immediate offsets (the stages of one operand span < 64 KB).
     __shared__ __attribute__((aligned(16))) float lds_a[S * A_FL];
     __shared__ __attribute__((aligned(16))) float lds_b[S * B_FL];
-    typedef DlOperand<NT, AKC, BK> OpA;
-    typedef DlOperand<NT, BKC, BK> OpB;
     constexpr int LPT = OpA::NS + OpB::NS;  // load instructions per tile per wavefront
 
     const int tid = threadIdx.x;
@@ -216,7 +218,7 @@ gemm_direct_kernel(TiledArgs p) {
     // The tile mapping divides in VALU registers; the results are wave-uniform, and keeping
     // them (and everything derived from them: k-tile indices, load bases) in scalar
     // registers leaves the vector registers to the accumulators and fragments.
-    TileCoord tc = tile_coord<DT, DT>(p, blockIdx.x);
+    TileCoord tc = tile_coord<BM, BN>(p, blockIdx.x);
     tc.split = __builtin_amdgcn_readfirstlane(tc.split);
     tc.b = __builtin_amdgcn_readfirstlane(tc.b);
     tc.m0 = __builtin_amdgcn_readfirstlane(tc.m0);
@@ -247,8 +249,8 @@ gemm_direct_kernel(TiledArgs p) {
         opb.issue(lds_b + st * B_FL, kt, p.ldb);
     };
     auto frags = [&](int st, int g, f4(&fa)[FM], f4(&fb)[FN]) {
-        dl_frags<AKC, BK, FM>(lds_a + st * A_FL, wm * WTM, g, lane, fa);
-        dl_frags<BKC, BK, FN>(lds_b + st * B_FL, wn * WTN, g, lane, fb);
+        dl_frags<AKC, BK, BM, FM>(lds_a + st * A_FL, wm * WTM, g, lane, fa);
+        dl_frags<BKC, BK, BN, FN>(lds_b + st * B_FL, wn * WTN, g, lane, fb);
     };
     auto mfmas = [&](const f4(&fa)[FM], const f4(&fb)[FN]) {
 #pragma unroll
@@ -325,10 +327,10 @@ gemm_direct_kernel(TiledArgs p) {
     store_tile<FM, FN>(p, tc, tc.m0 + wm * WTM, tc.n0 + wn * WTN, lane, acc);
 }
 
-template <int WM, int WN, bool AKC, bool BKC, int BK, int S, int D>
+template <int BM, int BN, int WM, int WN, bool AKC, bool BKC, int BK, int S, int D, int OCC>
 int launch_direct(hipStream_t s, TiledArgs &a) {
-    a.tiles_m = (a.M + DT - 1) / DT;
-    a.tiles_n = (a.N + DT - 1) / DT;
+    a.tiles_m = (a.M + BM - 1) / BM;
+    a.tiles_n = (a.N + BN - 1) / BN;
     const int nk = (a.K + BK - 1) / BK;
     const int want = a.splits < nk ? a.splits : nk;
     a.kt_per_split = (nk + want - 1) / want;
@@ -338,32 +340,57 @@ int launch_direct(hipStream_t s, TiledArgs &a) {
         return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm: %lld tiles exceed one launch",
                          (long long)total);
     a.total = (int)total;
-    hipLaunchKernelGGL((gemm_direct_kernel<WM, WN, AKC, BKC, BK, S, D>), dim3(a.total),
+    hipLaunchKernelGGL((gemm_direct_kernel<BM, BN, WM, WN, AKC, BKC, BK, S, D, OCC>), dim3(a.total),
                        dim3(WM * WN * 64), 0, s, a);
     return hip_check(hipGetLastError(), "gemm_direct_kernel launch");
 }
 
-// Every operand layout (NN, NT, TN, TT) runs 16 wavefronts of 32x128.
-template <int BK, int S, int D>
+// Every operand layout (NN, NT, TN, TT) with wavefronts of 32x128.
+template <int BM, int BN, int BK, int S, int D, int OCC = 1>
 int launch_layouts(hipStream_t s, TiledArgs &a, bool akc, bool bkc) {
-    if (akc && bkc) return launch_direct<8, 2, true, true, BK, S, D>(s, a);
-    if (akc) return launch_direct<8, 2, true, false, BK, S, D>(s, a);
-    if (!bkc) return launch_direct<8, 2, false, false, BK, S, D>(s, a);
-    return launch_direct<8, 2, false, true, BK, S, D>(s, a);
+    constexpr int WM = BM / 32;
+    constexpr int WN = BN / 128;
+    if (akc && bkc) return launch_direct<BM, BN, WM, WN, true, true, BK, S, D, OCC>(s, a);
+    if (akc) return launch_direct<BM, BN, WM, WN, true, false, BK, S, D, OCC>(s, a);
+    if (!bkc) return launch_direct<BM, BN, WM, WN, false, false, BK, S, D, OCC>(s, a);
+    return launch_direct<BM, BN, WM, WN, false, true, BK, S, D, OCC>(s, a);
 }
 
 }  // namespace
 
-int launch_gemm_direct(hipStream_t stream, TiledArgs &a, bool akc, bool bkc) {
-    // BK = 32 with two stages, loads two tiles ahead (2 x 130 KB of LDS, one barrier per 32
-    // k). Measured at 4096^3 against BK = 16 with three stages (the alternative kept under
-    // MIGEMM_DVAR=1, read per call), interleaved in one process, TFLOP/s NN / NT / TN:
-    // 148.2 / 150.9 / 147.4 against 148.0 / 150.3 / 147.8; with loads three tiles ahead
-    // (three stages) 146.7 / 150.0 / 143.4; four stages 145.9 / 149.9 / 142.9; TN with 8
-    // wavefronts of 64x128 144.3-145.5. The register-staged kernel: 144.6 / 147.7 / 143.0.
+int launch_gemm_direct(hipStream_t stream, TiledArgs &a, int bm, int bn, bool akc, bool bkc) {
+    // MIGEMM_DVAR (read per call) selects pipeline variants for tuning sweeps.
     const char *v = getenv("MIGEMM_DVAR");
-    if (v != nullptr && atoi(v) == 1) return launch_layouts<16, 3, 2>(stream, a, akc, bkc);
-    return launch_layouts<32, 2, 2>(stream, a, akc, bkc);
+    const int var = v != nullptr ? atoi(v) : 0;
+    if (bm == 256) {
+        // BK = 32 with two stages, loads two tiles ahead (2 x 128 KB of LDS, one barrier per
+        // 32 k). Measured at 4096^3 against BK = 16 with three stages (MIGEMM_DVAR=1),
+        // interleaved in one process, TFLOP/s NN / NT / TN: 148.2 / 150.9 / 147.4 against
+        // 148.0 / 150.3 / 147.8; with loads three tiles ahead (three stages) 146.7 / 150.0 /
+        // 143.4; four stages 145.9 / 149.9 / 142.9; TN with 8 wavefronts of 64x128
+        // 144.3-145.5. The register-staged kernel: 144.6 / 147.7 / 143.0.
+        if (var == 1) return launch_layouts<256, 256, 16, 3, 2>(stream, a, akc, bkc);
+        return launch_layouts<256, 256, 32, 2, 2>(stream, a, akc, bkc);
+    }
+    if (bn == 256) {
+        // BK = 16 with three stages (2 x 72 KB: two work-groups per CU). At 4096 x K x 4096
+        // (K = 256 .. 4096) and 4096 x 2048 x 2048 NT within 1 % of two stages (MIGEMM_DVAR=2)
+        // and 7-11 % faster than the register-staged 128x256 kernel.
+        if (var == 2) return launch_layouts<128, 256, 16, 2, 2>(stream, a, akc, bkc);
+        if (var == 3) return launch_layouts<128, 256, 32, 2, 2>(stream, a, akc, bkc);
+        return launch_layouts<128, 256, 16, 3, 2>(stream, a, akc, bkc);
+    }
+    // BK = 16, two stages (32 KB) and at most 128 VGPRs: four work-groups (16 wavefronts) per
+    // CU. Measured (us; direct with this occupancy / with up to 168 VGPRs, three work-groups
+    // (MIGEMM_DVAR=2) / three stages (MIGEMM_DVAR=1) / BK = 32 (MIGEMM_DVAR=3) / register-
+    // staged): 4096 x 1024 x 4096 NN 249.6 / 293.9 / 307.0 / 258.5 / 271.0; 4096^3 949.7 /
+    // 1141.4 / 943.5 / 957.2 / 1033.0; 2048^3 TN 142.2 / 145.6 / 147.0 / 154.3 / 164.3;
+    // 6400 x 512 x 4096 226.9 / 230.6 / 230.5 / 243.3 / 243.0. With three work-groups per CU
+    // the 1024 tiles of a 4096-wide output leave a ragged last round.
+    if (var == 1) return launch_layouts<128, 128, 16, 3, 2>(stream, a, akc, bkc);
+    if (var == 2) return launch_layouts<128, 128, 16, 2, 2>(stream, a, akc, bkc);
+    if (var == 3) return launch_layouts<128, 128, 32, 2, 2>(stream, a, akc, bkc);
+    return launch_layouts<128, 128, 16, 2, 2, 4>(stream, a, akc, bkc);
 }
 
 }  // namespace migemm

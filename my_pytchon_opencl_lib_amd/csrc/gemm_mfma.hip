@@ -498,13 +498,19 @@ int lds_pad_bytes() {
     static const int pad = env_int("MIGEMM_LDS_PAD");
     return pad > 0 && pad <= 65536 ? pad : 0;
 }
-// 256x256 tiles use gemm_direct_kernel unless MIGEMM_DIRECT=0 (read per call, for
-// interleaved comparisons in one process) when its loads apply: every row and batch entry of
-// both operands starts on a 16-byte boundary (the loads into LDS move aligned 16-byte
-// pieces), and a lane's offset within a 256-row panel fits the loads' 32-bit offsets.
-bool direct_loads(const GemmDesc &d) {
+// MIGEMM_DIRECT (read per call, for interleaved comparisons in one process): 0 = never use
+// gemm_direct_kernel, 2 = use it for every 128x128 / 128x256 / 256x256 tile it can run
+// (tests), unset or 1 = the measured choice.
+int direct_mode() {
     const char *v = getenv("MIGEMM_DIRECT");
-    if (v != nullptr && atoi(v) == 0) return false;
+    return v != nullptr ? atoi(v) : 1;
+}
+
+// gemm_direct_kernel's loads apply: every row and batch entry of both operands starts on a
+// 16-byte boundary (the loads into LDS move aligned 16-byte pieces), and a lane's offset
+// within a 256-row panel fits the loads' 32-bit offsets.
+bool direct_loads(const GemmDesc &d) {
+    if (direct_mode() == 0) return false;
     auto ok = [](const float *p, int64_t ld, int64_t stride) {
         return ((uintptr_t)p & 15) == 0 && ld % 4 == 0 && stride % 4 == 0 && ld <= (1 << 21);
     };
@@ -598,30 +604,44 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     }
     // Large outputs: pick the macro-tile by the busiest CU's share of the work. The work-
     // groups are dealt over the 256 CUs, so a CU carries ceil(tiles / 256) tiles of area x
-    // (K + a per-tile overhead), at each tile's own rate. With 128-bit loads of both operands
-    // the rates and overheads are fitted to NN at 4096 x K x 4096, K = 512 .. 4096 (TFLOP/s
-    // x K / (K + o)): 256x256 147.2, o = 73; 128x256 140.6, o = 99; 128x128 138.9, o = 78;
-    // 64x64 134.2, o = 75. The tile count's quantization then decides: 3072 x 1024 x 3072
-    // runs 119.4 TFLOP/s in 64x64 tiles (9 per CU) against 96.7 in 128x128 (2.25 per CU);
-    // 4096 x 512 x 4096 128.9 in 256x256 against 120.6. Element-wise loads (M, N or K not a
-    // multiple of 4) keep the earlier three-shape model: 256x256 work-groups fill a CU alone,
-    // their prologue and C store not overlapped (about 32 k-steps per tile, 16 for 128x256),
-    // which decides short K: 12000 x 6565 x 500 runs 729 us at 128x128, 747 at 256x256.
-    if (cfg == 128 && splits == 1) {
+    // (K + a per-tile overhead), at each tile's own rate. The rates and overheads are fitted
+    // to NN at 4096 x K x 4096, K = 256 .. 4096 (time = tiles per CU x area x (K + o) /
+    // rate), in one process on one box:
+    //   operands loaded straight into LDS (gemm_direct_kernel; 16-byte aligned rows):
+    //     256x256 151.6 TFLOP/s, o = 70; 128x256 150.8, o = 89; 128x128 147.7, o = 83;
+    //     64x64 (register-staged) 129.5, o = 64;
+    //   register-staged kernels (other 128-bit operands): 256x256 147.2, o = 73; 128x256
+    //     140.6, o = 99; 128x128 138.9, o = 78; 64x64 134.2, o = 75.
+    // The tile count's quantization then decides: 3072 x 1024 x 3072 runs 173.9 us in 64x64
+    // tiles (9 per CU) against 189.0 in 128x128 (2.25 per CU); 4096 x 256 x 4096 72.0 in
+    // 256x256 against 77.4 in 128x128. With direct loads 128x128 tiles are also weighed for
+    // outputs of 256-511 of them (2048^3 TN: 142.2 us against 160.1 in 64x64 tiles).
+    // Element-wise loads (M, N or K not a multiple of 4) keep the earlier three-shape model:
+    // 256x256 work-groups fill a CU alone, their prologue and C store not overlapped (about
+    // 32 k-steps per tile, 16 for 128x256), which decides short K: 12000 x 6565 x 500 runs
+    // 729 us at 128x128, 747 at 256x256.
+    const bool direct = av && bv && direct_loads(d);
+    if (splits == 1 && (cfg == 128 || (cfg == 64 && direct && tiles(128, 128) >= 256))) {
         const double k = d.K;
         auto cost = [&](int bm, int bn, double rate, double over) {
             return (double)((tiles(bm, bn) + 255) / 256) * bm * bn * (k + over) / rate;
         };
         if (av && bv) {
-            const double c64 = cost(64, 64, 134.2, 75), c0 = cost(128, 128, 138.9, 78);
-            const double c1 = cost(128, 256, 140.6, 99), c2 = cost(256, 256, 147.2, 73);
+            double c64, c0, c1, c2;
+            if (direct) {
+                c64 = cost(64, 64, 129.5, 64);
+                c0 = cost(128, 128, 147.7, 83);
+                c1 = cost(128, 256, 150.8, 89);
+                c2 = cost(256, 256, 151.6, 70);
+            } else {
+                c64 = cost(64, 64, 134.2, 75);
+                c0 = cost(128, 128, 138.9, 78);
+                c1 = cost(128, 256, 140.6, 99);
+                c2 = cost(256, 256, 147.2, 73);
+            }
             const double best = std::min(std::min(c64, c0), std::min(c1, c2));
-            if (best == c2)
-                big = 2;
-            else if (best == c1)
-                big = 1;
-            else if (best == c64)
-                cfg = 64;
+            cfg = best == c64 ? 64 : 128;
+            big = best == c2 ? 2 : (best == c1 ? 1 : 0);
         } else {
             const double c0 = cost(128, 128, 0.966, 0), c1 = cost(128, 256, 0.981, 16);
             const double c2 = cost(256, 256, 1.0, 32);
@@ -684,8 +704,14 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
                 // I-contiguous) runs 8 wavefronts of 64x128 (2 per SIMD, ~220 VGPRs): 143.2
                 // against 142.5 at 4096^3, 145.9 against 144.3 at 8192^3; NN and NT are
                 // slower that way (142.7 / 143.0).
-                if (big == 2 && av && bv && direct_loads(d))
-                    rc = launch_gemm_direct(stream, a, akc, bkc);
+                // Split 128-wide tiles (long K over few tiles) keep the register-staged
+                // kernel: direct loads measured 5-8 % slower there (6400 x 4096 x 512 NT in 6
+                // ranges 268.3 against 246.1 us, 1536 x 4096 x 1536 in 8: 190.4 / 180.9,
+                // 1000 x 4096 x 3000 in 6: 253.1 / 233.9), while split 256x256 tiles gain
+                // (1024 x 6400 x 4096 TN in 4 ranges: 383.2 / 395.8).
+                if (direct && (big == 2 || splits == 1 || direct_mode() == 2))
+                    rc = launch_gemm_direct(stream, a, big == 2 ? 256 : 128, big >= 1 ? 256 : 128,
+                                            akc, bkc);
                 else if (big == 2 && akc && bkc)
                     rc = launch_tiles<256, 256, 32, 8, 2, 3>(stream, a, akc, bkc, av, bv);
                 else if (big == 2 && !akc && !bkc)

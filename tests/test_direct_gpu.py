@@ -1,5 +1,5 @@
-"""GPU parity of the 256x256 kernel whose operands are loaded straight into LDS
-(gemm_direct_kernel), through the C ABI.
+"""GPU parity of the tiled kernel whose operands are loaded straight into LDS
+(gemm_direct_kernel: 256x256, 128x256 and 128x128 tiles), through the C ABI.
 
 The kernel runs a three-stage LDS pipeline over 16-wide k-tiles: a prologue of one or two
 tiles, a main loop of three tiles per pass, a remainder of one or two, and a zero-filled K
@@ -53,13 +53,15 @@ class _Env:
                 os.environ[k] = v
 
 
-@pytest.fixture
-def tiled256():
-    """The TILED policy with 256x256 tiles forced (MIGEMM_TILE), direct loads on."""
+@pytest.fixture(params=["256", "128x256", "128"])
+def tiled256(request):
+    """The TILED policy with one macro-tile forced (MIGEMM_TILE: 256x256, 128x256,
+    128x128), direct loads forced wherever they apply (MIGEMM_DIRECT=2: also for split-K
+    ranges of 128-wide tiles, which the library's own choice runs register-staged)."""
     from my_pytchon_opencl_lib_amd import _native
     env = _Env()
     prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_TILED)
-    env.set(MIGEMM_TILE=256, MIGEMM_DIRECT=1, MIGEMM_SPLITK=None)
+    env.set(MIGEMM_TILE=request.param, MIGEMM_DIRECT=2, MIGEMM_SPLITK=None)
     yield env
     env.restore()
     _native.set_gemm_policy(prev)
@@ -140,8 +142,8 @@ def test_direct_split_ranges(tiled256, splits, ta, tb):
 
 @pytest.mark.parametrize("ta,tb", LAYOUTS)
 def test_direct_equals_staged_kernel(tiled256, ta, tb):
-    """N(0,1) operands: the direct kernel and the register-staged 256x256 kernel (the same
-    MFMA sequence per output) give identical bits. K is not split (the staged NT kernel
+    """N(0,1) operands: the direct kernel and the register-staged kernel of the same tile
+    (the same MFMA sequence per output) give identical bits. K is not split (the staged NT kernel
     counts ranges in 32-wide k-tiles, the direct kernel in 16-wide ones)."""
     tiled256.set(MIGEMM_SPLITK=1)
     g = torch.Generator(device="cpu").manual_seed(77 + ta + 2 * tb)
@@ -151,7 +153,7 @@ def test_direct_equals_staged_kernel(tiled256, ta, tb):
         B = torch.randn((N, K) if tb else (K, N), generator=g).cuda()
         bias = torch.randn(N, generator=g).cuda()
         outs = []
-        for direct in (1, 0):
+        for direct in (2, 0):
             tiled256.set(MIGEMM_DIRECT=direct)
             c = torch.empty((M, N), device="cuda")
             gemm_ex(ta, tb, M, N, K, A, A.shape[1], 0, B, B.shape[1], 0, bias, c, N, 0, 1)
