@@ -1,0 +1,46 @@
+"""Checks on the generated gfx950 code of the direct-to-LDS GEMM kernel (CPU only: hipcc
+cross-compiles the device code to assembly text).
+
+gemm_direct.hip issues global_load_lds_dwordx4 through inline assembly that sets M0 itself
+and declares it clobbered. M0 is a register the compiler reserves, so the kernels may only
+be correct if no compiler-generated code relies on M0 across those statements. This test
+pins that: in the device assembly, M0 is written only by `s_mov_b32 m0, s<n>` immediately
+followed by a global_load_lds_dwordx4, and nothing reads it otherwise."""
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+SRC = os.path.join(ROOT, "my_pytchon_opencl_lib_amd", "csrc", "gemm_direct.hip")
+
+
+def _hipcc():
+    for c in ("/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if c and os.path.exists(c):
+            return c
+    return None
+
+
+@pytest.mark.skipif(_hipcc() is None, reason="hipcc not available")
+def test_m0_only_feeds_the_lds_loads(tmp_path):
+    out = tmp_path / "gemm_direct.s"
+    subprocess.run([_hipcc(), "--offload-arch=gfx950", "-O3", "-std=c++17",
+                    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                    "-Wno-inline-asm", "--cuda-device-only", "-S", SRC, "-o", str(out)],
+                   check=True, capture_output=True)
+    lines = [l.split(";")[0].strip() for l in out.read_text().splitlines()]
+    code = [l for l in lines if l and not l.startswith(".") and not l.endswith(":")]
+    loads = 0
+    for i, l in enumerate(code):
+        if not re.search(r"\bm0\b", l):
+            continue
+        assert re.fullmatch(r"s_mov_b32 m0, s\d+", l), f"unexpected use of M0: {l!r}"
+        assert code[i + 1].startswith("global_load_lds_dwordx4"), \
+            f"M0 written without a following LDS load: {l!r} then {code[i + 1]!r}"
+        loads += 1
+    assert loads > 0, "no global_load_lds_dwordx4 found"
+    n_lds = sum(1 for l in code if l.startswith("global_load_lds_dwordx4"))
+    assert n_lds == loads, (n_lds, loads)
