@@ -91,7 +91,7 @@ __device__ __forceinline__ int ic_swz(int k) { return ((k >> 2) & 1) << 5; }
 // instruction; the launcher checks that the offsets fit.
 template <int NT, bool KC, int BK, int T>
 struct DlOperand {
-    static_assert(T == 128 || T == 256, "tile edge");
+    static_assert(T == 64 || T == 128 || T == 256, "tile edge");
     static constexpr int NW = NT / 64;
     static constexpr int NI = T * BK / 256;  // load instructions per tile
     static constexpr int NS = NI / NW;
@@ -345,11 +345,12 @@ int launch_direct(hipStream_t s, TiledArgs &a) {
     return hip_check(hipGetLastError(), "gemm_direct_kernel launch");
 }
 
-// Every operand layout (NN, NT, TN, TT) with wavefronts of 32x128.
+// Every operand layout (NN, NT, TN, TT) with wavefronts of 32x128 (64x64 tiles: 2 x 2
+// wavefronts of 32x32).
 template <int BM, int BN, int BK, int S, int D, int OCC = 1>
 int launch_layouts(hipStream_t s, TiledArgs &a, bool akc, bool bkc) {
-    constexpr int WM = BM / 32;
-    constexpr int WN = BN / 128;
+    constexpr int WM = BN >= 128 ? BM / 32 : 2;
+    constexpr int WN = BN >= 128 ? BN / 128 : 2;
     if (akc && bkc) return launch_direct<BM, BN, WM, WN, true, true, BK, S, D, OCC>(s, a);
     if (akc) return launch_direct<BM, BN, WM, WN, true, false, BK, S, D, OCC>(s, a);
     if (!bkc) return launch_direct<BM, BN, WM, WN, false, false, BK, S, D, OCC>(s, a);
@@ -371,6 +372,14 @@ int launch_gemm_direct(hipStream_t stream, TiledArgs &a, int bm, int bn, bool ak
         // 144.3-145.5. The register-staged kernel: 144.6 / 147.7 / 143.0.
         if (var == 1) return launch_layouts<256, 256, 16, 3, 2>(stream, a, akc, bkc);
         return launch_layouts<256, 256, 32, 2, 2>(stream, a, akc, bkc);
+    }
+    if (bm == 64) {
+        // 2 x 2 wavefronts of 32x32, BK = 32, two stages (32 KB). Against BK = 16
+        // (MIGEMM_DVAR=5) and three stages (MIGEMM_DVAR=6), us: 1024^3 22.4 / 22.6 / 22.5,
+        // 2048 x 512 x 2048 38.8 / 40.1 / 43.6, 3072 x 1024 x 3072 157.1 / 156.0 / 151.9.
+        if (var == 5) return launch_layouts<64, 64, 16, 2, 2>(stream, a, akc, bkc);
+        if (var == 6) return launch_layouts<64, 64, 32, 3, 2>(stream, a, akc, bkc);
+        return launch_layouts<64, 64, 32, 2, 2>(stream, a, akc, bkc);
     }
     if (bn == 256) {
         // BK = 16 with three stages (2 x 72 KB: two work-groups per CU). At 4096 x K x 4096

@@ -608,20 +608,21 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     // to NN at 4096 x K x 4096, K = 256 .. 4096 (time = tiles per CU x area x (K + o) /
     // rate), in one process on one box:
     //   operands loaded straight into LDS (gemm_direct_kernel; 16-byte aligned rows):
-    //     256x256 151.6 TFLOP/s, o = 70; 128x256 150.8, o = 89; 128x128 147.7, o = 83;
-    //     64x64 (register-staged) 129.5, o = 64;
+    //     256x256 152.6 TFLOP/s, o = 75; 128x256 152.1, o = 98; 128x128 147.6, o = 90;
+    //     64x64 135.2, o = 95;
     //   register-staged kernels (other 128-bit operands): 256x256 147.2, o = 73; 128x256
     //     140.6, o = 99; 128x128 138.9, o = 78; 64x64 134.2, o = 75.
-    // The tile count's quantization then decides: 3072 x 1024 x 3072 runs 173.9 us in 64x64
-    // tiles (9 per CU) against 189.0 in 128x128 (2.25 per CU); 4096 x 256 x 4096 72.0 in
-    // 256x256 against 77.4 in 128x128. With direct loads 128x128 tiles are also weighed for
-    // outputs of 256-511 of them (2048^3 TN: 142.2 us against 160.1 in 64x64 tiles).
+    // The tile count's quantization then decides: 3072 x 1024 x 3072 runs 168.7 us in 64x64
+    // tiles (9 per CU) against 190.1 in 128x128 (2.25 per CU); 4096 x 256 x 4096 74.4 in
+    // 256x256 against 82.1 in 128x128. (Outputs of 256-511 tiles of 128x128 stay on 64x64
+    // tiles: one 4-wavefront work-group per CU hides latency poorly, 2048 x 1024 x 2048 TN
+    // 81.0 us in direct 64x64 tiles against 86.3 in 128x128.)
     // Element-wise loads (M, N or K not a multiple of 4) keep the earlier three-shape model:
     // 256x256 work-groups fill a CU alone, their prologue and C store not overlapped (about
     // 32 k-steps per tile, 16 for 128x256), which decides short K: 12000 x 6565 x 500 runs
     // 729 us at 128x128, 747 at 256x256.
     const bool direct = av && bv && direct_loads(d);
-    if (splits == 1 && (cfg == 128 || (cfg == 64 && direct && tiles(128, 128) >= 256))) {
+    if (cfg == 128 && splits == 1) {
         const double k = d.K;
         auto cost = [&](int bm, int bn, double rate, double over) {
             return (double)((tiles(bm, bn) + 255) / 256) * bm * bn * (k + over) / rate;
@@ -629,10 +630,10 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         if (av && bv) {
             double c64, c0, c1, c2;
             if (direct) {
-                c64 = cost(64, 64, 129.5, 64);
-                c0 = cost(128, 128, 147.7, 83);
-                c1 = cost(128, 256, 150.8, 89);
-                c2 = cost(256, 256, 151.6, 70);
+                c64 = cost(64, 64, 135.2, 95);
+                c0 = cost(128, 128, 147.6, 90);
+                c1 = cost(128, 256, 152.1, 98);
+                c2 = cost(256, 256, 152.6, 75);
             } else {
                 c64 = cost(64, 64, 134.2, 75);
                 c0 = cost(128, 128, 138.9, 78);
@@ -723,7 +724,15 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
                 else
                     rc = launch_tiles<128, 128, 16, 4, 1>(stream, a, akc, bkc, av, bv);
                 break;
-            case 64: rc = launch_tiles<64, 64, 32, 2, 2>(stream, a, akc, bkc, av, bv); break;
+            case 64:
+                // Unsplit 64x64 tiles load straight into LDS (4-13 % faster than the staged
+                // kernel: 1024^3 25.4 -> 22.4 us, 2048 x 1024 x 2048 TN 77.8 -> 68.9);
+                // MIGEMM_DVAR=9 keeps them register-staged for comparisons.
+                if (direct && (splits == 1 || direct_mode() == 2) && env_int("MIGEMM_DVAR") != 9)
+                    rc = launch_gemm_direct(stream, a, 64, 64, akc, bkc);
+                else
+                    rc = launch_tiles<64, 64, 32, 2, 2>(stream, a, akc, bkc, av, bv);
+                break;
             default: rc = launch_tiles<32, 32, 32, 1, 1>(stream, a, akc, bkc, av, bv); break;
         }
     }

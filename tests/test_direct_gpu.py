@@ -1,5 +1,5 @@
 """GPU parity of the tiled kernel whose operands are loaded straight into LDS
-(gemm_direct_kernel: 256x256, 128x256 and 128x128 tiles), through the C ABI.
+(gemm_direct_kernel: 256x256, 128x256, 128x128 and 64x64 tiles), through the C ABI.
 
 The kernel runs a three-stage LDS pipeline over 16-wide k-tiles: a prologue of one or two
 tiles, a main loop of three tiles per pass, a remainder of one or two, and a zero-filled K
@@ -53,10 +53,10 @@ class _Env:
                 os.environ[k] = v
 
 
-@pytest.fixture(params=["256", "128x256", "128"])
+@pytest.fixture(params=["256", "128x256", "128", "64"])
 def tiled256(request):
     """The TILED policy with one macro-tile forced (MIGEMM_TILE: 256x256, 128x256,
-    128x128), direct loads forced wherever they apply (MIGEMM_DIRECT=2: also for split-K
+    128x128, 64x64), direct loads forced wherever they apply (MIGEMM_DIRECT=2: also for split-K
     ranges of 128-wide tiles, which the library's own choice runs register-staged)."""
     from my_pytchon_opencl_lib_amd import _native
     env = _Env()
