@@ -37,11 +37,12 @@
 namespace migemm {
 namespace {
 
-// s_waitcnt vmcnt(N) with expcnt and lgkmcnt left at their maxima (N < 16).
+// s_waitcnt vmcnt(N) with expcnt and lgkmcnt left at their maxima. The 6-bit vmcnt field
+// is split over bits 3:0 and 15:14 of the immediate.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 16, "vmcnt immediate");
-    __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+    static_assert(N >= 0 && N < 64, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
 typedef __attribute__((address_space(3))) float *lds_ptr_t;
@@ -56,6 +57,16 @@ typedef __attribute__((address_space(3))) float *lds_ptr_t;
 __device__ __forceinline__ void dma16(const char *sbase, uint32_t voff, float *dst) {
     const uint32_t lds = (uint32_t)(uintptr_t)(lds_ptr_t)dst;
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds)
+                 : "memory", "m0");
+}
+
+// global_load_lds_dword, the 4-byte form for operands whose rows are not 16-byte aligned:
+// each lane's float at sbase + voff goes to LDS at `dst` + 4 * lane.
+__device__ __forceinline__ void dma4(const char *sbase, uint32_t voff, float *dst) {
+    const uint32_t lds = (uint32_t)(uintptr_t)(lds_ptr_t)dst;
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1"
                  :
                  : "v"(voff), "s"(sbase), "s"(lds)
                  : "memory", "m0");
@@ -83,26 +94,30 @@ __device__ __forceinline__ int kc_swz(int r) {
 // column on alternate groups of 4 k-rows puts them on complementary halves of the 64 banks.
 __device__ __forceinline__ int ic_swz(int k) { return ((k >> 2) & 1) << 5; }
 
-// One operand of a T x BK tile (T = 128 or 256 rows of the M or N dimension). A load
-// instruction fills 1 KB: KC, 64 / (BK / 4) whole rows; otherwise 256 / T whole k-rows.
-// NS = instructions per wavefront per tile. The loads address memory as a wave-uniform base
-// (the tile's first row / column at k-tile 0, advanced per k-tile in scalar registers) plus
-// a 32-bit per-lane byte offset, which keeps the per-lane state to one register per
-// instruction; the launcher checks that the offsets fit.
-template <int NT, bool KC, int BK, int T>
+// One operand of a T x BK tile (T = 64, 128 or 256 rows of the M or N dimension), loaded W
+// floats per lane (W = 4: global_load_lds_dwordx4, rows 16-byte aligned and the contiguous
+// extent a multiple of 4; W = 1: global_load_lds_dword, any operand). A load instruction
+// fills the next 64 W floats of the tile in LDS order: lane L the W floats at LDS position
+// 64 W q + W L, which hold tile row / k-row f / BK (KC) or f / T (I-contiguous), de-swizzled
+// to the element they must contain. NS = instructions per wavefront per tile. The loads
+// address memory as a wave-uniform base (the tile's first row / column at k-tile 0,
+// advanced per k-tile in scalar registers) plus a 32-bit per-lane byte offset, which keeps
+// the per-lane state to one register per instruction; the launcher checks that the offsets
+// fit.
+template <int NT, bool KC, int BK, int T, int W>
 struct DlOperand {
     static_assert(T == 64 || T == 128 || T == 256, "tile edge");
+    static_assert(W == 1 || W == 4, "floats per lane");
     static constexpr int NW = NT / 64;
-    static constexpr int NI = T * BK / 256;  // load instructions per tile
+    static constexpr int FPI = 64 * W;       // floats per load instruction
+    static constexpr int NI = T * BK / FPI;  // load instructions per tile
     static constexpr int NS = NI / NW;
     static_assert(NS >= 1 && NS * NW == NI, "the tile's loads split evenly over the wavefronts");
-    static constexpr int CPR = BK / 4;
-    static constexpr int RPI = KC ? 64 / CPR : 256 / T;  // rows (KC) / k-rows per instruction
     static constexpr int FLOATS = T * BK;
     const char *base;      // wave-uniform: element (i0, 0) of the operand
     uint32_t voff[NS];     // this lane's byte offset from `base` at k-tile 0
+    int kk[NS];            // the k (within a tile) of this lane's first float
     int q0;                // first instruction of this wavefront (wave-uniform)
-    int c[NS];             // KC: the logical chunk this lane fetches per instruction
 
     __device__ __forceinline__ void init(const float *op, int64_t ld, int i0, int rows,
                                          int wave, int lane) {
@@ -110,24 +125,26 @@ struct DlOperand {
         base = reinterpret_cast<const char *>(op + (KC ? (int64_t)i0 * ld : (int64_t)i0));
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
-            const int q = q0 + j;
+            const int f = FPI * (q0 + j) + W * lane;  // LDS position within the tile
             if constexpr (KC) {
-                const int r = RPI * q + lane / CPR;  // tile row
-                c[j] = (lane % CPR) ^ kc_swz<BK>(r);
+                const int r = f / BK;                 // tile row
+                const int pos = f % BK;
+                const int k = 4 * ((pos / 4) ^ kc_swz<BK>(r)) + pos % 4;
                 int gi = i0 + r;
                 gi = gi < rows ? gi : rows - 1;
-                voff[j] = (uint32_t)(((gi - i0) * (uint32_t)ld + 4 * c[j]) * 4);
+                kk[j] = k;
+                voff[j] = (uint32_t)(((gi - i0) * (uint32_t)ld + k) * 4);
             } else {
-                const int k = RPI * q + lane / (T / 4);  // k-row of the tile
-                c[j] = 0;
-                int gi = i0 + ((4 * (lane % (T / 4))) ^ ic_swz(k));
-                gi = gi < rows ? gi : rows - 4;
+                const int k = f / T;                  // k-row of the tile
+                int gi = i0 + ((f % T) ^ ic_swz(k));
+                gi = gi < rows ? gi : rows - W;
+                kk[j] = k;
                 voff[j] = (uint32_t)((k * (uint32_t)ld + (gi - i0)) * 4);
             }
         }
     }
 
-    __device__ __forceinline__ int lds_off(int j) const { return (q0 + j) * 256; }
+    __device__ __forceinline__ int lds_off(int j) const { return (q0 + j) * FPI; }
 
     __device__ __forceinline__ const char *tile_base(int kt, int64_t ld) const {
         return base + (KC ? (int64_t)kt * BK * 4 : (int64_t)kt * BK * ld * 4);
@@ -137,7 +154,12 @@ struct DlOperand {
     __device__ __forceinline__ void issue(float *stage, int kt, int64_t ld) const {
         const char *tb = tile_base(kt, ld);
 #pragma unroll
-        for (int j = 0; j < NS; ++j) dma16(tb, voff[j], stage + lds_off(j));
+        for (int j = 0; j < NS; ++j) {
+            if constexpr (W == 4)
+                dma16(tb, voff[j], stage + lds_off(j));
+            else
+                dma4(tb, voff[j], stage + lds_off(j));
+        }
     }
 
     // The tail tile kt (k0 = BK kt, k0 + BK > K) through registers, k >= K zero-filled,
@@ -148,16 +170,20 @@ struct DlOperand {
         const char *tb = tile_base(kt, ld);
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
-            f4 v = {0.f, 0.f, 0.f, 0.f};
             const float *src = reinterpret_cast<const float *>(tb + voff[j]);
-            if constexpr (KC) {
+            if constexpr (W == 4) {
+                f4 v = {0.f, 0.f, 0.f, 0.f};
+                if constexpr (KC) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (k0 + 4 * c[j] + e < K) v[e] = src[e];
+                    for (int e = 0; e < 4; ++e)
+                        if (k0 + kk[j] + e < K) v[e] = src[e];
+                } else {
+                    if (k0 + kk[j] < K) v = dl_load16(src);
+                }
+                *reinterpret_cast<f4 *>(stage + lds_off(j) + 4 * lane) = v;
             } else {
-                if (k0 + RPI * (q0 + j) + lane / (T / 4) < K) v = dl_load16(src);
+                stage[lds_off(j) + lane] = k0 + kk[j] < K ? *src : 0.f;
             }
-            *reinterpret_cast<f4 *>(stage + lds_off(j) + 4 * lane) = v;
         }
     }
 };
@@ -188,7 +214,8 @@ __device__ __forceinline__ void dl_frags(const float *lds, int off, int g, int l
 // BM x BN tiles, WM x WN wavefronts; S LDS stages; tile kt lives in stage (kt - kt0) % S
 // and is loaded D (<= S) tiles ahead. OCC: wavefronts per SIMD the register allocation must
 // allow (4 for four 4-wavefront work-groups per CU).
-template <int BM, int BN, int WM, int WN, bool AKC, bool BKC, int BK, int S, int D, int OCC>
+template <int BM, int BN, int WM, int WN, bool AKC, bool BKC, int BK, int S, int D, int OCC,
+          int WA, int WB>
 __global__ void __launch_bounds__(WM *WN * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
 gemm_direct_kernel(TiledArgs p) {
     static_assert(D >= 2 && D <= S, "loads run 2..S tiles ahead");
@@ -199,8 +226,8 @@ gemm_direct_kernel(TiledArgs p) {
     constexpr int FN = WTN / 32;
     constexpr int G = BK / 8;  // k-groups per tile
     static_assert(FM >= 1 && FN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "bad wave tile");
-    typedef DlOperand<NT, AKC, BK, BM> OpA;
-    typedef DlOperand<NT, BKC, BK, BN> OpB;
+    typedef DlOperand<NT, AKC, BK, BM, WA> OpA;
+    typedef DlOperand<NT, BKC, BK, BN, WB> OpB;
     constexpr int A_FL = OpA::FLOATS;
     constexpr int B_FL = OpB::FLOATS;
     // One array per operand, so each wavefront reads every stage of an operand from one
@@ -327,7 +354,8 @@ gemm_direct_kernel(TiledArgs p) {
     store_tile<FM, FN>(p, tc, tc.m0 + wm * WTM, tc.n0 + wn * WTN, lane, acc);
 }
 
-template <int BM, int BN, int WM, int WN, bool AKC, bool BKC, int BK, int S, int D, int OCC>
+template <int BM, int BN, int WM, int WN, bool AKC, bool BKC, int BK, int S, int D, int OCC,
+          int WA = 4, int WB = 4>
 int launch_direct(hipStream_t s, TiledArgs &a) {
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
@@ -340,29 +368,39 @@ int launch_direct(hipStream_t s, TiledArgs &a) {
         return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm: %lld tiles exceed one launch",
                          (long long)total);
     a.total = (int)total;
-    hipLaunchKernelGGL((gemm_direct_kernel<BM, BN, WM, WN, AKC, BKC, BK, S, D, OCC>), dim3(a.total),
+    hipLaunchKernelGGL((gemm_direct_kernel<BM, BN, WM, WN, AKC, BKC, BK, S, D, OCC, WA, WB>),
+                       dim3(a.total),
                        dim3(WM * WN * 64), 0, s, a);
     return hip_check(hipGetLastError(), "gemm_direct_kernel launch");
 }
 
 // Every operand layout (NN, NT, TN, TT) with wavefronts of 32x128 (64x64 tiles: 2 x 2
 // wavefronts of 32x32).
-template <int BM, int BN, int BK, int S, int D, int OCC = 1>
+template <int BM, int BN, int BK, int S, int D, int OCC = 1, int WA = 4, int WB = 4>
 int launch_layouts(hipStream_t s, TiledArgs &a, bool akc, bool bkc) {
     constexpr int WM = BN >= 128 ? BM / 32 : 2;
     constexpr int WN = BN >= 128 ? BN / 128 : 2;
-    if (akc && bkc) return launch_direct<BM, BN, WM, WN, true, true, BK, S, D, OCC>(s, a);
-    if (akc) return launch_direct<BM, BN, WM, WN, true, false, BK, S, D, OCC>(s, a);
-    if (!bkc) return launch_direct<BM, BN, WM, WN, false, false, BK, S, D, OCC>(s, a);
-    return launch_direct<BM, BN, WM, WN, false, true, BK, S, D, OCC>(s, a);
+    if (akc && bkc) return launch_direct<BM, BN, WM, WN, true, true, BK, S, D, OCC, WA, WB>(s, a);
+    if (akc) return launch_direct<BM, BN, WM, WN, true, false, BK, S, D, OCC, WA, WB>(s, a);
+    if (!bkc) return launch_direct<BM, BN, WM, WN, false, false, BK, S, D, OCC, WA, WB>(s, a);
+    return launch_direct<BM, BN, WM, WN, false, true, BK, S, D, OCC, WA, WB>(s, a);
 }
 
 }  // namespace
 
-int launch_gemm_direct(hipStream_t stream, TiledArgs &a, int bm, int bn, bool akc, bool bkc) {
+int launch_gemm_direct(hipStream_t stream, TiledArgs &a, int bm, int bn, bool akc, bool bkc,
+                       int wa, int wb) {
     // MIGEMM_DVAR (read per call) selects pipeline variants for tuning sweeps.
     const char *v = getenv("MIGEMM_DVAR");
     const int var = v != nullptr ? atoi(v) : 0;
+    if (wa != 4 || wb != 4) {
+        // An operand loaded 4 bytes per lane (rows not 16-byte aligned): 64x64 tiles only.
+        if (bm != 64 || bn != 64)
+            return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm: 4-byte direct loads need 64x64 tiles");
+        if (wa == 1 && wb == 1) return launch_layouts<64, 64, 32, 2, 2, 1, 1, 1>(stream, a, akc, bkc);
+        if (wa == 1) return launch_layouts<64, 64, 32, 2, 2, 1, 1, 4>(stream, a, akc, bkc);
+        return launch_layouts<64, 64, 32, 2, 2, 1, 4, 1>(stream, a, akc, bkc);
+    }
     if (bm == 256) {
         // BK = 32 with two stages, loads two tiles ahead (2 x 128 KB of LDS, one barrier per
         // 32 k). Measured at 4096^3 against BK = 16 with three stages (MIGEMM_DVAR=1),

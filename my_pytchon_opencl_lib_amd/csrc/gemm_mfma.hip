@@ -506,15 +506,10 @@ int direct_mode() {
     return v != nullptr ? atoi(v) : 1;
 }
 
-// gemm_direct_kernel's loads apply: every row and batch entry of both operands starts on a
-// 16-byte boundary (the loads into LDS move aligned 16-byte pieces), and a lane's offset
-// within a 256-row panel fits the loads' 32-bit offsets.
-bool direct_loads(const GemmDesc &d) {
-    if (direct_mode() == 0) return false;
-    auto ok = [](const float *p, int64_t ld, int64_t stride) {
-        return ((uintptr_t)p & 15) == 0 && ld % 4 == 0 && stride % 4 == 0 && ld <= (1 << 21);
-    };
-    return ok(d.A, d.lda, d.sA) && ok(d.B, d.ldb, d.sB);
+// An operand's rows and batch entries all start on 16-byte boundaries, as
+// global_load_lds_dwordx4 needs.
+bool rows16(const float *p, int64_t ld, int64_t stride) {
+    return ((uintptr_t)p & 15) == 0 && ld % 4 == 0 && stride % 4 == 0;
 }
 }  // namespace
 
@@ -621,7 +616,13 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     // 256x256 work-groups fill a CU alone, their prologue and C store not overlapped (about
     // 32 k-steps per tile, 16 for 128x256), which decides short K: 12000 x 6565 x 500 runs
     // 729 us at 128x128, 747 at 256x256.
-    const bool direct = av && bv && direct_loads(d);
+    // gemm_direct_kernel applies when a lane's offset within a 256-row panel fits its loads'
+    // 32-bit offsets; with both operands loaded 16 bytes per lane (wa = wb = 4) for any tile,
+    // with 4-byte loads for an unaligned operand for 64x64 tiles.
+    const int wa = av && rows16(d.A, d.lda, d.sA) ? 4 : 1;
+    const int wb = bv && rows16(d.B, d.ldb, d.sB) ? 4 : 1;
+    const bool fits = direct_mode() != 0 && d.lda <= (1 << 21) && d.ldb <= (1 << 21);
+    const bool direct = fits && wa == 4 && wb == 4;
     if (cfg == 128 && splits == 1) {
         const double k = d.K;
         auto cost = [&](int bm, int bn, double rate, double over) {
@@ -728,8 +729,8 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
                 // Unsplit 64x64 tiles load straight into LDS (4-13 % faster than the staged
                 // kernel: 1024^3 25.4 -> 22.4 us, 2048 x 1024 x 2048 TN 77.8 -> 68.9);
                 // MIGEMM_DVAR=9 keeps them register-staged for comparisons.
-                if (direct && (splits == 1 || direct_mode() == 2) && env_int("MIGEMM_DVAR") != 9)
-                    rc = launch_gemm_direct(stream, a, 64, 64, akc, bkc);
+                if (fits && (splits == 1 || direct_mode() == 2) && env_int("MIGEMM_DVAR") != 9)
+                    rc = launch_gemm_direct(stream, a, 64, 64, akc, bkc, wa, wb);
                 else
                     rc = launch_tiles<64, 64, 32, 2, 2>(stream, a, akc, bkc, av, bv);
                 break;

@@ -119,12 +119,14 @@ __device__ __forceinline__ void store_tile(const TiledArgs &p, const TileCoord &
         store(std::false_type{});
 }
 
-// Tiles of bm x bn (256x256, 128x256 or 128x128) with operands loaded straight into LDS
-// (gemm_direct.hip). Requires every contiguous extent to be a multiple of 4 (K for a
-// K-contiguous operand, M or N otherwise) and 16-byte aligned rows and batch entries.
+// Tiles of bm x bn (256x256, 128x256, 128x128 or 64x64) with operands loaded straight into
+// LDS (gemm_direct.hip). wa / wb: floats per lane of each operand's loads, 4 (every row and
+// batch entry 16-byte aligned and the contiguous extent a multiple of 4: K for a
+// K-contiguous operand, M or N otherwise) or 1 (any operand; 64x64 tiles only).
 // On entry a.splits is the requested number of split-K ranges; on return `a` holds the grid
 // (tiles_m, tiles_n, kt_per_split in the kernel's k-tiles, total) and the non-empty range
 // count.
-int launch_gemm_direct(hipStream_t stream, TiledArgs &a, int bm, int bn, bool akc, bool bkc);
+int launch_gemm_direct(hipStream_t stream, TiledArgs &a, int bm, int bn, bool akc, bool bkc,
+                       int wa = 4, int wb = 4);
 
 }  // namespace migemm

@@ -1,11 +1,12 @@
 """Checks on the generated gfx950 code of the direct-to-LDS GEMM kernel (CPU only: hipcc
 cross-compiles the device code to assembly text).
 
-gemm_direct.hip issues global_load_lds_dwordx4 through inline assembly that sets M0 itself
-and declares it clobbered. M0 is a register the compiler reserves, so the kernels may only
-be correct if no compiler-generated code relies on M0 across those statements. This test
-pins that: in the device assembly, M0 is written only by `s_mov_b32 m0, s<n>` immediately
-followed by a global_load_lds_dwordx4, and nothing reads it otherwise."""
+gemm_direct.hip issues global_load_lds_dwordx4 / global_load_lds_dword through inline
+assembly that sets M0 itself and declares it clobbered. M0 is a register the compiler
+reserves, so the kernels may only be correct if no compiler-generated code relies on M0
+across those statements. This test pins that: in the device assembly, M0 is written only by
+`s_mov_b32 m0, s<n>` immediately followed by one of those loads, and nothing reads it
+otherwise."""
 import os
 import re
 import shutil
@@ -38,9 +39,9 @@ def test_m0_only_feeds_the_lds_loads(tmp_path):
         if not re.search(r"\bm0\b", l):
             continue
         assert re.fullmatch(r"s_mov_b32 m0, s\d+", l), f"unexpected use of M0: {l!r}"
-        assert code[i + 1].startswith("global_load_lds_dwordx4"), \
+        assert re.match(r"global_load_lds_dword(x4)? ", code[i + 1]), \
             f"M0 written without a following LDS load: {l!r} then {code[i + 1]!r}"
         loads += 1
-    assert loads > 0, "no global_load_lds_dwordx4 found"
-    n_lds = sum(1 for l in code if l.startswith("global_load_lds_dwordx4"))
+    assert loads > 0, "no global_load_lds_dword(x4) found"
+    n_lds = sum(1 for l in code if re.match(r"global_load_lds_dword(x4)? ", l))
     assert n_lds == loads, (n_lds, loads)

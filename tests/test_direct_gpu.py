@@ -161,9 +161,10 @@ def test_direct_equals_staged_kernel(tiled256, ta, tb):
         assert np.array_equal(outs[0], outs[1])
 
 
-def test_unaligned_rows_use_staged_kernel(tiled256):
+def test_unaligned_rows(tiled256):
     """Leading dimensions that are not multiples of 4 (rows off 16-byte boundaries) and an
-    operand starting 4 bytes into its buffer take the register-staged kernel; exact."""
+    operand starting 4 bytes into its buffer: 4-byte loads into LDS for 64x64 tiles, the
+    register-staged kernel for larger tiles; exact."""
     M, K, N = 300, 100, 260
     for lda, ldb, off in [(K + 1, N, 0), (K, N + 2, 0), (K, N, 1)]:
         say("direct unaligned", lda, ldb, off)
@@ -176,3 +177,36 @@ def test_unaligned_rows_use_staged_kernel(tiled256):
         gemm_ex(0, 0, M, N, K, av, lda, 0, b, ldb, 0, None, c, N, 0, 1)
         expect = A[:, :K].astype(np.float64) @ B[:, :N].astype(np.float64)
         assert np.array_equal(host(c), expect.astype(np.float32))
+
+
+UNALIGNED = [(67, 5, 129), (130, 33, 70), (257, 131, 259), (1000, 777, 300), (64, 777, 64)]
+
+
+@pytest.mark.parametrize("M,K,N", UNALIGNED)
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_direct_unaligned_operands_exact(tiled256, M, K, N, ta, tb):
+    """Odd K, M and N (contiguous extents not multiples of 4, rows off 16-byte boundaries):
+    64x64 tiles load such operands 4 bytes per lane (global_load_lds_dword); larger tiles take
+    the register-staged kernel. Exact small-integer products, batch 2 with bias."""
+    say("direct unaligned exact", M, K, N, ta, tb)
+    got, expect = run_exact(M, K, N, ta, tb, batch=2, bias=True, seed=M * 3 + K + N + ta)
+    assert np.array_equal(got, expect)
+
+
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_direct_unaligned_equals_staged_kernel(tiled256, ta, tb):
+    """N(0,1) operands with odd K / M / N (4-byte loads into LDS for 64x64 tiles) give the
+    same bits as the register-staged kernel of the same tile (one split range)."""
+    tiled256.set(MIGEMM_SPLITK=1)
+    g = torch.Generator(device="cpu").manual_seed(99 + ta + 2 * tb)
+    for M, K, N in [(1000, 777, 3000), (131, 1001, 257)]:
+        say("direct unaligned vs staged", M, K, N, ta, tb)
+        A = torch.randn((K, M) if ta else (M, K), generator=g).cuda()
+        B = torch.randn((N, K) if tb else (K, N), generator=g).cuda()
+        outs = []
+        for direct in (2, 0):
+            tiled256.set(MIGEMM_DIRECT=direct)
+            c = torch.empty((M, N), device="cuda")
+            gemm_ex(ta, tb, M, N, K, A, A.shape[1], 0, B, B.shape[1], 0, None, c, N, 0, 1)
+            outs.append(host(c))
+        assert np.array_equal(outs[0], outs[1])
