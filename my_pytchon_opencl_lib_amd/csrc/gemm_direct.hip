@@ -394,12 +394,26 @@ int launch_gemm_direct(hipStream_t stream, TiledArgs &a, int bm, int bn, bool ak
     const char *v = getenv("MIGEMM_DVAR");
     const int var = v != nullptr ? atoi(v) : 0;
     if (wa != 4 || wb != 4) {
-        // An operand loaded 4 bytes per lane (rows not 16-byte aligned): 64x64 tiles only.
-        if (bm != 64 || bn != 64)
-            return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm: 4-byte direct loads need 64x64 tiles");
-        if (wa == 1 && wb == 1) return launch_layouts<64, 64, 32, 2, 2, 1, 1, 1>(stream, a, akc, bkc);
-        if (wa == 1) return launch_layouts<64, 64, 32, 2, 2, 1, 1, 4>(stream, a, akc, bkc);
-        return launch_layouts<64, 64, 32, 2, 2, 1, 4, 1>(stream, a, akc, bkc);
+        // An operand loaded 4 bytes per lane (rows not 16-byte aligned, or a contiguous
+        // extent that is not a multiple of 4), in the shipped pipeline of each tile.
+        if (bm == 64) {
+            if (wa == 1 && wb == 1) return launch_layouts<64, 64, 32, 2, 2, 1, 1, 1>(stream, a, akc, bkc);
+            if (wa == 1) return launch_layouts<64, 64, 32, 2, 2, 1, 1, 4>(stream, a, akc, bkc);
+            return launch_layouts<64, 64, 32, 2, 2, 1, 4, 1>(stream, a, akc, bkc);
+        }
+        if (bm == 256) {
+            if (wa == 1 && wb == 1) return launch_layouts<256, 256, 32, 2, 2, 1, 1, 1>(stream, a, akc, bkc);
+            if (wa == 1) return launch_layouts<256, 256, 32, 2, 2, 1, 1, 4>(stream, a, akc, bkc);
+            return launch_layouts<256, 256, 32, 2, 2, 1, 4, 1>(stream, a, akc, bkc);
+        }
+        if (bn == 256) {
+            if (wa == 1 && wb == 1) return launch_layouts<128, 256, 16, 3, 2, 1, 1, 1>(stream, a, akc, bkc);
+            if (wa == 1) return launch_layouts<128, 256, 16, 3, 2, 1, 1, 4>(stream, a, akc, bkc);
+            return launch_layouts<128, 256, 16, 3, 2, 1, 4, 1>(stream, a, akc, bkc);
+        }
+        if (wa == 1 && wb == 1) return launch_layouts<128, 128, 16, 2, 2, 4, 1, 1>(stream, a, akc, bkc);
+        if (wa == 1) return launch_layouts<128, 128, 16, 2, 2, 4, 1, 4>(stream, a, akc, bkc);
+        return launch_layouts<128, 128, 16, 2, 2, 4, 4, 1>(stream, a, akc, bkc);
     }
     if (bm == 256) {
         // BK = 32 with two stages, loads two tiles ahead (2 x 128 KB of LDS, one barrier per

@@ -617,8 +617,8 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     // 32 k-steps per tile, 16 for 128x256), which decides short K: 12000 x 6565 x 500 runs
     // 729 us at 128x128, 747 at 256x256.
     // gemm_direct_kernel applies when a lane's offset within a 256-row panel fits its loads'
-    // 32-bit offsets; with both operands loaded 16 bytes per lane (wa = wb = 4) for any tile,
-    // with 4-byte loads for an unaligned operand for 64x64 tiles.
+    // 32-bit offsets: an operand with 16-byte aligned rows and a contiguous extent that is a
+    // multiple of 4 is loaded 16 bytes per lane (wa / wb = 4), any other 4 bytes per lane.
     const int wa = av && rows16(d.A, d.lda, d.sA) ? 4 : 1;
     const int wb = bv && rows16(d.B, d.ldb, d.sB) ? 4 : 1;
     const bool fits = direct_mode() != 0 && d.lda <= (1 << 21) && d.ldb <= (1 << 21);
@@ -711,9 +711,11 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
                 // ranges 268.3 against 246.1 us, 1536 x 4096 x 1536 in 8: 190.4 / 180.9,
                 // 1000 x 4096 x 3000 in 6: 253.1 / 233.9), while split 256x256 tiles gain
                 // (1024 x 6400 x 4096 TN in 4 ranges: 383.2 / 395.8).
-                if (direct && (big == 2 || splits == 1 || direct_mode() == 2))
+                // An unaligned operand is loaded 4 bytes per lane: Linear(500 -> 6565) forward
+                // 12000 x 500 x 6565 735.3 -> 648.8 us, 4096 x 4096 x 4095 TN 1015.6 -> 924.1.
+                if (fits && (big == 2 || splits == 1 || direct_mode() == 2))
                     rc = launch_gemm_direct(stream, a, big == 2 ? 256 : 128, big >= 1 ? 256 : 128,
-                                            akc, bkc);
+                                            akc, bkc, wa, wb);
                 else if (big == 2 && akc && bkc)
                     rc = launch_tiles<256, 256, 32, 8, 2, 3>(stream, a, akc, bkc, av, bv);
                 else if (big == 2 && !akc && !bkc)

@@ -122,7 +122,7 @@ __device__ __forceinline__ void store_tile(const TiledArgs &p, const TileCoord &
 // Tiles of bm x bn (256x256, 128x256, 128x128 or 64x64) with operands loaded straight into
 // LDS (gemm_direct.hip). wa / wb: floats per lane of each operand's loads, 4 (every row and
 // batch entry 16-byte aligned and the contiguous extent a multiple of 4: K for a
-// K-contiguous operand, M or N otherwise) or 1 (any operand; 64x64 tiles only).
+// K-contiguous operand, M or N otherwise) or 1 (any operand).
 // On entry a.splits is the requested number of split-K ranges; on return `a` holds the grid
 // (tiles_m, tiles_n, kt_per_split in the kernel's k-tiles, total) and the non-empty range
 // count.

@@ -163,8 +163,7 @@ def test_direct_equals_staged_kernel(tiled256, ta, tb):
 
 def test_unaligned_rows(tiled256):
     """Leading dimensions that are not multiples of 4 (rows off 16-byte boundaries) and an
-    operand starting 4 bytes into its buffer: 4-byte loads into LDS for 64x64 tiles, the
-    register-staged kernel for larger tiles; exact."""
+    operand starting 4 bytes into its buffer: 4-byte loads into LDS; exact."""
     M, K, N = 300, 100, 260
     for lda, ldb, off in [(K + 1, N, 0), (K, N + 2, 0), (K, N, 1)]:
         say("direct unaligned", lda, ldb, off)
@@ -186,8 +185,8 @@ UNALIGNED = [(67, 5, 129), (130, 33, 70), (257, 131, 259), (1000, 777, 300), (64
 @pytest.mark.parametrize("ta,tb", LAYOUTS)
 def test_direct_unaligned_operands_exact(tiled256, M, K, N, ta, tb):
     """Odd K, M and N (contiguous extents not multiples of 4, rows off 16-byte boundaries):
-    64x64 tiles load such operands 4 bytes per lane (global_load_lds_dword); larger tiles take
-    the register-staged kernel. Exact small-integer products, batch 2 with bias."""
+    such operands are loaded 4 bytes per lane (global_load_lds_dword). Exact small-integer
+    products, batch 2 with bias."""
     say("direct unaligned exact", M, K, N, ta, tb)
     got, expect = run_exact(M, K, N, ta, tb, batch=2, bias=True, seed=M * 3 + K + N + ta)
     assert np.array_equal(got, expect)
@@ -195,8 +194,8 @@ def test_direct_unaligned_operands_exact(tiled256, M, K, N, ta, tb):
 
 @pytest.mark.parametrize("ta,tb", LAYOUTS)
 def test_direct_unaligned_equals_staged_kernel(tiled256, ta, tb):
-    """N(0,1) operands with odd K / M / N (4-byte loads into LDS for 64x64 tiles) give the
-    same bits as the register-staged kernel of the same tile (one split range)."""
+    """N(0,1) operands with odd K / M / N (4-byte loads into LDS) give the same bits as the
+    register-staged kernel of the same tile (one split range)."""
     tiled256.set(MIGEMM_SPLITK=1)
     g = torch.Generator(device="cpu").manual_seed(99 + ta + 2 * tb)
     for M, K, N in [(1000, 777, 3000), (131, 1001, 257)]:
