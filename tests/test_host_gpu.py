@@ -240,3 +240,22 @@ def test_c_caller_on_the_gpu():
     r = c_abi.run("gpu")
     assert r.returncode == 0, r.stdout + r.stderr
     assert "c_abi_check gpu: ok" in r.stdout
+
+
+def test_shared_weight_batches_run_as_one_gemm(nncl):
+    """Under the AUTO policy a batch that shares B (stride 0) with contiguous A and C entries
+    runs as one GEMM of batch * M rows: LinearForward on [8, 300, 52] -> 260 equals the
+    flattened [2400, 52] GEMM + bias bit for bit, and the NT form (dX = dY W^T) likewise."""
+    X = oracle.normal((8, 300, 52), 41, 0)
+    W = oracle.uniform((1, 52, 260), 41, 1)
+    bias = oracle.uniform((260,), 41, 2)
+    say("shared weight batches")
+    y = host(nncl.LinearForward(dev(X), dev(W), dev(bias)))
+    flat = host(nncl.gemm(dev(X.reshape(2400, 52)), dev(W[0]), bias=dev(bias)))
+    assert np.array_equal(y.reshape(2400, 260), flat)
+    G = oracle.normal((8, 300, 260), 41, 3)
+    gx = host(nncl.BmmPermute(dev(G), dev(W), transB=True))
+    flat = host(nncl.gemm(dev(G.reshape(2400, 260)), dev(W[0]), transB=True))
+    assert np.array_equal(gx.reshape(2400, 52), flat)
+    check_gemm(gx.reshape(2400, 52), G.reshape(2400, 260), W[0], 0, 1, M=2400, N=52, K=260,
+               lda=260, ldb=260)
