@@ -1,0 +1,21 @@
+// gemm_direct_kernel instantiations for 64x64 tiles (kernel: gemm_direct.hip, gemm_direct.h).
+#include "gemm_direct.h"
+
+namespace migemm {
+
+int launch_direct_64(hipStream_t stream, TiledArgs &a, bool akc, bool bkc, int wa, int wb,
+    int var) {
+    if (wa != 4 || wb != 4) {
+        if (wa == 1 && wb == 1) return launch_layouts<64, 64, 32, 2, 2, 1, 1, 1>(stream, a, akc, bkc);
+        if (wa == 1) return launch_layouts<64, 64, 32, 2, 2, 1, 1, 4>(stream, a, akc, bkc);
+        return launch_layouts<64, 64, 32, 2, 2, 1, 4, 1>(stream, a, akc, bkc);
+    }
+    // 2 x 2 wavefronts of 32x32, BK = 32, two stages (32 KB). Against BK = 16
+    // (MIGEMM_DVAR=5) and three stages (MIGEMM_DVAR=6), us: 1024^3 22.4 / 22.6 / 22.5,
+    // 2048 x 512 x 2048 38.8 / 40.1 / 43.6, 3072 x 1024 x 3072 157.1 / 156.0 / 151.9.
+    if (var == 5) return launch_layouts<64, 64, 16, 2, 2>(stream, a, akc, bkc);
+    if (var == 6) return launch_layouts<64, 64, 32, 3, 2>(stream, a, akc, bkc);
+    return launch_layouts<64, 64, 32, 2, 2>(stream, a, akc, bkc);
+}
+
+}  // namespace migemm

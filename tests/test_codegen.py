@@ -15,7 +15,9 @@ import subprocess
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-SRC = os.path.join(ROOT, "my_pytchon_opencl_lib_amd", "csrc", "gemm_direct.hip")
+CSRC = os.path.join(ROOT, "my_pytchon_opencl_lib_amd", "csrc")
+# the translation units that instantiate gemm_direct_kernel (one per tile shape)
+SRCS = [os.path.join(CSRC, f"gemm_direct_{t}.hip") for t in ("256", "128x256", "128", "64")]
 
 
 def _hipcc():
@@ -27,21 +29,26 @@ def _hipcc():
 
 @pytest.mark.skipif(_hipcc() is None, reason="hipcc not available")
 def test_m0_only_feeds_the_lds_loads(tmp_path):
-    out = tmp_path / "gemm_direct.s"
-    subprocess.run([_hipcc(), "--offload-arch=gfx950", "-O3", "-std=c++17",
-                    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-                    "-Wno-inline-asm", "--cuda-device-only", "-S", SRC, "-o", str(out)],
-                   check=True, capture_output=True)
-    lines = [l.split(";")[0].strip() for l in out.read_text().splitlines()]
-    code = [l for l in lines if l and not l.startswith(".") and not l.endswith(":")]
-    loads = 0
-    for i, l in enumerate(code):
-        if not re.search(r"\bm0\b", l):
-            continue
-        assert re.fullmatch(r"s_mov_b32 m0, s\d+", l), f"unexpected use of M0: {l!r}"
-        assert re.match(r"global_load_lds_dword(x4)? ", code[i + 1]), \
-            f"M0 written without a following LDS load: {l!r} then {code[i + 1]!r}"
-        loads += 1
-    assert loads > 0, "no global_load_lds_dword(x4) found"
-    n_lds = sum(1 for l in code if re.match(r"global_load_lds_dword(x4)? ", l))
-    assert n_lds == loads, (n_lds, loads)
+    procs = []
+    for src in SRCS:
+        out = tmp_path / (os.path.basename(src) + ".s")
+        procs.append((src, out, subprocess.Popen(
+            [_hipcc(), "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
+             "-Xclang", "-packed-fp32-ops", "-Wno-inline-asm", "--cuda-device-only", "-S", src,
+             "-o", str(out)], stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
+    for src, out, p in procs:
+        log, _ = p.communicate()
+        assert p.returncode == 0, log.decode(errors="replace")[-2000:]
+        lines = [l.split(";")[0].strip() for l in out.read_text().splitlines()]
+        code = [l for l in lines if l and not l.startswith(".") and not l.endswith(":")]
+        loads = 0
+        for i, l in enumerate(code):
+            if not re.search(r"\bm0\b", l):
+                continue
+            assert re.fullmatch(r"s_mov_b32 m0, s\d+", l), f"{src}: unexpected use of M0: {l!r}"
+            assert re.match(r"global_load_lds_dword(x4)? ", code[i + 1]), \
+                f"{src}: M0 written without a following LDS load: {l!r} then {code[i + 1]!r}"
+            loads += 1
+        assert loads > 0, f"{src}: no global_load_lds_dword(x4) found"
+        n_lds = sum(1 for l in code if re.match(r"global_load_lds_dword(x4)? ", l))
+        assert n_lds == loads, (src, n_lds, loads)
