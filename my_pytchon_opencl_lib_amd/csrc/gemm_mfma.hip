@@ -34,6 +34,7 @@
 //    (the dispatcher deals work-groups round-robin over the 8 XCDs, each with its own
 //    L2), then rastered in groups of 8 tile-rows so concurrently running tiles share
 //    A and B panels in that L2.
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -557,24 +558,55 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     // tiles, 8 ranges leave most CUs idle: 256x4096x256 41.5 against 64x64 / 16 ranges 14.1;
     // 128x4096x4096 64x64 with 4 / 5 / 8 / 16 ranges: 49.2 / 55.0 / 47.9 / 51.5;
     // 512x16384x512 TN with 5 / 8 / 10: 119.9 / 78.4 / 91.0.
+    // gemm_direct_kernel applies when a lane's offset within a 256-row panel fits its loads'
+    // 32-bit offsets: an operand with 16-byte aligned rows and a contiguous extent that is a
+    // multiple of 4 is loaded 16 bytes per lane (wa / wb = 4), any other 4 bytes per lane.
+    const int wa = av && rows16(d.A, d.lda, d.sA) ? 4 : 1;
+    const int wb = bv && rows16(d.B, d.ldb, d.sB) ? 4 : 1;
+    const bool fits = direct_mode() != 0 && d.lda <= (1 << 21) && d.ldb <= (1 << 21);
+    const bool direct = fits && wa == 4 && wb == 4;
     int cfg, splits = 1;
     int big = 0;  // 128x128 tiles; 1: 128x256, 2: 256x256 (see below)
     if (tiles(128, 128) >= 512) {
         cfg = 128;
     } else if (d.K >= 4096 && d.M >= 128 && d.N >= 128 && tiles(128, 128) >= 128) {
+        // Long K over few tiles. Weighed by time ~ rounds of 256 work-groups x 2 area
+        // (k + o) / rate (the fitted rates of the tile cost model below), plus for split
+        // ranges the partial sums' HBM traffic, (2S + 1) M N 4 bytes at ~6 TB/s:
+        //   128x128 tiles (register-staged) in S ranges, an even S <= 8 giving ~1024
+        //     work-groups;
+        //   256x256 tiles split so that every CU holds one work-group (32 or 64 tiles);
+        //   whole 64x64 tiles (loaded straight into LDS).
+        // Measured against the estimate's choice (us): 2048 x 4096 x 1024 256-split 144.6,
+        // 64x64 130.7 (chosen); 1024 x 6400 x 4096 TN 256-split 386.5 (chosen), 64x64 396.1;
+        // 512 x 6400 x 4096 TN 256-split 207.9, 64x64 203.2 (chosen); 1000 x 4096 x 3000
+        // 128-split 249.7, 64x64 198.4 (chosen); 500 x 12000 x 6565 TN 128-split 685.0
+        // (chosen), 64x64 722.4; 12000 x 6565 x 500 NT 128-split 669.8, 64x64 633.1 (chosen).
+        auto est = [](int64_t t, double area, double k, double o, double rate) {
+            return (double)((t + 255) / 256) * 256.0 * 2.0 * area * (k + o) / (rate * 1e6);
+        };
+        auto traffic = [&](int s) { return (2.0 * s + 1) * d.M * d.N * 4.0 * d.batch / 6e6; };
+        const int64_t t128 = tiles(128, 128), t256 = tiles(256, 256), t64 = tiles(64, 64);
+        int64_t want = (1024 + t128 - 1) / t128;
+        want += want & 1;
+        const int s128 = (int)(want < 8 ? want : 8);
+        double best = est(t128 * s128, 16384, (double)d.K / s128, 78, 138.9) + traffic(s128);
         cfg = 128;
-        const int64_t t256 = tiles(256, 256);
+        splits = s128;
         if (av && bv && (t256 == 32 || t256 == 64)) {
-            // 256x256 tiles split into exactly one work-group per CU (512 x 6400 x 4096 TN
-            // 225.7 -> 213.2 us, 1024 x 6400 x 4096 TN 425.3 -> 395.8, 4096 x 4096 x 1024
-            // 278.6 -> 265.8); with fewer tiles, or a count that does not divide the CUs,
-            // the 128x128 split stays faster (768 x 4096 x 3072: 182.3 against 264.2)
-            big = 2;
-            splits = (int)(256 / t256);
-        } else {
-            int64_t want = (1024 + tiles(128, 128) - 1) / tiles(128, 128);
-            want += want & 1;
-            splits = (int)(want < 8 ? want : 8);
+            const int s256 = (int)(256 / t256);
+            const double c = est(256, 65536, (double)d.K / s256, direct ? 75 : 73,
+                                 direct ? 152.6 : 147.2) + traffic(s256);
+            if (c < best) {
+                best = c;
+                big = 2;
+                splits = s256;
+            }
+        }
+        if (fits && est(t64, 4096, d.K, 95, 135.2) < best) {
+            cfg = 64;
+            big = 0;
+            splits = 1;
         }
     } else if (tiles(64, 64) >= 256 || nk32 < 8) {
         cfg = tiles(64, 64) >= 256 ? 64 : 32;
@@ -616,13 +648,6 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     // 256x256 work-groups fill a CU alone, their prologue and C store not overlapped (about
     // 32 k-steps per tile, 16 for 128x256), which decides short K: 12000 x 6565 x 500 runs
     // 729 us at 128x128, 747 at 256x256.
-    // gemm_direct_kernel applies when a lane's offset within a 256-row panel fits its loads'
-    // 32-bit offsets: an operand with 16-byte aligned rows and a contiguous extent that is a
-    // multiple of 4 is loaded 16 bytes per lane (wa / wb = 4), any other 4 bytes per lane.
-    const int wa = av && rows16(d.A, d.lda, d.sA) ? 4 : 1;
-    const int wb = bv && rows16(d.B, d.ldb, d.sB) ? 4 : 1;
-    const bool fits = direct_mode() != 0 && d.lda <= (1 << 21) && d.ldb <= (1 << 21);
-    const bool direct = fits && wa == 4 && wb == 4;
     if (cfg == 128 && splits == 1) {
         const double k = d.K;
         auto cost = [&](int bm, int bn, double rate, double over) {
@@ -669,6 +694,12 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         }
     }
     if (force_split >= 1) splits = force_split;
+    if (env_int("MIGEMM_TRACE") != 0)  // tuning aid: the dispatcher's choice, on stderr
+        fprintf(stderr, "migemm tiled %dx%dx%d batch %d t%d%d: tile %s splits %d loads %s\n", d.M,
+                d.K, d.N, d.batch, (int)d.transA, (int)d.transB,
+                cfg == 128 ? (big == 2 ? "256x256" : big == 1 ? "128x256" : "128x128")
+                           : (cfg == 64 ? "64x64" : "32x32"),
+                splits, fits ? (wa == 4 && wb == 4 ? "direct16" : "direct4") : "staged");
 
     a.splits = splits;
     a.partial = nullptr;
