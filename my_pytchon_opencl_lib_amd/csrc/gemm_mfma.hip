@@ -565,6 +565,27 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     const int wb = bv && rows16(d.B, d.ldb, d.sB) ? 4 : 1;
     const bool fits = direct_mode() != 0 && d.lda <= (1 << 21) && d.ldb <= (1 << 21);
     const bool direct = fits && wa == 4 && wb == 4;
+    // Estimated time (us) of `t` tiles of `area` outputs over k at a fitted rate (TFLOP/s)
+    // with a per-tile overhead of o k-steps: the work-groups are dealt over the 256 CUs in
+    // rounds, each round as long as one tile.
+    auto est = [](int64_t t, double area, double k, double o, double rate) {
+        return (double)((t + 255) / 256) * 256.0 * 2.0 * area * (k + o) / (rate * 1e6);
+    };
+    // Whole 128x256 or 256x256 tiles (loaded straight into LDS) instead of 64x64 ones for
+    // outputs with few 128x128 tiles, when the estimate says so: 8000 x 4096 x 1000 runs
+    // 476.1 us in 128x256 tiles against 538.9 in 64x64, 1000 x 4096 x 8000 TN 485.6 / 519.0,
+    // 8000 x 1024 x 1000 131.6 / 147.0.
+    auto wider = [&](double c64, int &cfg_out, int &big_out) {
+        const double c1 = est(tiles(128, 256), 32768, d.K, 98, 152.1);
+        const double c2 = est(tiles(256, 256), 65536, d.K, 75, 152.6);
+        if (c1 < c64 && c1 <= c2) {
+            cfg_out = 128;
+            big_out = 1;
+        } else if (c2 < c64) {
+            cfg_out = 128;
+            big_out = 2;
+        }
+    };
     int cfg, splits = 1;
     int big = 0;  // 128x128 tiles; 1: 128x256, 2: 256x256 (see below)
     if (tiles(128, 128) >= 512) {
@@ -582,9 +603,6 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         // 512 x 6400 x 4096 TN 256-split 207.9, 64x64 203.2 (chosen); 1000 x 4096 x 3000
         // 128-split 249.7, 64x64 198.4 (chosen); 500 x 12000 x 6565 TN 128-split 685.0
         // (chosen), 64x64 722.4; 12000 x 6565 x 500 NT 128-split 669.8, 64x64 633.1 (chosen).
-        auto est = [](int64_t t, double area, double k, double o, double rate) {
-            return (double)((t + 255) / 256) * 256.0 * 2.0 * area * (k + o) / (rate * 1e6);
-        };
         auto traffic = [&](int s) { return (2.0 * s + 1) * d.M * d.N * 4.0 * d.batch / 6e6; };
         const int64_t t128 = tiles(128, 128), t256 = tiles(256, 256), t64 = tiles(64, 64);
         int64_t want = (1024 + t128 - 1) / t128;
@@ -604,9 +622,19 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
             }
         }
         if (fits && est(t64, 4096, d.K, 95, 135.2) < best) {
+            best = est(t64, 4096, d.K, 95, 135.2);
             cfg = 64;
             big = 0;
             splits = 1;
+        }
+        if (direct) {
+            int c = cfg, b = big;
+            wider(best, c, b);
+            if (c != cfg || b != big) {
+                cfg = c;
+                big = b;
+                splits = 1;
+            }
         }
     } else if (tiles(64, 64) >= 256 || nk32 < 8) {
         cfg = tiles(64, 64) >= 256 ? 64 : 32;
@@ -617,6 +645,7 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         if (t64 >= 256 && t64 < 320 && nk32 >= 24 &&
             (d.K >= 2048 || (t64 % 256 != 0 && d.K >= 768)))
             splits = 3;
+        if (direct && splits == 1 && cfg == 64) wider(est(t64, 4096, d.K, 95, 135.2), cfg, big);
     } else {
         cfg = 64;
         const int64_t t64 = tiles(64, 64);
@@ -648,7 +677,7 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     // 256x256 work-groups fill a CU alone, their prologue and C store not overlapped (about
     // 32 k-steps per tile, 16 for 128x256), which decides short K: 12000 x 6565 x 500 runs
     // 729 us at 128x128, 747 at 256x256.
-    if (cfg == 128 && splits == 1) {
+    if (cfg == 128 && splits == 1 && tiles(128, 128) >= 512) {
         const double k = d.K;
         auto cost = [&](int bm, int bn, double rate, double over) {
             return (double)((tiles(bm, bn) + 255) / 256) * bm * bn * (k + over) / rate;
