@@ -723,12 +723,27 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         }
     }
     if (force_split >= 1) splits = force_split;
+    // gemm_direct_kernel runs the tile unless split 64- or 128-wide ranges keep the register-
+    // staged kernel (direct loads measured 5-8 % slower there: 6400 x 4096 x 512 NT in 6
+    // ranges 268.3 against 246.1 us, 1536 x 4096 x 1536 in 8: 190.4 / 180.9, 1000 x 4096 x
+    // 3000 in 6: 253.1 / 233.9; split 256x256 tiles gain: 1024 x 6400 x 4096 TN in 4 ranges
+    // 386.1 / 396.6). Unsplit 64x64 tiles: 4-13 % faster than the staged kernel (1024^3
+    // 25.4 -> 22.4 us, 2048 x 1024 x 2048 TN 77.8 -> 68.9). An unaligned operand is loaded 4
+    // bytes per lane (Linear(500 -> 6565) forward 12000 x 500 x 6565 735.3 -> 648.8 us,
+    // 4096 x 4096 x 4095 TN 1015.6 -> 924.1). MIGEMM_DIRECT=2 forces direct loads for every
+    // 64x64 / 128x128 / 128x256 / 256x256 tile, MIGEMM_DVAR=9 keeps 64x64 tiles staged.
+    const bool use_direct =
+        fits && cfg != 32 &&
+        ((cfg == 128 && big == 2) || splits == 1 || direct_mode() == 2) &&
+        !(cfg == 64 && env_int("MIGEMM_DVAR") == 9);
     if (env_int("MIGEMM_TRACE") != 0)  // tuning aid: the dispatcher's choice, on stderr
-        fprintf(stderr, "migemm tiled %dx%dx%d batch %d t%d%d: tile %s splits %d loads %s\n", d.M,
-                d.K, d.N, d.batch, (int)d.transA, (int)d.transB,
+        fprintf(stderr, "migemm tiled %dx%dx%d batch %d t%d%d: tile %s splits %d kernel %s\n",
+                d.M, d.K, d.N, d.batch, (int)d.transA, (int)d.transB,
                 cfg == 128 ? (big == 2 ? "256x256" : big == 1 ? "128x256" : "128x128")
                            : (cfg == 64 ? "64x64" : "32x32"),
-                splits, fits ? (wa == 4 && wb == 4 ? "direct16" : "direct4") : "staged");
+                splits,
+                use_direct ? (wa == 4 && wb == 4 ? "direct (16-byte loads)" : "direct (4-byte loads)")
+                           : "register-staged");
 
     a.splits = splits;
     a.partial = nullptr;
@@ -766,14 +781,7 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
                 // I-contiguous) runs 8 wavefronts of 64x128 (2 per SIMD, ~220 VGPRs): 143.2
                 // against 142.5 at 4096^3, 145.9 against 144.3 at 8192^3; NN and NT are
                 // slower that way (142.7 / 143.0).
-                // Split 128-wide tiles (long K over few tiles) keep the register-staged
-                // kernel: direct loads measured 5-8 % slower there (6400 x 4096 x 512 NT in 6
-                // ranges 268.3 against 246.1 us, 1536 x 4096 x 1536 in 8: 190.4 / 180.9,
-                // 1000 x 4096 x 3000 in 6: 253.1 / 233.9), while split 256x256 tiles gain
-                // (1024 x 6400 x 4096 TN in 4 ranges: 383.2 / 395.8).
-                // An unaligned operand is loaded 4 bytes per lane: Linear(500 -> 6565) forward
-                // 12000 x 500 x 6565 735.3 -> 648.8 us, 4096 x 4096 x 4095 TN 1015.6 -> 924.1.
-                if (fits && (big == 2 || splits == 1 || direct_mode() == 2))
+                if (use_direct)
                     rc = launch_gemm_direct(stream, a, big == 2 ? 256 : 128, big >= 1 ? 256 : 128,
                                             akc, bkc, wa, wb);
                 else if (big == 2 && akc && bkc)
@@ -788,10 +796,7 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
                     rc = launch_tiles<128, 128, 16, 4, 1>(stream, a, akc, bkc, av, bv);
                 break;
             case 64:
-                // Unsplit 64x64 tiles load straight into LDS (4-13 % faster than the staged
-                // kernel: 1024^3 25.4 -> 22.4 us, 2048 x 1024 x 2048 TN 77.8 -> 68.9);
-                // MIGEMM_DVAR=9 keeps them register-staged for comparisons.
-                if (fits && (splits == 1 || direct_mode() == 2) && env_int("MIGEMM_DVAR") != 9)
+                if (use_direct)
                     rc = launch_gemm_direct(stream, a, 64, 64, akc, bkc, wa, wb);
                 else
                     rc = launch_tiles<64, 64, 32, 2, 2>(stream, a, akc, bkc, av, bv);
