@@ -5,11 +5,23 @@ namespace migemm {
 
 int launch_direct_128(hipStream_t stream, TiledArgs &a, bool akc, bool bkc, int wa, int wb,
     int var) {
+    // Split-K ranges take the variant without the 128-VGPR cap (three work-groups per CU):
+    // the ranges are sized for ~1024 work-groups, which at four per CU leave a nearly empty
+    // second round. Measured (us, capped / uncapped / register-staged): 6400 x 4096 x 512 NT
+    // in 6 ranges 263.1 / 230.6 / 244.4; 500 x 12000 x 6564 TN in 6 ranges 700.7 / 603.6 /
+    // 651.2.
+    const bool split = a.splits > 1;
     if (wa != 4 || wb != 4) {
+        if (split) {
+            if (wa == 1 && wb == 1) return launch_layouts<128, 128, 16, 2, 2, 1, 1, 1>(stream, a, akc, bkc);
+            if (wa == 1) return launch_layouts<128, 128, 16, 2, 2, 1, 1, 4>(stream, a, akc, bkc);
+            return launch_layouts<128, 128, 16, 2, 2, 1, 4, 1>(stream, a, akc, bkc);
+        }
         if (wa == 1 && wb == 1) return launch_layouts<128, 128, 16, 2, 2, 4, 1, 1>(stream, a, akc, bkc);
         if (wa == 1) return launch_layouts<128, 128, 16, 2, 2, 4, 1, 4>(stream, a, akc, bkc);
         return launch_layouts<128, 128, 16, 2, 2, 4, 4, 1>(stream, a, akc, bkc);
     }
+    if (split && var == 0) var = 2;
     // BK = 16, two stages (32 KB) and at most 128 VGPRs: four work-groups (16 wavefronts) per
     // CU. Measured (us; direct with this occupancy / with up to 168 VGPRs, three work-groups
     // (MIGEMM_DVAR=2) / three stages (MIGEMM_DVAR=1) / BK = 32 (MIGEMM_DVAR=3) / register-

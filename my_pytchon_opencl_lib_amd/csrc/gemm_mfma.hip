@@ -685,10 +685,16 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         if (av && bv) {
             double c64, c0, c1, c2;
             if (direct) {
+                // At K <= 512 the per-tile prologue and C store of the larger tiles weigh
+                // 1.5x their fitted overhead: on a grid of 200 shapes (M, N in 1000..8000, K
+                // in 256..4096, NN and TN, every tile timed) the picks' total time above the
+                // per-shape best falls from 0.32 % to 0.18 %, and 3000 x 256 x 8000 takes
+                // 64x64 tiles (115.1 us) instead of 128x256 (136.7 us).
+                const double s = d.K <= 512 ? 1.5 : 1.0;
                 c64 = cost(64, 64, 135.2, 95);
-                c0 = cost(128, 128, 147.6, 90);
-                c1 = cost(128, 256, 152.1, 98);
-                c2 = cost(256, 256, 152.6, 75);
+                c0 = cost(128, 128, 147.6, 90 * s);
+                c1 = cost(128, 256, 152.1, 98 * s);
+                c2 = cost(256, 256, 152.6, 75 * s);
             } else {
                 c64 = cost(64, 64, 134.2, 75);
                 c0 = cost(128, 128, 138.9, 78);
@@ -723,18 +729,18 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         }
     }
     if (force_split >= 1) splits = force_split;
-    // gemm_direct_kernel runs the tile unless split 64- or 128-wide ranges keep the register-
-    // staged kernel (direct loads measured 5-8 % slower there: 6400 x 4096 x 512 NT in 6
-    // ranges 268.3 against 246.1 us, 1536 x 4096 x 1536 in 8: 190.4 / 180.9, 1000 x 4096 x
-    // 3000 in 6: 253.1 / 233.9; split 256x256 tiles gain: 1024 x 6400 x 4096 TN in 4 ranges
-    // 386.1 / 396.6). Unsplit 64x64 tiles: 4-13 % faster than the staged kernel (1024^3
-    // 25.4 -> 22.4 us, 2048 x 1024 x 2048 TN 77.8 -> 68.9). An unaligned operand is loaded 4
-    // bytes per lane (Linear(500 -> 6565) forward 12000 x 500 x 6565 735.3 -> 648.8 us,
-    // 4096 x 4096 x 4095 TN 1015.6 -> 924.1). MIGEMM_DIRECT=2 forces direct loads for every
-    // 64x64 / 128x128 / 128x256 / 256x256 tile, MIGEMM_DVAR=9 keeps 64x64 tiles staged.
+    // gemm_direct_kernel runs the tile unless split 64x64 or 128x256 ranges keep the register-
+    // staged kernel. Split 256x256 tiles gain (1024 x 6400 x 4096 TN in 4 ranges 386.1 /
+    // 396.6 us), and so do split 128x128 tiles in their uncapped variant (gemm_direct_128.hip;
+    // 6400 x 4096 x 512 NT in 6 ranges 230.6 / 244.4). Unsplit 64x64 tiles: 4-13 % faster than
+    // the staged kernel (1024^3 25.4 -> 22.4 us, 2048 x 1024 x 2048 TN 77.8 -> 68.9). An
+    // unaligned operand is loaded 4 bytes per lane (Linear(500 -> 6565) forward 12000 x 500 x
+    // 6565 735.3 -> 648.8 us, 4096 x 4096 x 4095 TN 1015.6 -> 924.1). MIGEMM_DIRECT=2 forces
+    // direct loads for every 64x64 / 128x128 / 128x256 / 256x256 tile, MIGEMM_DVAR=9 keeps
+    // 64x64 tiles staged.
     const bool use_direct =
         fits && cfg != 32 &&
-        ((cfg == 128 && big == 2) || splits == 1 || direct_mode() == 2) &&
+        ((cfg == 128 && big != 1) || splits == 1 || direct_mode() == 2) &&
         !(cfg == 64 && env_int("MIGEMM_DVAR") == 9);
     if (env_int("MIGEMM_TRACE") != 0)  // tuning aid: the dispatcher's choice, on stderr
         fprintf(stderr, "migemm tiled %dx%dx%d batch %d t%d%d: tile %s splits %d kernel %s\n",
