@@ -729,18 +729,17 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         }
     }
     if (force_split >= 1) splits = force_split;
-    // gemm_direct_kernel runs the tile unless split 64x64 or 128x256 ranges keep the register-
-    // staged kernel. Split 256x256 tiles gain (1024 x 6400 x 4096 TN in 4 ranges 386.1 /
-    // 396.6 us), and so do split 128x128 tiles in their uncapped variant (gemm_direct_128.hip;
-    // 6400 x 4096 x 512 NT in 6 ranges 230.6 / 244.4). Unsplit 64x64 tiles: 4-13 % faster than
-    // the staged kernel (1024^3 25.4 -> 22.4 us, 2048 x 1024 x 2048 TN 77.8 -> 68.9). An
-    // unaligned operand is loaded 4 bytes per lane (Linear(500 -> 6565) forward 12000 x 500 x
-    // 6565 735.3 -> 648.8 us, 4096 x 4096 x 4095 TN 1015.6 -> 924.1). MIGEMM_DIRECT=2 forces
-    // direct loads for every 64x64 / 128x128 / 128x256 / 256x256 tile, MIGEMM_DVAR=9 keeps
-    // 64x64 tiles staged.
+    // gemm_direct_kernel runs every 64x64, 128x128, 128x256 and 256x256 tile except split
+    // 128x256 ranges (which the dispatcher does not pick; MIGEMM_DIRECT=2 forces them too).
+    // Measured against the register-staged kernel (us): unsplit 64x64 1024^3 24.7 / 21.5,
+    // 2048 x 1024 x 2048 TN 77.8 / 68.9; split 64x64 ranges 512 x 16384 x 512 TN 78.6 / 72.3,
+    // 256 x 8192 x 1024 43.9 / 40.0, 1024 x 2048 x 1024 NT 46.2 / 42.6; split 128x128 ranges
+    // in the uncapped variant (gemm_direct_128.hip) 6400 x 4096 x 512 NT 244.4 / 230.6;
+    // split 256x256 tiles 1024 x 6400 x 4096 TN 396.6 / 386.1. An unaligned operand is loaded
+    // 4 bytes per lane (Linear(500 -> 6565) forward 12000 x 500 x 6565 735.3 -> 648.8 us,
+    // 4096 x 4096 x 4095 TN 1015.6 -> 924.1). MIGEMM_DVAR=9 keeps 64x64 tiles staged.
     const bool use_direct =
-        fits && cfg != 32 &&
-        ((cfg == 128 && big != 1) || splits == 1 || direct_mode() == 2) &&
+        fits && cfg != 32 && (splits == 1 || big != 1 || direct_mode() == 2) &&
         !(cfg == 64 && env_int("MIGEMM_DVAR") == 9);
     if (env_int("MIGEMM_TRACE") != 0)  // tuning aid: the dispatcher's choice, on stderr
         fprintf(stderr, "migemm tiled %dx%dx%d batch %d t%d%d: tile %s splits %d kernel %s\n",
