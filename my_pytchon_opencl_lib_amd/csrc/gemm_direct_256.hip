@@ -15,7 +15,9 @@ int launch_direct_256(hipStream_t stream, TiledArgs &a, bool akc, bool bkc, int 
     // interleaved in one process, TFLOP/s NN / NT / TN: 148.2 / 150.9 / 147.4 against
     // 148.0 / 150.3 / 147.8; with loads three tiles ahead (three stages) 146.7 / 150.0 /
     // 143.4; four stages 145.9 / 149.9 / 142.9; TN with 8 wavefronts of 64x128
-    // 144.3-145.5. The register-staged kernel: 144.6 / 147.7 / 143.0.
+    // 144.3-145.5. The register-staged kernel: 144.6 / 147.7 / 143.0. Raising the wavefront
+    // priority (s_setprio 1 or 3) around each k-group's MFMAs: 126.3 / 129.5 / 133.5 against
+    // 149.6 / 150.1 / 149.3.
     if (var == 1) return launch_layouts<256, 256, 16, 3, 2>(stream, a, akc, bkc);
     return launch_layouts<256, 256, 32, 2, 2>(stream, a, akc, bkc);
 }
