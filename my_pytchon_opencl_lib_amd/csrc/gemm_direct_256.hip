@@ -17,7 +17,8 @@ int launch_direct_256(hipStream_t stream, TiledArgs &a, bool akc, bool bkc, int 
     // 143.4; four stages 145.9 / 149.9 / 142.9; TN with 8 wavefronts of 64x128
     // 144.3-145.5. The register-staged kernel: 144.6 / 147.7 / 143.0. Raising the wavefront
     // priority (s_setprio 1 or 3) around each k-group's MFMAs: 126.3 / 129.5 / 133.5 against
-    // 149.6 / 150.1 / 149.3.
+    // 149.6 / 150.1 / 149.3. Eight wavefronts of 64x128 with this pipeline (176-184 VGPRs):
+    // 146.7 / 147.4 / 146.6 against 150.4 / 150.5 / 150.3.
     if (var == 1) return launch_layouts<256, 256, 16, 3, 2>(stream, a, akc, bkc);
     return launch_layouts<256, 256, 32, 2, 2>(stream, a, akc, bkc);
 }
