@@ -489,8 +489,8 @@ int launch_reduce_slices(hipStream_t stream, const float *partial, int slices, i
 }
 
 namespace {
-// Tuning overrides (MIGEMM_TILE = 32 | 64 | 128 | 256, MIGEMM_SPLITK = S, MIGEMM_VARIANT,
-// MIGEMM_LDS_PAD).
+// Tuning overrides (MIGEMM_TILE = 32 | 64 | 128 | 128x256 | 256, MIGEMM_SPLITK = S,
+// MIGEMM_DIRECT, MIGEMM_LDS_PAD).
 int env_int(const char *name) {
     const char *v = getenv(name);
     return v != nullptr ? atoi(v) : 0;
@@ -714,7 +714,6 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     // MIGEMM_TILE = 32 | 64 | 128 | 128x256 | 256
     const char *tile_env = getenv("MIGEMM_TILE");
     const int force_split = env_int("MIGEMM_SPLITK");
-    const int variant = env_int("MIGEMM_VARIANT");
     if (tile_env != nullptr) {
         const int ft = atoi(tile_env);
         if (strcmp(tile_env, "128x256") == 0) {
@@ -759,55 +758,41 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         if (a.partial == nullptr) return st;
     }
     int rc;
-    if (variant != 0 && cfg == 128 && av && bv) {
-        // Tile-shape variants for tuning sweeps (MIGEMM_VARIANT); 128-bit loads only.
-        switch (variant) {
-            case 1: rc = launch_tiles<256, 128, 16, 8, 1>(stream, a, akc, bkc, true, true); break;
-            case 2: rc = launch_tiles<128, 256, 16, 4, 2>(stream, a, akc, bkc, true, true); break;
-            case 3: rc = launch_tiles<128, 128, 32, 4, 1>(stream, a, akc, bkc, true, true); break;
-            case 4: rc = launch_tiles<256, 128, 16, 4, 2>(stream, a, akc, bkc, true, true); break;
-            case 5: rc = launch_tiles<128, 128, 16, 2, 2>(stream, a, akc, bkc, true, true); break;
-            case 6: rc = launch_tiles<128, 128, 16, 1, 4>(stream, a, akc, bkc, true, true); break;
-            case 7: rc = launch_tiles<256, 256, 16, 8, 2>(stream, a, akc, bkc, true, true); break;
-            default: rc = launch_tiles<128, 128, 16, 4, 1>(stream, a, akc, bkc, av, bv); break;
-        }
-    } else {
-        switch (cfg) {
-            case 128:
-                // Wavefronts of 32x128 (124-128 VGPRs, 4 per SIMD). Measured at 4096^3
-                // (graph replay, 5 rounds), NN / NT / TN TFLOP/s: 256x256 with 16 wavefronts
-                // 141.4 / 145.4 / 144.6; 128x256 with 8: 141.2 / 140.5 / 141.5; 128x128 with
-                // 4: 140.2 / 136.1 / 140.3; 128x128 with 2x2 wavefronts of 64x64: 140.1 /
-                // 125.9 / 140.2.
-                // NT (both operands K-contiguous) runs BK = 32: half the barriers, 144 KB of
-                // LDS; measured NT 146.3 against 144.1 TFLOP/s at 4096^3, 148.6 against 145.5
-                // at 8192^3. With an I-contiguous operand BK = 32 spills and is slower (NN
-                // 133.0 against 143.5), so NN / TN keep BK = 16. TN (both operands
-                // I-contiguous) runs 8 wavefronts of 64x128 (2 per SIMD, ~220 VGPRs): 143.2
-                // against 142.5 at 4096^3, 145.9 against 144.3 at 8192^3; NN and NT are
-                // slower that way (142.7 / 143.0).
-                if (use_direct)
-                    rc = launch_gemm_direct(stream, a, big == 2 ? 256 : 128, big >= 1 ? 256 : 128,
-                                            akc, bkc, wa, wb);
-                else if (big == 2 && akc && bkc)
-                    rc = launch_tiles<256, 256, 32, 8, 2, 3>(stream, a, akc, bkc, av, bv);
-                else if (big == 2 && !akc && !bkc)
-                    rc = launch_tiles<256, 256, 16, 4, 2, 0>(stream, a, akc, bkc, av, bv);
-                else if (big == 2)
-                    rc = launch_tiles<256, 256, 16, 8, 2>(stream, a, akc, bkc, av, bv);
-                else if (big == 1)
-                    rc = launch_tiles<128, 256, 16, 4, 2>(stream, a, akc, bkc, av, bv);
-                else
-                    rc = launch_tiles<128, 128, 16, 4, 1>(stream, a, akc, bkc, av, bv);
-                break;
-            case 64:
-                if (use_direct)
-                    rc = launch_gemm_direct(stream, a, 64, 64, akc, bkc, wa, wb);
-                else
-                    rc = launch_tiles<64, 64, 32, 2, 2>(stream, a, akc, bkc, av, bv);
-                break;
-            default: rc = launch_tiles<32, 32, 32, 1, 1>(stream, a, akc, bkc, av, bv); break;
-        }
+    switch (cfg) {
+        case 128:
+            // Wavefronts of 32x128 (124-128 VGPRs, 4 per SIMD). Measured at 4096^3
+            // (graph replay, 5 rounds), NN / NT / TN TFLOP/s: 256x256 with 16 wavefronts
+            // 141.4 / 145.4 / 144.6; 128x256 with 8: 141.2 / 140.5 / 141.5; 128x128 with
+            // 4: 140.2 / 136.1 / 140.3; 128x128 with 2x2 wavefronts of 64x64: 140.1 /
+            // 125.9 / 140.2.
+            // NT (both operands K-contiguous) runs BK = 32: half the barriers, 144 KB of
+            // LDS; measured NT 146.3 against 144.1 TFLOP/s at 4096^3, 148.6 against 145.5
+            // at 8192^3. With an I-contiguous operand BK = 32 spills and is slower (NN
+            // 133.0 against 143.5), so NN / TN keep BK = 16. TN (both operands
+            // I-contiguous) runs 8 wavefronts of 64x128 (2 per SIMD, ~220 VGPRs): 143.2
+            // against 142.5 at 4096^3, 145.9 against 144.3 at 8192^3; NN and NT are
+            // slower that way (142.7 / 143.0).
+            if (use_direct)
+                rc = launch_gemm_direct(stream, a, big == 2 ? 256 : 128, big >= 1 ? 256 : 128,
+                                        akc, bkc, wa, wb);
+            else if (big == 2 && akc && bkc)
+                rc = launch_tiles<256, 256, 32, 8, 2, 3>(stream, a, akc, bkc, av, bv);
+            else if (big == 2 && !akc && !bkc)
+                rc = launch_tiles<256, 256, 16, 4, 2, 0>(stream, a, akc, bkc, av, bv);
+            else if (big == 2)
+                rc = launch_tiles<256, 256, 16, 8, 2>(stream, a, akc, bkc, av, bv);
+            else if (big == 1)
+                rc = launch_tiles<128, 256, 16, 4, 2>(stream, a, akc, bkc, av, bv);
+            else
+                rc = launch_tiles<128, 128, 16, 4, 1>(stream, a, akc, bkc, av, bv);
+            break;
+        case 64:
+            if (use_direct)
+                rc = launch_gemm_direct(stream, a, 64, 64, akc, bkc, wa, wb);
+            else
+                rc = launch_tiles<64, 64, 32, 2, 2>(stream, a, akc, bkc, av, bv);
+            break;
+        default: rc = launch_tiles<32, 32, 32, 1, 1>(stream, a, akc, bkc, av, bv); break;
     }
     splits = a.splits;
     if (rc != MIGEMM_OK || splits == 1) return rc;
