@@ -109,7 +109,11 @@ def run(pools, ta, tb, M, K, N, batch, sA, sB, sC, lda, ldb, ldc, bias=False, ac
 
 
 LAYOUTS = [(0, 0), (0, 1), (1, 0), (1, 1)]
-FAMILIES = [("TILED", {}), ("TILED", {"MIGEMM_DIRECT": 0}), ("SMALL", {})]
+# Kernel families, each forced: the direct kernel in 64x64 and 256x256 tiles (MIGEMM_TILE; the
+# dispatcher would take 32x32 tiles at these sizes), the register-staged kernel in 128x128
+# tiles and the small-output kernel.
+FAMILIES = [("TILED", {"MIGEMM_TILE": 64}), ("TILED", {"MIGEMM_TILE": 256}),
+            ("TILED", {"MIGEMM_TILE": 128, "MIGEMM_DIRECT": 0}), ("SMALL", {})]
 
 
 @pytest.mark.parametrize("fam", range(len(FAMILIES)))
@@ -127,14 +131,16 @@ def test_batch_entries_beyond_2_31(pools, policy, fam, ta, tb):
     assert np.array_equal(got, expect)
 
 
+@pytest.mark.parametrize("tile", ["128", "256"])
 @pytest.mark.parametrize("ta,tb", LAYOUTS)
-def test_split_ranges_beyond_2_31(pools, policy, ta, tb):
-    """Split-K partial sums reduced into batch entries 2^31 + 1024 floats apart, C += result."""
-    policy("TILED", MIGEMM_SPLITK=3)
+def test_split_ranges_beyond_2_31(pools, policy, tile, ta, tb):
+    """Split-K partial sums reduced into batch entries 2^31 + 1024 floats apart, C += result
+    (direct loads into LDS, also for 128x128 ranges)."""
+    policy("TILED", MIGEMM_SPLITK=3, MIGEMM_TILE=tile, MIGEMM_DIRECT=2)
     M, K, N = 260, 1036, 300
     lda = M if ta else K
     ldb = K if tb else N
-    say("large offsets split", ta, tb)
+    say("large offsets split", tile, ta, tb)
     got, expect = run(pools, ta, tb, M, K, N, 2, BIG, BIG, BIG, lda, ldb, N, acc=True,
                       seed=11 + ta + 2 * tb)
     assert np.array_equal(got, expect)
@@ -152,17 +158,18 @@ def test_skinny_batch_entries_beyond_2_31(pools, policy, ta):
 
 
 @pytest.mark.parametrize("fam", range(len(FAMILIES)))
-@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1)])
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
 def test_rows_beyond_2_31(pools, policy, fam, ta, tb):
-    """A's rows 2^21 floats apart (the direct loads' limit), 1100 of them: the last tile
-    rows start 2^31 floats in."""
+    """A's rows (or k-rows, transposed) 2^21 floats apart, the direct loads' limit. Not
+    transposed, 1100 rows: the last tiles start 2^31 floats in, and a 256-row tile's lanes
+    reach 255 * 2^21 floats past its base."""
     name, env = FAMILIES[fam]
     policy(name, **env)
     M, K, N = 1100, 64, 260
     ldb = K if tb else N
     say("large offsets rows", name, env, ta, tb)
     got, expect = run(pools, ta, tb, M, K, N, 1, 0, 0, 0, LD_DIRECT, ldb, N, bias=True,
-                      seed=31 + tb + 2 * fam)
+                      seed=31 + ta + 2 * tb + 4 * fam)
     assert np.array_equal(got, expect)
 
 
