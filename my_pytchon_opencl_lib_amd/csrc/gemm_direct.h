@@ -147,10 +147,12 @@ struct DlOperand {
         }
     }
 
-    // The tail tile kt (k0 = BK kt, k0 + BK > K) through registers, k >= K zero-filled,
-    // written where the direct load would have put it.
-    __device__ __forceinline__ void tail(float *stage, int kt, int K, int64_t ld,
-                                         int lane) const {
+    // This lane's floats of the tail tile kt (k0 = BK kt, k0 + BK > K), k >= K zero-filled.
+    typedef typename std::conditional<W == 4, f4, float>::type TailElem;
+    struct Tail {
+        TailElem v[NS];
+    };
+    __device__ __forceinline__ void tail_fetch(Tail &t, int kt, int K, int64_t ld) const {
         const int k0 = kt * BK;
         const char *tb = tile_base(kt, ld);
 #pragma unroll
@@ -165,10 +167,21 @@ struct DlOperand {
                 } else {
                     if (k0 + kk[j] < K) v = dl_load16(src);
                 }
-                *reinterpret_cast<f4 *>(stage + lds_off(j) + 4 * lane) = v;
+                t.v[j] = v;
             } else {
-                stage[lds_off(j) + lane] = k0 + kk[j] < K ? *src : 0.f;
+                t.v[j] = k0 + kk[j] < K ? *src : 0.f;
             }
+        }
+    }
+
+    // Writes a fetched tail tile where the direct loads would have put it.
+    __device__ __forceinline__ void tail_put(const Tail &t, float *stage, int lane) const {
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+            if constexpr (W == 4)
+                *reinterpret_cast<f4 *>(stage + lds_off(j) + 4 * lane) = t.v[j];
+            else
+                stage[lds_off(j) + lane] = t.v[j];
         }
     }
 };
@@ -300,6 +313,21 @@ gemm_direct_kernel(TiledArgs p) {
         mfmas(fa[(G - 1) & 1], fb[(G - 1) & 1]);
     };
 
+    // 64x64 tiles fetch the tail tile into registers before the first direct loads (16
+    // registers per lane, which these tiles have to spare), so its memory latency overlaps
+    // the k loop; a work-group runs the whole k loop with others of the same launch wave,
+    // and latency left at the end is not hidden by other work-groups. Issued first, these
+    // loads are the oldest in the vmcnt order and every wait below also covers them.
+    constexpr bool TAIL_EARLY = BM == 64 && BN == 64;
+    typename OpA::Tail ta;
+    typename OpB::Tail tb;
+    if constexpr (TAIL_EARLY) {
+        if (kf < kt1) {
+            opa.tail_fetch(ta, kf, K, p.lda);
+            opb.tail_fetch(tb, kf, K, p.ldb);
+        }
+    }
+
     int kt = kt0;
     if (kt0 < kf) {
 #pragma unroll
@@ -325,15 +353,24 @@ gemm_direct_kernel(TiledArgs p) {
     }
     wait_vmcnt<0>();  // no load into LDS outlives the loop
     if (kt < kt1) {  // the tail tile: k >= K zero-filled in both operands
+        if constexpr (!TAIL_EARLY) {
+            opa.tail_fetch(ta, kt, K, p.lda);
+            opb.tail_fetch(tb, kt, K, p.ldb);
+        }
         __syncthreads();  // every wavefront is done reading the stages
-        opa.tail(lds_a, kt, K, p.lda, lane);
-        opb.tail(lds_b, kt, K, p.ldb, lane);
+        opa.tail_put(ta, lds_a, lane);
+        opb.tail_put(tb, lds_b, lane);
         __syncthreads();
+        // k-groups wholly at k >= K hold zeros in both operands; their MFMAs would add
+        // exact zeros (an accumulator that starts at +0 is never -0), so they are skipped.
+        const int groups = (K - kt * BK + 7) / 8;
         f4 fa[FM], fb[FN];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            frags(0, g, fa, fb);
-            mfmas(fa, fb);
+            if (g < groups) {
+                frags(0, g, fa, fb);
+                mfmas(fa, fb);
+            }
         }
     }
     store_tile<FM, FN>(p, tc, tc.m0 + wm * WTM, tc.n0 + wn * WTN, lane, acc);

@@ -26,7 +26,9 @@
 //        half-wavefronts of a fragment read, k-rows 4 apart, on different banks).
 //  * Edges: rows / columns beyond M / N are clamped on load (they feed outputs that are not
 //    stored); the k tail (K % BK != 0) is fetched through registers with k >= K zero-filled
-//    (matmul.cl:39-52) into the same layout, after the pipelined loop.
+//    (matmul.cl:39-52) and written into the same layout after the pipelined loop (64x64
+//    tiles fetch it before the loop, so its latency is hidden); k-groups wholly past K
+//    are skipped.
 //  * K order within an MFMA step, split-K ranges, the XCD-aware raster and the epilogue are
 //    those of gemm_mfma_kernel (tiled_common.h); each output's k sum runs in the same order
 //    as in gemm_mfma_kernel, so both give identical bits for one split.
