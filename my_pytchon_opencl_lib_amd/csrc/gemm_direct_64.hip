@@ -13,6 +13,10 @@ int launch_direct_64(hipStream_t stream, TiledArgs &a, bool akc, bool bkc, int w
     // 2 x 2 wavefronts of 32x32, BK = 32, two stages (32 KB). Against BK = 16
     // (MIGEMM_DVAR=5) and three stages (MIGEMM_DVAR=6), us: 1024^3 22.4 / 22.6 / 22.5,
     // 2048 x 512 x 2048 38.8 / 40.1 / 43.6, 3072 x 1024 x 3072 157.1 / 156.0 / 151.9.
+    // Loading further ahead did not pay either (us, shipped / BK = 32 with three stages
+    // loaded three tiles ahead / BK = 16 with four stages four ahead): 1000 x 777 x 3000
+    // 45.9 / 46.2 / 45.6, 2048 x 512 x 2048 38.4 / 40.5 / 38.3, 4096 x 1024 x 4096 263.2 /
+    // 258.8 / 261.4, 12000 x 6565 x 500 NT 638.8 / 637.0 / 687.0.
     if (var == 5) return launch_layouts<64, 64, 16, 2, 2>(stream, a, akc, bkc);
     if (var == 6) return launch_layouts<64, 64, 32, 3, 2>(stream, a, akc, bkc);
     return launch_layouts<64, 64, 32, 2, 2>(stream, a, akc, bkc);
