@@ -37,10 +37,11 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="target duration of the bounded CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--pmc-target", action="store_true",
-                   help="run only the profiling target for rocprofv3 --pmc passes: the three "
-                        "4096^3 forms 3x each, then a 256 MiB device copy 3x (the reference "
-                        "for scaling FETCH_SIZE / WRITE_SIZE to bytes)")
+    p.add_argument("--pmc-target", nargs="?", const="4096", choices=["4096", "5a"],
+                   help="run only a profiling target for rocprofv3 --pmc passes: '4096' (the "
+                        "default) the three 4096^3 forms 3x each, '5a' config 5a (1000x777x3000 "
+                        "NN) 3x; then a 256 MiB device copy 3x (the reference for scaling "
+                        "FETCH_SIZE / WRITE_SIZE to bytes)")
     return p.parse_args()
 
 
@@ -113,7 +114,7 @@ def main():
     from my_pytchon_opencl_lib_amd import NnClGlob, _native
 
     if args.pmc_target:
-        pmc_target(torch, NnClGlob("cuda:0"))
+        pmc_target(torch, NnClGlob("cuda:0"), args.pmc_target)
         return
     nncl = NnClGlob("cuda:0")
     dev = torch.device("cuda:0")
@@ -194,17 +195,25 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def pmc_target(torch, nncl):
-    n = 4096
+def pmc_target(torch, nncl, which="4096"):
     g = torch.Generator(device="cuda:0")
-    g.manual_seed(3)
-    A = torch.randn(n, n, device="cuda:0", generator=g) / 64
-    B = torch.randn(n, n, device="cuda:0", generator=g) / 64
-    C = torch.empty(n, n, device="cuda:0")
-    for _ in range(3):
-        nncl.gemm(A, B, out=C)
-        nncl.gemm(A, B, transB=True, out=C)
-        nncl.gemm(A, B, transA=True, out=C)
+    if which == "5a":
+        g.manual_seed(4)
+        A = torch.rand(1000, 777, device="cuda:0", generator=g) * 2 - 1
+        B = torch.rand(777, 3000, device="cuda:0", generator=g) * 2 - 1
+        C = torch.empty(1000, 3000, device="cuda:0")
+        for _ in range(3):
+            nncl.gemm(A, B, out=C)
+    else:
+        n = 4096
+        g.manual_seed(3)
+        A = torch.randn(n, n, device="cuda:0", generator=g) / 64
+        B = torch.randn(n, n, device="cuda:0", generator=g) / 64
+        C = torch.empty(n, n, device="cuda:0")
+        for _ in range(3):
+            nncl.gemm(A, B, out=C)
+            nncl.gemm(A, B, transB=True, out=C)
+            nncl.gemm(A, B, transA=True, out=C)
     src = torch.ones(64 * 1024 * 1024, device="cuda:0")
     dst = torch.empty_like(src)
     for _ in range(3):
