@@ -40,6 +40,24 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
     assert set(_native.SIGNATURES) == set(names)
 
 
+def _arg_count(params):
+    params = " ".join(params.split())
+    return 0 if params in ("", "void") else params.count(",") + 1
+
+
+def test_pinvoke_block_binds_every_declared_function():
+    """INTEGRATION.md's C# P/Invoke block declares every function of include/migemm.h with
+    the header's argument count, so a maintainer can paste it as the host's binding."""
+    header = open(HEADER).read()
+    decl = {m.group(1): _arg_count(m.group(2)) for m in
+            re.finditer(r"^(?:int|const char \*)\s*(migemm_\w+)\(([^)]*)\);", header, re.M)}
+    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    bound = {m.group(1): _arg_count(m.group(2)) for m in
+             re.finditer(r"static extern \w+\s+(migemm_\w+)\(([^)]*)\);", doc)}
+    assert set(decl) == set(header_functions())
+    assert bound == decl
+
+
 def test_version_and_empty_last_error(lib):
     assert lib.migemm_version().decode() == "0.1.0"
     assert isinstance(lib.migemm_last_error(), bytes)
