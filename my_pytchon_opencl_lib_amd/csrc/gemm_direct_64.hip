@@ -16,7 +16,12 @@ int launch_direct_64(hipStream_t stream, TiledArgs &a, bool akc, bool bkc, int w
     // Loading further ahead did not pay either (us, shipped / BK = 32 with three stages
     // loaded three tiles ahead / BK = 16 with four stages four ahead): 1000 x 777 x 3000
     // 45.9 / 46.2 / 45.6, 2048 x 512 x 2048 38.4 / 40.5 / 38.3, 4096 x 1024 x 4096 263.2 /
-    // 258.8 / 261.4, 12000 x 6565 x 500 NT 638.8 / 637.0 / 687.0.
+    // 258.8 / 261.4, 12000 x 6565 x 500 NT 638.8 / 637.0 / 687.0. Nor did 5 or 8 stages
+    // loaded as many tiles ahead on few-tile long-K shapes (us, shipped / BK = 32 with 8
+    // stages / BK = 32 with 5 / BK = 16 with 8): 512 x 16384 x 512 TN 71.8 / 79.9 / 73.5 /
+    // 72.7, 384 x 6000 x 384 27.8 / 33.1 / 29.5 / 28.4, 128 x 4096 x 4096 43.2 / 52.0 /
+    // 45.9 / 45.1; the config-3 gate GEMM in 4 ranges 16.0 / 16.8 / 16.1 / 16.2 (the
+    // small-output kernel: 14.7).
     if (var == 5) return launch_layouts<64, 64, 16, 2, 2>(stream, a, akc, bkc);
     if (var == 6) return launch_layouts<64, 64, 32, 3, 2>(stream, a, akc, bkc);
     return launch_layouts<64, 64, 32, 2, 2>(stream, a, akc, bkc);
