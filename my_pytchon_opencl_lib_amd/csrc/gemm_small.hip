@@ -7,7 +7,7 @@
 // In the tiled kernel one wavefront walks the whole K range of its 32x32 sub-tile, so with
 // few tiles the MFMA chain of a single wavefront is the run time. Here the K range is
 // divided among the wavefronts instead:
-//  * A work-group owns a (16*MB) x 16 tile of C and has NW wavefronts; wavefront w
+//  * A work-group owns a (16*MB) x (16*NB) tile of C and has NW wavefronts; wavefront w
 //    multiplies the w-th contiguous share of the work-group's 16-wide k-groups, and the NW
 //    partial tiles are added in LDS in the order w = 0..NW-1 (deterministic).
 //  * No LDS staging of operands: wavefronts of one work-group share no operand data (each
@@ -51,6 +51,7 @@ struct SmallArgs {
     int groups_per_split;  // 16-wide k-groups per range
     float *partial;        // [splits][batch][M][N] when splits > 1
     int accumulate;        // C += result instead of C = result
+    int m_fast;            // consecutive tiles step along M (else along N)
 };
 
 constexpr int KG = 16;       // k values per k-group (4 MFMA steps of 4)
@@ -63,17 +64,18 @@ __device__ __forceinline__ f4 load16(const float *p) {
 }
 
 // One k-group (16 values of k, four MFMA steps j of 4) of a wavefront's operands: a[blk]
-// for 16-row block blk of A, b for B. M/N-contiguous operand: the fragment values of steps
-// j = 0..3. K-contiguous operand: the 128-bit load, before the lane permutation.
-template <int MB>
+// for 16-row block blk of A, b[nb] for 16-column block nb of B. M/N-contiguous operand: the
+// fragment values of steps j = 0..3. K-contiguous operand: the 128-bit load, before the
+// lane permutation.
+template <int MB, int NB>
 struct Frag {
     f4 a[MB];
-    f4 b;
+    f4 b[NB];
 };
 
-template <int MB, int NW, bool AKC, bool BKC>
+template <int MB, int NB, int NW, bool AKC, bool BKC>
 __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(SmallArgs p) {
-    __shared__ float red[NW][MB * 4][64];
+    __shared__ float red[NW][MB * NB * 4][64];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -91,10 +93,16 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(SmallArgs p) {
     pid -= split * per_split;
     const int b = pid / per_batch;
     const int t = pid - b * per_batch;
-    const int tm = t / p.tiles_n;
-    const int tn = t - tm * p.tiles_n;
+    int tm, tn;
+    if (p.m_fast) {
+        tn = t / p.tiles_m;
+        tm = t - tn * p.tiles_m;
+    } else {
+        tm = t / p.tiles_n;
+        tn = t - tm * p.tiles_n;
+    }
     const int m0 = tm * 16 * MB;
-    const int n0 = tn * 16;
+    const int n0 = tn * 16 * NB;
 
     const float *Ab = p.A + (int64_t)b * p.sA;
     const float *Bb = p.B + (int64_t)b * p.sB;
@@ -120,13 +128,19 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(SmallArgs p) {
         else
             pa[blk] = Ab + (int64_t)(4 * lq) * p.lda + min(m0 + blk * 16 + li, p.M - 1);
     }
-    const float *pb = BKC ? Bb + (int64_t)min(n0 + crow, p.N - 1) * p.ldb + ck
-                          : Bb + (int64_t)(4 * lq) * p.ldb + min(n0 + li, p.N - 1);
+    const float *pb[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        if constexpr (BKC)
+            pb[nb] = Bb + (int64_t)min(n0 + nb * 16 + crow, p.N - 1) * p.ldb + ck;
+        else
+            pb[nb] = Bb + (int64_t)(4 * lq) * p.ldb + min(n0 + nb * 16 + li, p.N - 1);
+    }
     // distance between consecutive k-groups
     const int64_t a_gstep = AKC ? KG : (int64_t)KG * p.lda;
     const int64_t b_gstep = BKC ? KG : (int64_t)KG * p.ldb;
 
-    auto load = [&](Frag<MB> &f, int g) {
+    auto load = [&](Frag<MB, NB> &f, int g) {
 #pragma unroll
         for (int blk = 0; blk < MB; ++blk) {
             const float *q = pa[blk] + g * a_gstep;
@@ -135,11 +149,14 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(SmallArgs p) {
             else
                 f.a[blk] = f4{q[0], q[p.lda], q[2 * p.lda], q[3 * p.lda]};
         }
-        const float *q = pb + g * b_gstep;
-        if constexpr (BKC)
-            f.b = load16(q);
-        else
-            f.b = f4{q[0], q[p.ldb], q[2 * p.ldb], q[3 * p.ldb]};
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const float *q = pb[nb] + g * b_gstep;
+            if constexpr (BKC)
+                f.b[nb] = load16(q);
+            else
+                f.b[nb] = f4{q[0], q[p.ldb], q[2 * p.ldb], q[3 * p.ldb]};
+        }
     };
 
     auto permute = [&](f4 v) {
@@ -150,23 +167,29 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(SmallArgs p) {
         return r;
     };
 
-    f4 acc[MB];
+    f4 acc[MB][NB];
 #pragma unroll
-    for (int blk = 0; blk < MB; ++blk) acc[blk] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int blk = 0; blk < MB; ++blk)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[blk][nb] = f4{0.f, 0.f, 0.f, 0.f};
 
     // `direct`: the operands were loaded in fragment order (the partial k-group).
-    auto mma = [&](const Frag<MB> &f, bool direct) {
-        f4 fa[MB];
+    auto mma = [&](const Frag<MB, NB> &f, bool direct) {
+        f4 fa[MB], fb[NB];
 #pragma unroll
         for (int blk = 0; blk < MB; ++blk)
             fa[blk] = AKC && !direct ? permute(f.a[blk]) : f.a[blk];
-        const f4 fb = BKC && !direct ? permute(f.b) : f.b;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+            fb[nb] = BKC && !direct ? permute(f.b[nb]) : f.b[nb];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int blk = 0; blk < MB; ++blk)
-                acc[blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[blk][j], fb[j], acc[blk],
-                                                                0, 0, 0);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    acc[blk][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                        fa[blk][j], fb[nb][j], acc[blk][nb], 0, 0, 0);
     };
 
     // ---- k-groups of this wavefront ----
@@ -195,7 +218,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(SmallArgs p) {
         // barriers keep each set's loads together and in order: left free, the scheduler
         // sinks all refills to the end of the iteration and interleaves the sets, so the
         // first MFMA of an iteration has to wait for almost every load in flight.
-        Frag<MB> f[INFLIGHT];
+        Frag<MB, NB> f[INFLIGHT];
 #pragma unroll
         for (int i = 0; i < INFLIGHT; ++i) {
             load(f[i], kgroup(min(i, nfg - 1)));
@@ -218,8 +241,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(SmallArgs p) {
     if (ghi > gfull && glo <= gfull) {
         // the partial k-group: element-wise loads in fragment order, k >= K zero in both
         // operands
-        Frag<MB> f;
-        const int nc = min(n0 + li, p.N - 1);
+        Frag<MB, NB> f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int k = gfull * KG + 4 * lq + j;
@@ -230,8 +252,12 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(SmallArgs p) {
                 const int64_t off = AKC ? (int64_t)i * p.lda + k : (int64_t)k * p.lda + i;
                 f.a[blk][j] = ok ? Ab[off] : 0.f;
             }
-            const int64_t off = BKC ? (int64_t)nc * p.ldb + k : (int64_t)k * p.ldb + nc;
-            f.b[j] = ok ? Bb[off] : 0.f;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const int nc = min(n0 + nb * 16 + li, p.N - 1);
+                const int64_t off = BKC ? (int64_t)nc * p.ldb + k : (int64_t)k * p.ldb + nc;
+                f.b[nb][j] = ok ? Bb[off] : 0.f;
+            }
         }
         mma(f, true);
     }
@@ -242,14 +268,16 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(SmallArgs p) {
 #pragma unroll
     for (int blk = 0; blk < MB; ++blk)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[w][blk * 4 + r][lane] = acc[blk][r];
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[w][(blk * NB + nb) * 4 + r][lane] = acc[blk][nb][r];
     __syncthreads();
 
-    for (int e = tid; e < MB * 256; e += NW * 64) {
-        const int row = e >> 4;  // 0 .. 16*MB-1
-        const int col = e & 15;
-        const int slot = (row >> 4) * 4 + (row & 3);
-        const int src = ((row & 15) >> 2) * 16 + col;
+    for (int e = tid; e < MB * NB * 256; e += NW * 64) {
+        const int row = e / (16 * NB);  // 0 .. 16*MB-1
+        const int col = e % (16 * NB);  // 0 .. 16*NB-1
+        const int slot = ((row >> 4) * NB + (col >> 4)) * 4 + (row & 3);
+        const int src = ((row & 15) >> 2) * 16 + (col & 15);
         float v = red[0][slot][src];
 #pragma unroll
         for (int q = 1; q < NW; ++q) v += red[q][slot][src];
@@ -267,23 +295,24 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(SmallArgs p) {
     }
 }
 
-template <int MB, int NW>
+template <int MB, int NB, int NW>
 int launch_layout(hipStream_t st, const SmallArgs &a, bool akc, bool bkc) {
     const dim3 grid(a.total), block(NW * 64);
     if (akc && bkc)
-        hipLaunchKernelGGL((gemm_small_kernel<MB, NW, true, true>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((gemm_small_kernel<MB, NB, NW, true, true>), grid, block, 0, st, a);
     else if (akc)
-        hipLaunchKernelGGL((gemm_small_kernel<MB, NW, true, false>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((gemm_small_kernel<MB, NB, NW, true, false>), grid, block, 0, st, a);
     else if (bkc)
-        hipLaunchKernelGGL((gemm_small_kernel<MB, NW, false, true>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((gemm_small_kernel<MB, NB, NW, false, true>), grid, block, 0, st, a);
     else
-        hipLaunchKernelGGL((gemm_small_kernel<MB, NW, false, false>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((gemm_small_kernel<MB, NB, NW, false, false>), grid, block, 0, st, a);
     return hip_check(hipGetLastError(), "gemm_small_kernel launch");
 }
 
-template <int MB>
+template <int MB, int NB = 1>
 int launch_nw(hipStream_t st, const SmallArgs &a, int nw, bool akc, bool bkc) {
-    return nw == 8 ? launch_layout<MB, 8>(st, a, akc, bkc) : launch_layout<MB, 4>(st, a, akc, bkc);
+    return nw == 8 ? launch_layout<MB, NB, 8>(st, a, akc, bkc)
+                   : launch_layout<MB, NB, 4>(st, a, akc, bkc);
 }
 
 int env_value(const char *name) {
@@ -294,7 +323,7 @@ int env_value(const char *name) {
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 struct SmallPlan {
-    int mb, nw, splits;
+    int mb, nb, nw, splits;
     int64_t wgs;  // work-groups without the k split
 };
 
@@ -305,7 +334,7 @@ SmallPlan plan_small(const GemmDesc &d) {
     const int G = (int)cdiv(d.K, KG);
     const int nw = G >= 16 ? 8 : 4;
     const int mb_max = (int)(d.M > 48 ? 4 : cdiv(d.M, 16));
-    SmallPlan pl{1, nw, 1, 0};
+    SmallPlan pl{1, 1, nw, 1, 0};
     for (int mb = mb_max; mb >= 1; --mb) {
         const int64_t wgs = cdiv(d.M, 16 * mb) * cdiv(d.N, 16) * d.batch;
         const int64_t need = cdiv(256, wgs);
@@ -313,9 +342,22 @@ SmallPlan plan_small(const GemmDesc &d) {
         if (cap > 16) cap = 16;
         if (cap < 1) cap = 1;
         const int s = (int)(need < cap ? need : cap);
-        pl = SmallPlan{mb, nw, s, wgs};
+        pl = SmallPlan{mb, 1, nw, s, wgs};
         if (wgs * s >= 256) break;
     }
+    // 32x32 tiles (2 row blocks x 2 column blocks) instead of 64x16 when they make as many
+    // work-groups and A is K-contiguous: a work-group then reads 4 fragments per k-group
+    // instead of 5, and each XCD half of the activation panel that every work-group of the
+    // gate GEMM re-reads. Measured (graph replay, us, 32x32 / 64x16): 64 x 1536 x 4096 +
+    // bias 12.35 / 14.17; 64 x 1024 x 4096 9.55 / 11.18; 128 x 2048 x 2048 14.82 / 19.07;
+    // batch-32 128 x 128 x 64 4.24 / 4.71, 128 x 64 x 128 NT 4.60 / 4.76; 256^3 3.52 / 3.51.
+    // With A transposed they ran slower (64 x 1536 x 4096 TN 18.84 / 16.84).
+    // MIGEMM_SMALL_NB (tuning and tests, read per call): 1 never, 2 always (M, N > 16).
+    const int force_nb = env_value("MIGEMM_SMALL_NB");
+    const int64_t wgs22 = cdiv(d.M, 32) * cdiv(d.N, 32) * d.batch;
+    if (force_nb == 2 ? d.M > 16 && d.N > 16
+                      : force_nb != 1 && pl.mb == 4 && d.N > 16 && !d.transA && wgs22 == pl.wgs)
+        pl = SmallPlan{2, 2, nw, pl.splits, wgs22};
     return pl;
 }
 
@@ -368,7 +410,11 @@ int launch_gemm_small(hipStream_t stream, const GemmDesc &d) {
     a.K = d.K;
     a.accumulate = d.accumulate;
     a.tiles_m = (int)cdiv(d.M, 16 * pl.mb);
-    a.tiles_n = (int)cdiv(d.N, 16);
+    a.tiles_n = (int)cdiv(d.N, 16 * pl.nb);
+    // With 32x32 tiles, consecutive tiles (which share an XCD's L2) step along the shorter
+    // side, so each XCD reads a contiguous share of the larger operand (stepping along N:
+    // 64 x 1536 x 4096 13.73 us against 12.35).
+    a.m_fast = pl.nb == 2 && d.N >= d.M;
     a.batch = d.batch;
     const int G = (int)cdiv(d.K, KG);
     a.groups_per_split = (int)cdiv(G, pl.splits);
@@ -390,7 +436,10 @@ int launch_gemm_small(hipStream_t stream, const GemmDesc &d) {
     switch (pl.mb) {
         case 4: rc = launch_nw<4>(stream, a, pl.nw, akc, bkc); break;
         case 3: rc = launch_nw<3>(stream, a, pl.nw, akc, bkc); break;
-        case 2: rc = launch_nw<2>(stream, a, pl.nw, akc, bkc); break;
+        case 2:
+            rc = pl.nb == 2 ? launch_nw<2, 2>(stream, a, pl.nw, akc, bkc)
+                            : launch_nw<2>(stream, a, pl.nw, akc, bkc);
+            break;
         default: rc = launch_nw<1>(stream, a, pl.nw, akc, bkc); break;
     }
     if (rc != MIGEMM_OK || a.splits == 1) return rc;

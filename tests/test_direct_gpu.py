@@ -209,3 +209,27 @@ def test_direct_unaligned_equals_staged_kernel(tiled256, ta, tb):
             gemm_ex(ta, tb, M, N, K, A, A.shape[1], 0, B, B.shape[1], 0, None, c, N, 0, 1)
             outs.append(host(c))
         assert np.array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_small_kernel_32x32_tiles_exact(ta, tb):
+    """The small-output kernel with 32x32 work-group tiles (2 x 2 blocks of 16x16; forced
+    with MIGEMM_SMALL_NB=2 in every layout): ragged M and N, K tails, k ranges split over
+    work-groups, batch strides, bias and the accumulating epilogue, exact."""
+    from my_pytchon_opencl_lib_amd import _native
+    env = _Env()
+    prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_SMALL)
+    try:
+        env.set(MIGEMM_SMALL_NB=2, MIGEMM_SMALL_SPLITK=None)
+        for M, K, N, batch, bias, acc, splits in [
+                (64, 1536, 4096, 1, True, False, None), (100, 777, 300, 2, True, True, None),
+                (65, 4100, 33, 1, False, True, 5), (130, 40, 70, 3, True, False, None),
+                (64, 300, 50, 2, False, False, 3)]:
+            env.set(MIGEMM_SMALL_SPLITK=splits)
+            say("small 32x32", M, K, N, batch, bias, acc, splits, ta, tb)
+            got, expect = run_exact(M, K, N, ta, tb, batch=batch, bias=bias, acc=acc,
+                                    seed=M + K + N + ta + 2 * tb)
+            assert np.array_equal(got, expect)
+    finally:
+        env.restore()
+        _native.set_gemm_policy(prev)
