@@ -364,29 +364,35 @@ SmallPlan plan_small(const GemmDesc &d) {
 }  // namespace
 
 // Where the small kernel beats the tiled one (graph replay over a grid of M, N in 1..6000
-// and K in 16..8192, NN and TN; us, small / tiled):
+// and K in 16..8192, NN and TN, then a sweep of M in {64, 128, 200}, N in {512, 1536, 4096},
+// K in {1024 .. 8192}; shapes are M x K x N, us, small / tiled):
 //  * M or N <= 4 (unless B is large enough for the skinny kernel): the tiled kernel's
-//    64-wide tiles would be almost empty (6000 x 1 x 8192 48 / 63; 3 x 300 x 300 4.5 / 10.0).
+//    64-wide tiles would be almost empty (6000 x 8192 x 1 48 / 63; 3 x 300 x 300 4.5 / 10.0).
 //  * fewer 64x64 tiles than CUs, and then
-//    - a thin output (M or N <= 32) or K <= 64 (17 x 1024 x 8192 14.4 / 18.5);
-//    - K <= 1024 with < 128 tiles (777 x 300 x 300 9.7 / 11.7; 2048 x 300 x 300 takes the
-//      tiled kernel, 16.3 / 12.2);
-//    - K <= 2048 with < 12 tiles, or < 80 tiles that give the small kernel >= 128 work-
-//      groups without a k split (64 x 4096 x 1536 15.6 / 19.0; 200 x 300 x 2048, 76 work-
-//      groups, 15.3 / 12.8; 6000 x 64 x 2048 33.0 / 28.6);
-//    - longer K with at most 4 tiles (128 x 8192 x 128 11.7 / 13.4; 256 x 4096 x 256 takes
-//      the tiled split, 14.2 / 13.6).
+//    - a thin output (M or N <= 32) or K <= 64 (17 x 8192 x 1024 14.4 / 18.5);
+//    - K <= 1024: fewer than 24 tiles, or a plan without a k split (no reduce launch) and
+//      fewer than 128 tiles or K >= 768 (777 x 300 x 300 9.1 / 10.6; 128 x 1024 x 4096
+//      16.1 / 20.7; 512 x 1024 x 1024 16.1 / 20.8; 2048 x 300 x 300 15.8 / 11.1; with a k
+//      split the tiled kernel wins: 64 x 1024 x 1536 12.7 / 11.6, 200 x 1024 x 512 13.1 /
+//      11.8);
+//    - K <= 2048: fewer than 12 tiles, or a plan without a k split and fewer than 80 tiles
+//      or an output at most 128 wide (64 x 1536 x 4096 14.1 / 19.0; 128 x 2048 x 4096 28.3
+//      / 30.3; 200 x 2048 x 300 14.7 / 11.6; 128 x 2048 x 1536 20.2 / 18.5; 200 x 2048 x
+//      1536 33.1 / 27.1; 6000 x 2048 x 64 28.7 / 26.8);
+//    - longer K with at most 8 tiles (64 x 4096 x 512 10.5 / 11.8; 128 x 8192 x 128 11.7 /
+//      13.4; 256 x 4096 x 256 takes the tiled split, 14.2 / 13.6).
 bool small_preferred(const GemmDesc &d) {
     if (d.M <= 4 || d.N <= 4) return true;
     const int64_t tiles64 = cdiv(d.M, 64) * cdiv(d.N, 64) * d.batch;
     if (tiles64 >= 256) return false;
-    if ((d.M < d.N ? d.M : d.N) <= 32 || d.K <= 64) return true;
-    if (d.K <= 1024) return tiles64 < 128;
+    const int mn = d.M < d.N ? d.M : d.N;
+    if (mn <= 32 || d.K <= 64) return true;
     if (d.K <= 2048) {
-        const int64_t wgs = cdiv(d.M, 64) * cdiv(d.N, 16) * d.batch;  // row blocks of 4
-        return tiles64 < 12 || (wgs >= 128 && tiles64 < 80);
+        const bool whole = plan_small(d).splits == 1;
+        if (d.K <= 1024) return tiles64 < 24 || (whole && (tiles64 < 128 || d.K >= 768));
+        return tiles64 < 12 || (whole && (tiles64 < 80 || mn <= 128));
     }
-    return tiles64 <= 4;
+    return tiles64 <= 8;
 }
 
 int launch_gemm_small(hipStream_t stream, const GemmDesc &d) {
