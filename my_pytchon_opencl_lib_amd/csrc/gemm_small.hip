@@ -417,10 +417,11 @@ int launch_gemm_small(hipStream_t stream, const GemmDesc &d) {
     a.accumulate = d.accumulate;
     a.tiles_m = (int)cdiv(d.M, 16 * pl.mb);
     a.tiles_n = (int)cdiv(d.N, 16 * pl.nb);
-    // With 32x32 tiles, consecutive tiles (which share an XCD's L2) step along the shorter
-    // side, so each XCD reads a contiguous share of the larger operand (stepping along N:
-    // 64 x 1536 x 4096 13.73 us against 12.35).
-    a.m_fast = pl.nb == 2 && d.N >= d.M;
+    // Consecutive tiles (which share an XCD's L2) step along the shorter side, so each XCD
+    // reads a contiguous share of the larger operand. Against stepping along N (us):
+    // 64 x 1536 x 4096 (32x32 tiles) 12.35 / 13.73; 80 x 1024 x 4096 16.55 / 19.21;
+    // 80 x 2048 x 2048 15.31 / 18.56; 128 x 1024 x 4096 TN 22.32 / 22.94.
+    a.m_fast = d.N >= d.M;
     a.batch = d.batch;
     const int G = (int)cdiv(d.K, KG);
     a.groups_per_split = (int)cdiv(G, pl.splits);
