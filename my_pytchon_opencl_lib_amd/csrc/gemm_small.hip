@@ -10,6 +10,9 @@
 //  * A work-group owns a (16*MB) x (16*NB) tile of C and has NW wavefronts; wavefront w
 //    multiplies the w-th contiguous share of the work-group's 16-wide k-groups, and the NW
 //    partial tiles are added in LDS in the order w = 0..NW-1 (deterministic).
+//  * Work-groups are dealt to the 8 XCDs in contiguous chunks of tiles, and consecutive
+//    tiles step along the shorter side of C, so each XCD's L2 holds a contiguous share of
+//    the larger operand.
 //  * No LDS staging of operands: wavefronts of one work-group share no operand data (each
 //    has its own k range), so fragments go from global memory (L2) straight to registers,
 //    three k-groups in flight per wavefront.
