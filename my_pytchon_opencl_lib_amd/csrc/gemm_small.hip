@@ -374,14 +374,17 @@ SmallPlan plan_small(const GemmDesc &d) {
 //  * fewer 64x64 tiles than CUs, and then
 //    - a thin output (M or N <= 32) or K <= 64 (17 x 8192 x 1024 14.4 / 18.5);
 //    - K <= 1024: fewer than 24 tiles, or a plan without a k split (no reduce launch) and
-//      fewer than 128 tiles or K >= 768 (777 x 300 x 300 9.1 / 10.6; 128 x 1024 x 4096
-//      16.1 / 20.7; 512 x 1024 x 1024 16.1 / 20.8; 2048 x 300 x 300 15.8 / 11.1; with a k
-//      split the tiled kernel wins: 64 x 1024 x 1536 12.7 / 11.6, 200 x 1024 x 512 13.1 /
-//      11.8);
-//    - K <= 2048: fewer than 12 tiles, or a plan without a k split and fewer than 80 tiles
-//      or an output at most 128 wide (64 x 1536 x 4096 14.1 / 19.0; 128 x 2048 x 4096 28.3
-//      / 30.3; 200 x 2048 x 300 14.7 / 11.6; 128 x 2048 x 1536 20.2 / 18.5; 200 x 2048 x
-//      1536 33.1 / 27.1; 6000 x 2048 x 64 28.7 / 26.8);
+//      then, with 32x32 tiles, fewer than 128 tiles or K >= 768 (128 x 1024 x 4096 16.1 /
+//      20.7; 512 x 1024 x 1024 16.1 / 20.8; 2048 x 300 x 300 15.8 / 11.1), with 64x16 tiles
+//      (A transposed, or other M) fewer than 80 (777 x 300 x 300 9.1 / 10.6; TN: 64 x 1024 x
+//      4096 12.1 / 14.0, 200 x 1024 x 1536 22.8 / 18.6, 512 x 1024 x 1024 22.7 / 21.1);
+//      with a k split the tiled kernel wins: 64 x 1024 x 1536 12.7 / 11.6, 200 x 1024 x
+//      512 13.1 / 11.8;
+//    - K <= 2048: fewer than 12 tiles, or a plan without a k split and then, with 32x32
+//      tiles, fewer than 80 tiles or an output at most 128 wide (64 x 1536 x 4096 14.1 /
+//      19.0; 128 x 2048 x 4096 28.3 / 30.3; 200 x 2048 x 1536 33.1 / 27.1), with 64x16
+//      tiles fewer than 48 (TN: 64 x 2048 x 4096 21.8 / 19.3, 128 x 2048 x 4096 43.7 /
+//      30.7); 200 x 2048 x 300 14.7 / 11.6 and 6000 x 2048 x 64 28.7 / 26.8 split;
 //    - longer K with at most 8 tiles (64 x 4096 x 512 10.5 / 11.8; 128 x 8192 x 128 11.7 /
 //      13.4; 256 x 4096 x 256 takes the tiled split, 14.2 / 13.6).
 bool small_preferred(const GemmDesc &d) {
@@ -391,9 +394,14 @@ bool small_preferred(const GemmDesc &d) {
     const int mn = d.M < d.N ? d.M : d.N;
     if (mn <= 32 || d.K <= 64) return true;
     if (d.K <= 2048) {
-        const bool whole = plan_small(d).splits == 1;
-        if (d.K <= 1024) return tiles64 < 24 || (whole && (tiles64 < 128 || d.K >= 768));
-        return tiles64 < 12 || (whole && (tiles64 < 80 || mn <= 128));
+        const SmallPlan pl = plan_small(d);
+        const bool whole = pl.splits == 1;
+        if (pl.nb == 2) {  // 32x32 tiles
+            if (d.K <= 1024) return tiles64 < 24 || (whole && (tiles64 < 128 || d.K >= 768));
+            return tiles64 < 12 || (whole && (tiles64 < 80 || mn <= 128));
+        }
+        if (d.K <= 1024) return tiles64 < 24 || (whole && tiles64 < 80);
+        return tiles64 < 12 || (whole && tiles64 < 48);
     }
     return tiles64 <= 8;
 }
