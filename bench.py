@@ -37,11 +37,12 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="target duration of the bounded CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--pmc-target", nargs="?", const="4096", choices=["4096", "5a"],
+    p.add_argument("--pmc-target", nargs="?", const="4096", choices=["4096", "5a", "3"],
                    help="run only a profiling target for rocprofv3 --pmc passes: '4096' (the "
                         "default) the three 4096^3 forms 3x each, '5a' config 5a (1000x777x3000 "
-                        "NN) 3x; then a 256 MiB device copy 3x (the reference for scaling "
-                        "FETCH_SIZE / WRITE_SIZE to bytes)")
+                        "NN) 3x, '3' the config-3 gate GEMM (64x1536x4096 + bias) over 3 "
+                        "timestep inputs; then a 256 MiB device copy 3x (the reference for "
+                        "scaling FETCH_SIZE / WRITE_SIZE to bytes)")
     return p.parse_args()
 
 
@@ -197,7 +198,15 @@ def main():
 
 def pmc_target(torch, nncl, which="4096"):
     g = torch.Generator(device="cuda:0")
-    if which == "5a":
+    if which == "3":
+        g.manual_seed(2)
+        X = torch.randn(3, 64, 1536, device="cuda:0", generator=g)
+        W = (torch.rand(1536, 4096, device="cuda:0", generator=g) * 2 - 1) / 32
+        bias = (torch.rand(4096, device="cuda:0", generator=g) * 2 - 1) / 32
+        Y = torch.empty(64, 4096, device="cuda:0")
+        for i in range(3):
+            nncl.gemm(X[i], W, bias=bias, out=Y)
+    elif which == "5a":
         g.manual_seed(4)
         A = torch.rand(1000, 777, device="cuda:0", generator=g) * 2 - 1
         B = torch.rand(777, 3000, device="cuda:0", generator=g) * 2 - 1
