@@ -375,16 +375,17 @@ SmallPlan plan_small(const GemmDesc &d) {
 //    - a thin output (M or N <= 32) or K <= 64 (17 x 8192 x 1024 14.4 / 18.5);
 //    - K <= 1024: fewer than 24 tiles, or a plan without a k split (no reduce launch) and
 //      then, with 32x32 tiles, fewer than 128 tiles or K >= 768 (128 x 1024 x 4096 16.1 /
-//      20.7; 512 x 1024 x 1024 16.1 / 20.8; 2048 x 300 x 300 15.8 / 11.1), with 64x16 tiles
-//      (A transposed, or other M) fewer than 80 (777 x 300 x 300 9.1 / 10.6; TN: 64 x 1024 x
-//      4096 12.1 / 14.0, 200 x 1024 x 1536 22.8 / 18.6, 512 x 1024 x 1024 22.7 / 21.1);
-//      with a k split the tiled kernel wins: 64 x 1024 x 1536 12.7 / 11.6, 200 x 1024 x
-//      512 13.1 / 11.8;
+//      20.7; 512 x 1024 x 1024 16.1 / 20.8; 2048 x 300 x 300 15.8 / 11.1); with 64x16 tiles
+//      fewer than 128 (777 x 300 x 300 9.1 / 10.6; 200 x 1024 x 1536 17.7 / 18.4), or 80
+//      with A transposed (TN: 64 x 1024 x 4096 12.1 / 14.0, 200 x 1024 x 1536 22.8 / 18.6,
+//      512 x 1024 x 1024 22.7 / 21.1); with a k split the tiled kernel wins: 64 x 1024 x
+//      1536 12.7 / 11.6, 200 x 1024 x 512 13.1 / 11.8;
 //    - K <= 2048: fewer than 12 tiles, or a plan without a k split and then, with 32x32
 //      tiles, fewer than 80 tiles or an output at most 128 wide (64 x 1536 x 4096 14.1 /
-//      19.0; 128 x 2048 x 4096 28.3 / 30.3; 200 x 2048 x 1536 33.1 / 27.1), with 64x16
-//      tiles fewer than 48 (TN: 64 x 2048 x 4096 21.8 / 19.3, 128 x 2048 x 4096 43.7 /
-//      30.7); 200 x 2048 x 300 14.7 / 11.6 and 6000 x 2048 x 64 28.7 / 26.8 split;
+//      19.0; 128 x 2048 x 4096 28.3 / 30.3; 200 x 2048 x 1536 33.1 / 27.1); with 64x16
+//      tiles fewer than 80, with A transposed and K > 1536 fewer than 48 (TN: 64 x 1536 x
+//      4096 17.4 / 19.8, 64 x 2048 x 4096 21.8 / 19.3, 128 x 2048 x 4096 43.7 / 30.7);
+//      200 x 2048 x 300 14.7 / 11.6 and 6000 x 2048 x 64 28.7 / 26.8 split;
 //    - longer K with at most 8 tiles (64 x 4096 x 512 10.5 / 11.8; 128 x 8192 x 128 11.7 /
 //      13.4; 256 x 4096 x 256 takes the tiled split, 14.2 / 13.6).
 bool small_preferred(const GemmDesc &d) {
@@ -400,8 +401,12 @@ bool small_preferred(const GemmDesc &d) {
             if (d.K <= 1024) return tiles64 < 24 || (whole && (tiles64 < 128 || d.K >= 768));
             return tiles64 < 12 || (whole && (tiles64 < 80 || mn <= 128));
         }
+        if (!d.transA) {  // 64x16 tiles, A K-contiguous
+            if (d.K <= 1024) return tiles64 < 24 || (whole && tiles64 < 128);
+            return tiles64 < 12 || (whole && tiles64 < 80);
+        }
         if (d.K <= 1024) return tiles64 < 24 || (whole && tiles64 < 80);
-        return tiles64 < 12 || (whole && tiles64 < 48);
+        return tiles64 < 12 || (whole && tiles64 < (d.K <= 1536 ? 80 : 48));
     }
     return tiles64 <= 8;
 }
