@@ -348,18 +348,20 @@ SmallPlan plan_small(const GemmDesc &d) {
         pl = SmallPlan{mb, 1, nw, s, wgs};
         if (wgs * s >= 256) break;
     }
-    // 32x32 tiles (2 row blocks x 2 column blocks) instead of 64x16 when they make as many
-    // work-groups and A is K-contiguous: a work-group then reads 4 fragments per k-group
-    // instead of 5, and each XCD half of the activation panel that every work-group of the
-    // gate GEMM re-reads. Measured (graph replay, us, 32x32 / 64x16): 64 x 1536 x 4096 +
-    // bias 12.35 / 14.17; 64 x 1024 x 4096 9.55 / 11.18; 128 x 2048 x 2048 14.82 / 19.07;
-    // batch-32 128 x 128 x 64 4.24 / 4.71, 128 x 64 x 128 NT 4.60 / 4.76; 256^3 3.52 / 3.51.
-    // With A transposed they ran slower (64 x 1536 x 4096 TN 18.84 / 16.84).
+    // 32x32 tiles (2 row blocks x 2 column blocks) instead of 64x16 or 48x16 when A is
+    // K-contiguous, with the same k split: a work-group then reads 4 fragments per k-group
+    // instead of 5 (4), and a 32-row share of A. Measured (graph replay, us, 32x32 /
+    // 64x16): 64 x 1536 x 4096 + bias 12.35 / 14.17; 64 x 1024 x 4096 9.55 / 11.18;
+    // 128 x 2048 x 2048 14.82 / 19.07; 777 x 300 x 300 6.20 / 8.69; 200 x 1024 x 1536
+    // 15.31 / 17.19; 80 x 1024 x 4096 15.04 / 16.37; 200 x 777 x 300 (48x16) 8.82 / 10.10;
+    // batch-32 128 x 128 x 64 4.24 / 4.71, 128 x 64 x 128 NT 4.60 / 4.76; 256^3 (16x16
+    // plan, kept) 3.52 / 3.51; 100 x 777 x 300 (16x16 plan, kept) 9.00 / 8.11. With A
+    // transposed they ran slower (64 x 1536 x 4096 TN 18.84 / 16.84).
     // MIGEMM_SMALL_NB (tuning and tests, read per call): 1 never, 2 always (M, N > 16).
     const int force_nb = env_value("MIGEMM_SMALL_NB");
     const int64_t wgs22 = cdiv(d.M, 32) * cdiv(d.N, 32) * d.batch;
     if (force_nb == 2 ? d.M > 16 && d.N > 16
-                      : force_nb != 1 && pl.mb == 4 && d.N > 16 && !d.transA && wgs22 == pl.wgs)
+                      : force_nb != 1 && pl.mb >= 3 && d.N > 16 && !d.transA)
         pl = SmallPlan{2, 2, nw, pl.splits, wgs22};
     return pl;
 }
