@@ -383,8 +383,8 @@ SmallPlan plan_small(const GemmDesc &d) {
 //      512 x 1024 x 1024 22.7 / 21.1); with a k split the tiled kernel wins: 64 x 1024 x
 //      1536 12.7 / 11.6, 200 x 1024 x 512 13.1 / 11.8;
 //    - K <= 2048: fewer than 12 tiles, or a plan without a k split and then, with 32x32
-//      tiles, fewer than 80 tiles or an output at most 128 wide (64 x 1536 x 4096 14.1 /
-//      19.0; 128 x 2048 x 4096 28.3 / 30.3; 200 x 2048 x 1536 33.1 / 27.1); with 64x16
+//      tiles, fewer than 80 tiles or M <= 128 (64 x 1536 x 4096 14.1 / 19.0; 128 x 2048 x
+//      4096 28.3 / 30.3; 200 x 2048 x 1536 33.1 / 27.1; 6000 x 2048 x 64 28.5 / 26.4); with 64x16
 //      tiles fewer than 80, with A transposed and K > 1536 fewer than 48 (TN: 64 x 1536 x
 //      4096 17.4 / 19.8, 64 x 2048 x 4096 21.8 / 19.3, 128 x 2048 x 4096 43.7 / 30.7);
 //      200 x 2048 x 300 14.7 / 11.6 and 6000 x 2048 x 64 28.7 / 26.8 split;
@@ -401,7 +401,7 @@ bool small_preferred(const GemmDesc &d) {
         const bool whole = pl.splits == 1;
         if (pl.nb == 2) {  // 32x32 tiles
             if (d.K <= 1024) return tiles64 < 24 || (whole && (tiles64 < 128 || d.K >= 768));
-            return tiles64 < 12 || (whole && (tiles64 < 80 || mn <= 128));
+            return tiles64 < 12 || (whole && (tiles64 < 80 || d.M <= 128));
         }
         if (!d.transA) {  // 64x16 tiles, A K-contiguous
             if (d.K <= 1024) return tiles64 < 24 || (whole && tiles64 < 128);
