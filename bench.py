@@ -233,9 +233,8 @@ def pmc_target(torch, nncl, which="4096"):
 
 def tiled_kernel_name():
     """The kernel that runs the 4096^3 forms: 256x256 tiles with operands loaded straight
-    into LDS, unless MIGEMM_DIRECT=0 selects the register-staged kernel."""
-    return "gemm_mfma_kernel" if os.environ.get("MIGEMM_DIRECT", "1") == "0" else \
-        "gemm_direct_kernel"
+    into LDS."""
+    return "gemm_direct_kernel"
 
 
 def load_traffic(kernel_substr):

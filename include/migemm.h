@@ -200,8 +200,27 @@ int migemm_memcpy_h2d(void *stream, void *dst, const void *src, size_t bytes);
 int migemm_memcpy_d2h(void *stream, void *dst, const void *src, size_t bytes);
 int migemm_memset(void *stream, void *dst, int value, size_t bytes);
 int migemm_stream_create(void **stream);
+/* Waits for the stream's queued work, frees the library workspace held for it (see
+ * migemm_workspace_release) and destroys it. */
 int migemm_stream_destroy(void *stream);
 int migemm_stream_synchronize(void *stream);
+
+/* Library workspace. Split-K GEMMs, sliced GEMVs and long column sums keep fp32 partial
+ * sums in device memory that the library owns: one growing buffer per (device, stream),
+ * plus one for operands an entry point stages (lstm_gemm_grad_weights' H_prev), so calls
+ * on different streams never share partial sums. The reference host has no counterpart
+ * (its kernels never split K).
+ * Nothing is allocated while a stream is being captured into a HIP graph, and a capturing
+ * stream uses only its own buffers: size them before the capture, with this call or by
+ * running the same calls once on that stream. A call that needs more during a capture
+ * fails with MIGEMM_ERR_WORKSPACE. */
+/* Grows each of `stream`'s two workspace buffers (current device) to >= bytes. */
+int migemm_workspace_reserve(void *stream, size_t bytes);
+/* Waits for the stream's queued work and frees its workspace buffers (current device),
+ * except those a HIP graph captured, which live until the process ends. */
+int migemm_workspace_release(void *stream);
+/* Current size of `stream`'s partial-sum buffer on the current device (0 if none). */
+int migemm_workspace_size(void *stream, size_t *bytes);
 /* Message of the last failing call on this host thread ("" if none). */
 const char *migemm_last_error(void);
 /* Library version, e.g. "0.1.0". */
@@ -221,6 +240,26 @@ const char *migemm_version(void);
 /* Sets the policy; *previous (if not NULL) receives the one it replaces. Calls already
  * enqueued are unaffected. */
 int migemm_set_gemm_policy(int policy, int *previous);
+
+/* Tuning overrides of the dispatcher, process-wide, for tests and tuning sweeps; every
+ * value computes the same product within the fp32 tolerance. 0 (the initial value of every
+ * key) leaves the choice to the dispatcher. No other input (no environment variable)
+ * changes which kernel runs. */
+#define MIGEMM_TUNE_TILE 1         /* tiled kernel's output tile: 32, 64, 128, 256 (256x256)
+                                      or MIGEMM_TILE_128x256 */
+#define MIGEMM_TUNE_SPLITK 2       /* tiled kernel's k ranges: S in 1..64 */
+#define MIGEMM_TUNE_DIRECT 3       /* operands loaded straight into LDS: 1 never,
+                                      2 wherever the kernel applies (also split 128x256) */
+#define MIGEMM_TUNE_SMALL_TILES 4  /* small-output kernel's 32x32 tiles: 1 never,
+                                      2 always (M, N > 16) */
+#define MIGEMM_TUNE_SMALL_SPLITK 5 /* small-output kernel's k ranges: S in 1..64 */
+#define MIGEMM_TILE_128x256 128256
+int migemm_set_tuning(int key, int value, int *previous);
+
+/* Writes a one-line description of the kernel the last GEMM / permute / column-sum call of
+ * this host thread ran (family, output tile, k ranges, load width, shape, layout) into
+ * buf (NUL-terminated, truncated to len). For tests and tuning; the reference has none. */
+int migemm_last_plan(char *buf, size_t len);
 
 #ifdef __cplusplus
 }

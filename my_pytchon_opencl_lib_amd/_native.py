@@ -27,6 +27,17 @@ MIGEMM_POLICY_TILED = 1
 MIGEMM_POLICY_SMALL = 2
 MIGEMM_POLICY_SKINNY = 3
 
+# Tuning keys (migemm_set_tuning); 0 = the dispatcher's choice
+MIGEMM_TUNE_TILE = 1
+MIGEMM_TUNE_SPLITK = 2
+MIGEMM_TUNE_DIRECT = 3
+MIGEMM_TUNE_SMALL_TILES = 4
+MIGEMM_TUNE_SMALL_SPLITK = 5
+MIGEMM_TILE_128x256 = 128256
+TUNE_KEYS = {"tile": MIGEMM_TUNE_TILE, "splitk": MIGEMM_TUNE_SPLITK,
+             "direct": MIGEMM_TUNE_DIRECT, "small_tiles": MIGEMM_TUNE_SMALL_TILES,
+             "small_splitk": MIGEMM_TUNE_SMALL_SPLITK}
+
 STATUS_NAMES = {
     MIGEMM_OK: "MIGEMM_OK",
     MIGEMM_ERR_INVALID_ARG: "MIGEMM_ERR_INVALID_ARG",
@@ -91,9 +102,14 @@ SIGNATURES = {
     "migemm_stream_create": ([ctypes.POINTER(_vp)], _i32),
     "migemm_stream_destroy": ([_vp], _i32),
     "migemm_stream_synchronize": ([_vp], _i32),
+    "migemm_workspace_reserve": ([_vp, _sz], _i32),
+    "migemm_workspace_release": ([_vp], _i32),
+    "migemm_workspace_size": ([_vp, ctypes.POINTER(_sz)], _i32),
     "migemm_last_error": ([], ctypes.c_char_p),
     "migemm_version": ([], ctypes.c_char_p),
     "migemm_set_gemm_policy": ([_i32, _ip], _i32),
+    "migemm_set_tuning": ([_i32, _i32, _ip], _i32),
+    "migemm_last_plan": ([ctypes.c_char_p, _sz], _i32),
 }
 
 _lib = None
@@ -151,3 +167,37 @@ def set_gemm_policy(policy):
     prev = ctypes.c_int(0)
     call("migemm_set_gemm_policy", int(policy), ctypes.byref(prev))
     return prev.value
+
+
+def set_tuning(key, value):
+    """Set one dispatcher tuning override (a TUNE_KEYS name or MIGEMM_TUNE_* value; 0 = the
+    dispatcher's choice); returns the previous value."""
+    prev = ctypes.c_int(0)
+    call("migemm_set_tuning", TUNE_KEYS.get(key, key), int(value), ctypes.byref(prev))
+    return prev.value
+
+
+class tuned:
+    """Context manager: tuning overrides for a block (tile=, splitk=, direct=, small_tiles=,
+    small_splitk=), the previous values restored on exit."""
+
+    def __init__(self, **overrides):
+        self.overrides = overrides
+        self.saved = {}
+
+    def __enter__(self):
+        for k, v in self.overrides.items():
+            self.saved[k] = set_tuning(k, 0 if v is None else v)
+        return self
+
+    def __exit__(self, *exc):
+        for k, v in self.saved.items():
+            set_tuning(k, v)
+        return False
+
+
+def last_plan():
+    """What the last GEMM / permute / column-sum call of this thread ran."""
+    buf = ctypes.create_string_buffer(256)
+    call("migemm_last_plan", buf, len(buf))
+    return buf.value.decode()

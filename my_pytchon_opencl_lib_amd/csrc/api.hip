@@ -50,6 +50,9 @@ bool extent(int batch, int64_t stride, int rows, int64_t ld, int cols, int64_t *
 struct DeviceWorkspace {
     void *ptr = nullptr;
     size_t bytes = 0;
+    // Handed out to work captured into a HIP graph: the graph keeps the address, so the
+    // buffer is never freed (a replay may run at any later time).
+    bool captured = false;
 };
 std::mutex g_ws_mutex;
 // keyed by (device, stream, slot)
@@ -77,12 +80,14 @@ int hip_check(hipError_t e, const char *what) {
 // they can share a buffer, and calls on different streams (the reference host keeps one
 // queue per thread) never share one. A buffer that is outgrown is retired, not freed:
 // work already queued, or a HIP graph captured earlier, may still refer to it, so retired
-// buffers live until the process ends.
+// buffers live until the process ends (the doubling growth keeps them below the live
+// buffer's size). migemm_workspace_release / migemm_stream_destroy free a stream's live
+// buffers once its queued work is done, unless a graph captured them.
 // Nothing is allocated while the stream is being captured into a HIP graph (an allocation
-// would invalidate the capture). A capturing stream whose own buffer is too small (torch,
-// for one, captures on a stream of its own) takes the smallest large-enough buffer that
-// eager calls on the device have sized; the graph then shares it with that buffer's
-// stream.
+// would invalidate the capture), and a capturing stream only uses its own buffer: work on
+// another stream may run at the same time as a replay, so a borrowed buffer could race.
+// A caller sizes the capturing stream's buffer beforehand with migemm_workspace_reserve or
+// by running the same call once on that stream outside the capture.
 void *workspace(hipStream_t stream, size_t bytes, int *status, int slot) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -104,23 +109,17 @@ void *workspace(hipStream_t stream, size_t bytes, int *status, int slot) {
     const auto key = std::make_tuple(dev, reinterpret_cast<uintptr_t>(stream), slot);
     auto it = g_ws.find(key);
     if (it != g_ws.end() && it->second.bytes >= bytes) {
+        if (capture != hipStreamCaptureStatusNone) it->second.captured = true;
         *status = MIGEMM_OK;
         return it->second.ptr;
     }
     if (capture != hipStreamCaptureStatusNone) {
-        const DeviceWorkspace *best = nullptr;
-        for (const auto &kv : g_ws)
-            if (std::get<0>(kv.first) == dev && std::get<2>(kv.first) == slot &&
-                kv.second.bytes >= bytes && (best == nullptr || kv.second.bytes < best->bytes))
-                best = &kv.second;
-        if (best == nullptr) {
-            *status = set_error(MIGEMM_ERR_WORKSPACE,
-                                "workspace of %zu bytes is needed during HIP graph capture: "
-                                "run the same call once outside the capture first", bytes);
-            return nullptr;
-        }
-        *status = MIGEMM_OK;
-        return best->ptr;
+        *status = set_error(MIGEMM_ERR_WORKSPACE,
+                            "%zu bytes of workspace are needed during HIP graph capture but "
+                            "the capturing stream holds %zu: call migemm_workspace_reserve on "
+                            "that stream, or run the same call once on it, before capturing",
+                            bytes, it != g_ws.end() ? it->second.bytes : (size_t)0);
+        return nullptr;
     }
     DeviceWorkspace &w = g_ws[key];
     size_t want = bytes < ((size_t)8 << 20) ? ((size_t)8 << 20) : bytes;
@@ -134,8 +133,37 @@ void *workspace(hipStream_t stream, size_t bytes, int *status, int slot) {
     }
     w.ptr = p;  // the previous buffer (if any) is retired, never freed
     w.bytes = want;
+    w.captured = false;
     *status = MIGEMM_OK;
     return w.ptr;
+}
+
+float *partial_buffer(hipStream_t stream, const GemmDesc &d, size_t bytes, int *status) {
+    if (d.scratch == nullptr) return static_cast<float *>(workspace(stream, bytes, status, 0));
+    if (bytes > d.scratch_bytes) {
+        *status = set_error(MIGEMM_ERR_WORKSPACE,
+                            "this GEMM keeps %zu bytes of partial sums but the scratch it was "
+                            "given holds %zu", bytes, d.scratch_bytes);
+        return nullptr;
+    }
+    *status = MIGEMM_OK;
+    return d.scratch;
+}
+
+// Frees the live workspace buffers of `stream` on the current device (the caller has
+// waited for the stream's work). Buffers a graph captured are kept.
+static int release_workspace(hipStream_t stream) {
+    int dev = 0;
+    MIGEMM_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    for (int slot = 0; slot < kWorkspaceSlots; ++slot) {
+        auto it = g_ws.find(std::make_tuple(dev, reinterpret_cast<uintptr_t>(stream), slot));
+        if (it == g_ws.end()) continue;
+        const DeviceWorkspace w = it->second;
+        g_ws.erase(it);
+        if (!w.captured) MIGEMM_HIP(hipFree(w.ptr));
+    }
+    return MIGEMM_OK;
 }
 
 // Validates a general GEMM request and fills `d`. No HIP call is made.
@@ -194,8 +222,22 @@ static int validate_gemm(int transA, int transB, int M, int N, int K, const floa
     return MIGEMM_OK;
 }
 
-// Kernel-family policy (migemm_set_gemm_policy), process-wide.
+// Kernel-family policy (migemm_set_gemm_policy) and tuning overrides (migemm_set_tuning),
+// process-wide.
 static std::atomic<int> g_policy{MIGEMM_POLICY_AUTO};
+static std::atomic<int> g_tuning[MIGEMM_TUNE_SMALL_SPLITK + 1];
+
+int tuning(int key) { return g_tuning[key].load(std::memory_order_relaxed); }
+
+static thread_local PlanRecord g_plan = {"none", 0, 0, 0, 0, 0, 0, 0, 0, false, false};
+
+void record_plan(const PlanRecord &p) { g_plan = p; }
+
+void record_plan(const char *kernel, const GemmDesc &d, int bm, int bn, int splits,
+                 int load_bytes) {
+    g_plan = PlanRecord{kernel, bm, bn, splits, load_bytes, d.M, d.N, d.K, d.batch,
+                        d.transA, d.transB};
+}
 
 static int run_gemm(hipStream_t stream, const GemmDesc &desc) {
     GemmDesc d = desc;
@@ -555,7 +597,50 @@ int migemm_stream_create(void **stream) {
 int migemm_stream_destroy(void *stream) {
     clear_error();
     if (stream == nullptr) return MIGEMM_OK;
-    MIGEMM_HIP(hipStreamDestroy(static_cast<hipStream_t>(stream)));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // the stream's queued work may still use its workspace: wait for it, then free both
+    MIGEMM_HIP(hipStreamSynchronize(s));
+    int rc = release_workspace(s);
+    if (rc != MIGEMM_OK) return rc;
+    MIGEMM_HIP(hipStreamDestroy(s));
+    return MIGEMM_OK;
+}
+
+int migemm_workspace_reserve(void *stream, size_t bytes) {
+    clear_error();
+    if (bytes == 0) return MIGEMM_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    MIGEMM_HIP(hipStreamIsCapturing(s, &capture));
+    if (capture != hipStreamCaptureStatusNone)
+        return set_error(MIGEMM_ERR_INVALID_ARG,
+                         "workspace_reserve: the stream is being captured into a HIP graph");
+    int st = MIGEMM_OK;
+    for (int slot = 0; slot < kWorkspaceSlots; ++slot)
+        if (workspace(s, bytes, &st, slot) == nullptr) return st;
+    return MIGEMM_OK;
+}
+
+int migemm_workspace_release(void *stream) {
+    clear_error();
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    MIGEMM_HIP(hipStreamIsCapturing(s, &capture));
+    if (capture != hipStreamCaptureStatusNone)
+        return set_error(MIGEMM_ERR_INVALID_ARG,
+                         "workspace_release: the stream is being captured into a HIP graph");
+    MIGEMM_HIP(hipStreamSynchronize(s));
+    return release_workspace(s);
+}
+
+int migemm_workspace_size(void *stream, size_t *bytes) {
+    clear_error();
+    if (bytes == nullptr) return set_error(MIGEMM_ERR_INVALID_ARG, "workspace_size: null pointer");
+    int dev = 0;
+    MIGEMM_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    auto it = g_ws.find(std::make_tuple(dev, reinterpret_cast<uintptr_t>(stream), 0));
+    *bytes = it != g_ws.end() ? it->second.bytes : 0;
     return MIGEMM_OK;
 }
 
@@ -568,6 +653,40 @@ int migemm_stream_synchronize(void *stream) {
 const char *migemm_last_error(void) { return g_last_error; }
 
 const char *migemm_version(void) { return "0.1.0"; }
+
+int migemm_set_tuning(int key, int value, int *previous) {
+    clear_error();
+    bool ok;
+    switch (key) {
+        case MIGEMM_TUNE_TILE:
+            ok = value == 0 || value == 32 || value == 64 || value == 128 || value == 256 ||
+                 value == MIGEMM_TILE_128x256;
+            break;
+        case MIGEMM_TUNE_SPLITK:
+        case MIGEMM_TUNE_SMALL_SPLITK: ok = value >= 0 && value <= 64; break;
+        case MIGEMM_TUNE_DIRECT:
+        case MIGEMM_TUNE_SMALL_TILES: ok = value >= 0 && value <= 2; break;
+        default:
+            return set_error(MIGEMM_ERR_INVALID_ARG, "set_tuning: unknown key %d", key);
+    }
+    if (!ok)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "set_tuning: value %d is not valid for key %d",
+                         value, key);
+    const int old = g_tuning[key].exchange(value);
+    if (previous != nullptr) *previous = old;
+    return MIGEMM_OK;
+}
+
+int migemm_last_plan(char *buf, size_t len) {
+    clear_error();
+    if (buf == nullptr || len == 0)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "last_plan: null or empty buffer");
+    const PlanRecord &p = g_plan;
+    snprintf(buf, len, "%s tile=%dx%d splits=%d load_bytes=%d M=%d N=%d K=%d batch=%d %c%c",
+             p.kernel, p.bm, p.bn, p.splits, p.load_bytes, p.M, p.N, p.K, p.batch,
+             p.transA ? 'T' : 'N', p.transB ? 'T' : 'N');
+    return MIGEMM_OK;
+}
 
 int migemm_set_gemm_policy(int policy, int *previous) {
     clear_error();

@@ -157,6 +157,7 @@ int launch_permute(hipStream_t stream, const float *src, float *dst, const int *
         if (batch <= 65535 && (int64_t)tiles_r * tiles_c <= INT32_MAX) {
             hipLaunchKernelGGL(transpose_kernel, dim3(tiles_r * tiles_c, (unsigned)batch),
                                dim3(256), 0, stream, src, dst, R, Cc, tiles_c);
+            record_plan(PlanRecord{"transpose", 32, 32, 1, 0, R, Cc, 0, (int)batch, false, false});
             return hip_check(hipGetLastError(), "transpose_kernel launch");
         }
     }
@@ -178,6 +179,7 @@ int launch_permute(hipStream_t stream, const float *src, float *dst, const int *
     int64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     hipLaunchKernelGGL(permute_gather_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    record_plan(PlanRecord{"permute_gather", 0, 0, 1, 0, 0, 0, 0, num_dims, false, false});
     return hip_check(hipGetLastError(), "permute_gather_kernel launch");
 }
 
@@ -205,6 +207,8 @@ int launch_column_sum(hipStream_t stream, const float *X, float *Y, int outer, i
         hipLaunchKernelGGL(column_sum_kernel<1>, grid, dim3(256), 0, stream, X, dst, outer,
                            axis, inner, rows, (int)(accumulate && chunks == 1));
     const int rc = hip_check(hipGetLastError(), "column_sum_kernel launch");
+    record_plan(PlanRecord{"column_sum", rows, vec ? 4 : 1, chunks, 0, outer, inner, axis, 1,
+                           false, false});
     if (rc != MIGEMM_OK || chunks == 1) return rc;
     return launch_reduce_slices(stream, dst, chunks, outer, 1, inner, nullptr, Y, inner, inner,
                                 accumulate);

@@ -9,16 +9,13 @@
 
 namespace migemm {
 
-// Per tile shape: launches gemm_direct_kernel for the operand layouts (akc, bkc), load
-// widths (wa, wb: 4 or 1 floats per lane) and pipeline variant `var` (MIGEMM_DVAR).
-int launch_direct_256(hipStream_t stream, TiledArgs &a, bool akc, bool bkc, int wa, int wb,
-                      int var);
+// Per tile shape: launches gemm_direct_kernel for the operand layouts (akc, bkc) and load
+// widths (wa, wb: 4 or 1 floats per lane).
+int launch_direct_256(hipStream_t stream, TiledArgs &a, bool akc, bool bkc, int wa, int wb);
 int launch_direct_128x256(hipStream_t stream, TiledArgs &a, bool akc, bool bkc, int wa,
-                          int wb, int var);
-int launch_direct_128(hipStream_t stream, TiledArgs &a, bool akc, bool bkc, int wa, int wb,
-                      int var);
-int launch_direct_64(hipStream_t stream, TiledArgs &a, bool akc, bool bkc, int wa, int wb,
-                     int var);
+                          int wb);
+int launch_direct_128(hipStream_t stream, TiledArgs &a, bool akc, bool bkc, int wa, int wb);
+int launch_direct_64(hipStream_t stream, TiledArgs &a, bool akc, bool bkc, int wa, int wb);
 
 namespace {
 

@@ -32,23 +32,18 @@
 //  * K order within an MFMA step, split-K ranges, the XCD-aware raster and the epilogue are
 //    those of gemm_mfma_kernel (tiled_common.h); each output's k sum runs in the same order
 //    as in gemm_mfma_kernel, so both give identical bits for one split.
-#include <stdlib.h>
-
 #include "gemm_direct.h"
 
 namespace migemm {
 
 int launch_gemm_direct(hipStream_t stream, TiledArgs &a, int bm, int bn, bool akc, bool bkc,
                        int wa, int wb) {
-    // MIGEMM_DVAR (read per call) selects pipeline variants for tuning sweeps. An operand
-    // with wa / wb = 1 (rows not 16-byte aligned, or a contiguous extent that is not a
-    // multiple of 4) is loaded 4 bytes per lane in the shipped pipeline of each tile.
-    const char *v = getenv("MIGEMM_DVAR");
-    const int var = v != nullptr ? atoi(v) : 0;
-    if (bm == 256) return launch_direct_256(stream, a, akc, bkc, wa, wb, var);
-    if (bm == 64) return launch_direct_64(stream, a, akc, bkc, wa, wb, var);
-    if (bn == 256) return launch_direct_128x256(stream, a, akc, bkc, wa, wb, var);
-    return launch_direct_128(stream, a, akc, bkc, wa, wb, var);
+    // An operand with wa / wb = 1 (rows not 16-byte aligned, or a contiguous extent that is
+    // not a multiple of 4) is loaded 4 bytes per lane in the same pipeline.
+    if (bm == 256) return launch_direct_256(stream, a, akc, bkc, wa, wb);
+    if (bm == 64) return launch_direct_64(stream, a, akc, bkc, wa, wb);
+    if (bn == 256) return launch_direct_128x256(stream, a, akc, bkc, wa, wb);
+    return launch_direct_128(stream, a, akc, bkc, wa, wb);
 }
 
 }  // namespace migemm

@@ -414,14 +414,10 @@ struct TileCfg {
     int bm, bn;
 };
 
-int lds_pad_bytes();
-
 template <int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, bool AV, bool BV>
 int launch_one(hipStream_t s, const TiledArgs &a) {
-    // Dynamic LDS is unused by the kernel; a tuning override (MIGEMM_LDS_PAD bytes) may
-    // reserve some to cap how many work-groups share a CU.
     hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AKC, BKC, AV, BV>),
-                       dim3(a.total), dim3(WM * WN * 64), lds_pad_bytes(), s, a);
+                       dim3(a.total), dim3(WM * WN * 64), 0, s, a);
     return hip_check(hipGetLastError(), "gemm_mfma_kernel launch");
 }
 
@@ -489,23 +485,6 @@ int launch_reduce_slices(hipStream_t stream, const float *partial, int slices, i
 }
 
 namespace {
-// Tuning overrides (MIGEMM_TILE = 32 | 64 | 128 | 128x256 | 256, MIGEMM_SPLITK = S,
-// MIGEMM_DIRECT, MIGEMM_LDS_PAD).
-int env_int(const char *name) {
-    const char *v = getenv(name);
-    return v != nullptr ? atoi(v) : 0;
-}
-int lds_pad_bytes() {
-    static const int pad = env_int("MIGEMM_LDS_PAD");
-    return pad > 0 && pad <= 65536 ? pad : 0;
-}
-// MIGEMM_DIRECT (read per call, for interleaved comparisons in one process): 0 = never use
-// gemm_direct_kernel, 2 = use it for every 128x128 / 128x256 / 256x256 tile it can run
-// (tests), unset or 1 = the measured choice.
-int direct_mode() {
-    const char *v = getenv("MIGEMM_DIRECT");
-    return v != nullptr ? atoi(v) : 1;
-}
 
 // An operand's rows and batch entries all start on 16-byte boundaries, as
 // global_load_lds_dwordx4 needs.
@@ -563,7 +542,9 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     // multiple of 4 is loaded 16 bytes per lane (wa / wb = 4), any other 4 bytes per lane.
     const int wa = av && rows16(d.A, d.lda, d.sA) ? 4 : 1;
     const int wb = bv && rows16(d.B, d.ldb, d.sB) ? 4 : 1;
-    const bool fits = direct_mode() != 0 && d.lda <= (1 << 21) && d.ldb <= (1 << 21);
+    // MIGEMM_TUNE_DIRECT: 1 = never load straight into LDS, 2 = wherever the kernel applies
+    const int direct_mode = tuning(MIGEMM_TUNE_DIRECT);
+    const bool fits = direct_mode != 1 && d.lda <= (1 << 21) && d.ldb <= (1 << 21);
     const bool direct = fits && wa == 4 && wb == 4;
     // Estimated time (us) of `t` tiles of `area` outputs over k at a fitted rate (TFLOP/s)
     // with a per-tile overhead of o k-steps: the work-groups are dealt over the 256 CUs in
@@ -710,22 +691,18 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
             big = c2 <= c1 && c2 <= c0 ? 2 : (c1 <= c0 ? 1 : 0);
         }
     }
-    // read per call, so a tuning sweep can change them between calls in one process;
-    // MIGEMM_TILE = 32 | 64 | 128 | 128x256 | 256
-    const char *tile_env = getenv("MIGEMM_TILE");
-    const int force_split = env_int("MIGEMM_SPLITK");
-    if (tile_env != nullptr) {
-        const int ft = atoi(tile_env);
-        if (strcmp(tile_env, "128x256") == 0) {
-            cfg = 128;
-            big = 1;
-        } else if (ft == 32 || ft == 64 || ft == 128) {
-            cfg = ft;
-            big = 0;
-        } else if (ft == 256) {
-            cfg = 128;
-            big = 2;
-        }
+    // tuning overrides (migemm_set_tuning), validated when they were set
+    const int force_tile = tuning(MIGEMM_TUNE_TILE);
+    const int force_split = tuning(MIGEMM_TUNE_SPLITK);
+    if (force_tile == MIGEMM_TILE_128x256) {
+        cfg = 128;
+        big = 1;
+    } else if (force_tile == 32 || force_tile == 64 || force_tile == 128) {
+        cfg = force_tile;
+        big = 0;
+    } else if (force_tile == 256) {
+        cfg = 128;
+        big = 2;
     }
     if (force_split >= 1) splits = force_split;
     // gemm_direct_kernel runs every 64x64, 128x128, 128x256 and 256x256 tile except split
@@ -736,25 +713,16 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     // in the uncapped variant (gemm_direct_128.hip) 6400 x 4096 x 512 NT 244.4 / 230.6;
     // split 256x256 tiles 1024 x 6400 x 4096 TN 396.6 / 386.1. An unaligned operand is loaded
     // 4 bytes per lane (Linear(500 -> 6565) forward 12000 x 500 x 6565 735.3 -> 648.8 us,
-    // 4096 x 4096 x 4095 TN 1015.6 -> 924.1). MIGEMM_DVAR=9 keeps 64x64 tiles staged.
+    // 4096 x 4096 x 4095 TN 1015.6 -> 924.1).
     const bool use_direct =
-        fits && cfg != 32 && (splits == 1 || big != 1 || direct_mode() == 2) &&
-        !(cfg == 64 && env_int("MIGEMM_DVAR") == 9);
-    if (env_int("MIGEMM_TRACE") != 0)  // tuning aid: the dispatcher's choice, on stderr
-        fprintf(stderr, "migemm tiled %dx%dx%d batch %d t%d%d: tile %s splits %d kernel %s\n",
-                d.M, d.K, d.N, d.batch, (int)d.transA, (int)d.transB,
-                cfg == 128 ? (big == 2 ? "256x256" : big == 1 ? "128x256" : "128x128")
-                           : (cfg == 64 ? "64x64" : "32x32"),
-                splits,
-                use_direct ? (wa == 4 && wb == 4 ? "direct (16-byte loads)" : "direct (4-byte loads)")
-                           : "register-staged");
+        fits && cfg != 32 && (splits == 1 || big != 1 || direct_mode == 2);
 
     a.splits = splits;
     a.partial = nullptr;
     if (splits > 1) {
         int st = MIGEMM_OK;
-        a.partial = static_cast<float *>(
-            workspace(stream, (size_t)splits * d.batch * d.M * d.N * sizeof(float), &st));
+        a.partial =
+            partial_buffer(stream, d, (size_t)splits * d.batch * d.M * d.N * sizeof(float), &st);
         if (a.partial == nullptr) return st;
     }
     int rc;
@@ -794,7 +762,10 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
             break;
         default: rc = launch_tiles<32, 32, 32, 1, 1>(stream, a, akc, bkc, av, bv); break;
     }
-    splits = a.splits;
+    splits = a.splits;  // the launch drops empty k ranges
+    record_plan(use_direct ? "tiled-direct" : "tiled-staged", d,
+                cfg == 128 && big == 2 ? 256 : cfg, cfg == 128 && big >= 1 ? 256 : cfg, splits,
+                use_direct ? (wa == 4 && wb == 4 ? 16 : 4) : 0);
     if (rc != MIGEMM_OK || splits == 1) return rc;
     return launch_reduce_slices(stream, a.partial, splits, d.batch, d.M, d.N, d.bias, d.C,
                                 d.ldc, d.sC, d.accumulate);

@@ -178,21 +178,13 @@ __global__ void __launch_bounds__(SK_THREADS) gemm_skinny_kernel(SkinnyArgs p) {
     }
 }
 
-int env_flag(const char *name) {
-    const char *v = getenv(name);
-    return v != nullptr ? atoi(v) : 0;
-}
-
 template <int MR>
 int launch_mr(hipStream_t st, const SkinnyArgs &a, bool vec, int batch) {
     dim3 grid(a.cblocks, a.slices, batch);
     // B is streamed once: non-temporal loads (measured 1x11008x4096: 32.0 us against 36.6 us
-    // with ordinary loads, 3 rotating copies of B). MIGEMM_GEMV_NT=0 turns them off.
-    static const bool ntl = getenv("MIGEMM_GEMV_NT") == nullptr || env_flag("MIGEMM_GEMV_NT") != 0;
-    if (vec && ntl)
+    // with ordinary loads, 3 rotating copies of B).
+    if (vec)
         hipLaunchKernelGGL((gemm_skinny_kernel<MR, true, true>), grid, dim3(SK_THREADS), 0, st, a);
-    else if (vec)
-        hipLaunchKernelGGL((gemm_skinny_kernel<MR, true, false>), grid, dim3(SK_THREADS), 0, st, a);
     else
         hipLaunchKernelGGL((gemm_skinny_kernel<MR, false, false>), grid, dim3(SK_THREADS), 0, st, a);
     return hip_check(hipGetLastError(), "gemm_skinny_kernel launch");
@@ -239,11 +231,6 @@ int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {
     int kc = 256;
     const int64_t blocks = (int64_t)a.cblocks * d.batch;
     if (blocks >= 1024) kc = 512;  // enough column blocks already: fewer partials
-    static const int force_kc = [] {
-        const char *v = getenv("MIGEMM_GEMV_KC");
-        return v != nullptr ? atoi(v) : 0;
-    }();
-    if (force_kc >= 4) kc = (force_kc < SK_KC_MAX ? force_kc : SK_KC_MAX) / 4 * 4;
     if (kc >= d.K) kc = (d.K + 3) / 4 * 4;
     a.kc = kc;
     a.slices = (d.K + kc - 1) / kc;
@@ -256,7 +243,7 @@ int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {
     if (a.slices > 1) {
         const size_t part_bytes = (size_t)a.slices * d.batch * d.M * d.N * sizeof(float);
         int st = MIGEMM_OK;
-        a.partial = static_cast<float *>(workspace(stream, part_bytes, &st));
+        a.partial = partial_buffer(stream, d, part_bytes, &st);
         if (a.partial == nullptr) return st;
     }
     // 4-column groups never straddle N when N % 4 == 0 (16-byte loads need only 4-byte
@@ -269,6 +256,7 @@ int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {
         case 3: rc = launch_mr<3>(stream, a, vec, d.batch); break;
         default: rc = launch_mr<4>(stream, a, vec, d.batch); break;
     }
+    record_plan("skinny", d, 0, SK_COLS, a.slices, 0);
     if (rc != MIGEMM_OK || a.slices == 1) return rc;
     return launch_reduce_slices(stream, a.partial, a.slices, d.batch, d.M, d.N, d.bias, d.C,
                                 d.ldc, d.sC, d.accumulate);

@@ -318,11 +318,6 @@ int launch_nw(hipStream_t st, const SmallArgs &a, int nw, bool akc, bool bkc) {
                    : launch_layout<MB, NB, 4>(st, a, akc, bkc);
 }
 
-int env_value(const char *name) {
-    const char *v = getenv(name);
-    return v != nullptr ? atoi(v) : 0;
-}
-
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 struct SmallPlan {
@@ -338,13 +333,18 @@ SmallPlan plan_small(const GemmDesc &d) {
     const int nw = G >= 16 ? 8 : 4;
     const int mb_max = (int)(d.M > 48 ? 4 : cdiv(d.M, 16));
     SmallPlan pl{1, 1, nw, 1, 0};
-    for (int mb = mb_max; mb >= 1; --mb) {
-        const int64_t wgs = cdiv(d.M, 16 * mb) * cdiv(d.N, 16) * d.batch;
+    // k ranges that give `wgs` work-groups a CU each: at most 16, of >= 2 k-groups per
+    // wavefront
+    auto split_for = [&](int64_t wgs) {
         const int64_t need = cdiv(256, wgs);
         int64_t cap = G / (2 * nw);
         if (cap > 16) cap = 16;
         if (cap < 1) cap = 1;
-        const int s = (int)(need < cap ? need : cap);
+        return (int)(need < cap ? need : cap);
+    };
+    for (int mb = mb_max; mb >= 1; --mb) {
+        const int64_t wgs = cdiv(d.M, 16 * mb) * cdiv(d.N, 16) * d.batch;
+        const int s = split_for(wgs);
         pl = SmallPlan{mb, 1, nw, s, wgs};
         if (wgs * s >= 256) break;
     }
@@ -357,12 +357,15 @@ SmallPlan plan_small(const GemmDesc &d) {
     // batch-32 128 x 128 x 64 4.24 / 4.71, 128 x 64 x 128 NT 4.60 / 4.76; 256^3 (16x16
     // plan, kept) 3.52 / 3.51; 100 x 777 x 300 (16x16 plan, kept) 9.00 / 8.11. With A
     // transposed they ran slower (64 x 1536 x 4096 TN 18.84 / 16.84).
-    // MIGEMM_SMALL_NB (tuning and tests, read per call): 1 never, 2 always (M, N > 16).
-    const int force_nb = env_value("MIGEMM_SMALL_NB");
-    const int64_t wgs22 = cdiv(d.M, 32) * cdiv(d.N, 32) * d.batch;
+    // MIGEMM_TUNE_SMALL_TILES (tests and tuning): 1 never, 2 always (M, N > 16).
+    // The k split is recomputed for the 32x32 grid, so the split and small_preferred's
+    // whole-K test judge the grid that is launched.
+    const int force_nb = tuning(MIGEMM_TUNE_SMALL_TILES);
     if (force_nb == 2 ? d.M > 16 && d.N > 16
-                      : force_nb != 1 && pl.mb >= 3 && d.N > 16 && !d.transA)
-        pl = SmallPlan{2, 2, nw, pl.splits, wgs22};
+                      : force_nb != 1 && pl.mb >= 3 && d.N > 16 && !d.transA) {
+        const int64_t wgs22 = cdiv(d.M, 32) * cdiv(d.N, 32) * d.batch;
+        pl = SmallPlan{2, 2, nw, split_for(wgs22), wgs22};
+    }
     return pl;
 }
 
@@ -415,7 +418,7 @@ bool small_preferred(const GemmDesc &d) {
 
 int launch_gemm_small(hipStream_t stream, const GemmDesc &d) {
     SmallPlan pl = plan_small(d);
-    const int force_split = env_value("MIGEMM_SMALL_SPLITK");  // tuning, read per call
+    const int force_split = tuning(MIGEMM_TUNE_SMALL_SPLITK);
     if (force_split >= 1) pl.splits = force_split;
 
     SmallArgs a;
@@ -451,8 +454,8 @@ int launch_gemm_small(hipStream_t stream, const GemmDesc &d) {
     a.partial = nullptr;
     if (a.splits > 1) {
         int st = MIGEMM_OK;
-        a.partial = static_cast<float *>(
-            workspace(stream, (size_t)a.splits * d.batch * d.M * d.N * sizeof(float), &st));
+        a.partial = partial_buffer(stream, d,
+                                   (size_t)a.splits * d.batch * d.M * d.N * sizeof(float), &st);
         if (a.partial == nullptr) return st;
     }
     const bool akc = !d.transA;
@@ -467,6 +470,7 @@ int launch_gemm_small(hipStream_t stream, const GemmDesc &d) {
             break;
         default: rc = launch_nw<1>(stream, a, pl.nw, akc, bkc); break;
     }
+    record_plan("small", d, 16 * pl.mb, 16 * pl.nb, a.splits, 0);
     if (rc != MIGEMM_OK || a.splits == 1) return rc;
     return launch_reduce_slices(stream, a.partial, a.splits, d.batch, d.M, d.N, d.bias, d.C,
                                 d.ldc, d.sC, d.accumulate);

@@ -33,7 +33,33 @@ struct GemmDesc {
     int M, N, K, batch;
     bool transA, transB;
     bool accumulate;  // C = C + (op(A) op(B) + bias) instead of C = op(A) op(B) + bias
+    // Caller-provided scratch for partial sums (the no-allocation entry point's static
+    // device array); nullptr = the library workspace of the stream.
+    float *scratch = nullptr;
+    size_t scratch_bytes = 0;
 };
+
+// Device memory for `bytes` of fp32 partial sums of the GEMM `d`: d.scratch when the call
+// brought one (MIGEMM_ERR_WORKSPACE if it is too small), else the stream's workspace
+// (slot 0). Returns nullptr and sets *status on failure.
+float *partial_buffer(hipStream_t stream, const GemmDesc &d, size_t bytes, int *status);
+
+// Tuning override `key` (MIGEMM_TUNE_*), set by migemm_set_tuning; 0 = the dispatcher's
+// choice. A relaxed atomic load: production calls read no environment.
+int tuning(int key);
+
+// What the last dispatch on this host thread ran (migemm_last_plan formats it).
+struct PlanRecord {
+    const char *kernel;  // kernel family, e.g. "tiled-direct", "small", "skinny"
+    int bm, bn;          // output tile (0 when the kernel has none)
+    int splits;          // k ranges (1 = whole K)
+    int load_bytes;      // bytes per lane of each operand load into LDS (16 or 4; 0 = n/a)
+    int M, N, K, batch;
+    bool transA, transB;
+};
+void record_plan(const PlanRecord &p);
+void record_plan(const char *kernel, const GemmDesc &d, int bm, int bn, int splits,
+                 int load_bytes);
 
 // Launchers. They assume a validated descriptor and only enqueue work.
 int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d);

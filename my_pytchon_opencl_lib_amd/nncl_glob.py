@@ -54,10 +54,21 @@ def _stream(t):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
+_INT_RANGES = {ctypes.c_int: (-2 ** 31, 2 ** 31 - 1), ctypes.c_int64: (-2 ** 63, 2 ** 63 - 1)}
+
+
 def _launch(name, tensors, *args):
     """Calls C-ABI entry `name` on the current stream of the tensors' device, with that
     device current (the library launches on the current HIP device). All tensors of one
-    call must live on one device."""
+    call must live on one device. Integer arguments are range-checked against the C types
+    first: ctypes would silently wrap a size or stride of 2^31 or more into a valid-looking
+    int32 (the reference's kernels take int sizes and strides, matmul.cl:8-14, 78-87)."""
+    argtypes = _native.SIGNATURES[name][0][1:]
+    for i, (t, v) in enumerate(zip(argtypes, args)):
+        if t in _INT_RANGES and isinstance(v, int):
+            lo, hi = _INT_RANGES[t]
+            _require(lo <= v <= hi, f"{name}: argument {i + 1} = {v} does not fit the C "
+                                    f"ABI's {'int32' if t is ctypes.c_int else 'int64'}")
     devices = {t.device for t in tensors}
     _require(len(devices) == 1,
              f"all operands must be on one device (got {sorted(map(str, devices))})")

@@ -69,3 +69,26 @@ def check_gemm(C, A, B, transA, transB, bias=None, M=None, N=None, K=None, lda=N
     if ref is not None:
         assert vs_ref <= 2 * tol, f"distance to the reference arithmetic {vs_ref:.3e}"
     return worst_nw, worst_cw, vs_ref
+
+
+class Tuner:
+    """Sets dispatcher tuning overrides through the C ABI (migemm_set_tuning: tile=,
+    splitk=, direct=, small_tiles=, small_splitk=; None = the dispatcher's choice) and
+    restores the values it replaced."""
+
+    def __init__(self):
+        self.saved = {}
+
+    def set(self, **kv):
+        from my_pytchon_opencl_lib_amd import _native
+        for k, v in kv.items():
+            if k == "tile" and v == "128x256":
+                v = _native.MIGEMM_TILE_128x256
+            prev = _native.set_tuning(k, 0 if v is None else int(v))
+            self.saved.setdefault(k, prev)
+
+    def restore(self):
+        from my_pytchon_opencl_lib_amd import _native
+        for k, v in self.saved.items():
+            _native.set_tuning(k, v)
+        self.saved = {}

@@ -10,13 +10,12 @@ exact answer known in any summation order. On random operands the kernel must eq
 register-staged 256x256 kernel bit for bit: both sum each output over k in the same order.
 """
 import ctypes
-import os
 
 import numpy as np
 import pytest
 import torch
 
-from parity import dev, host
+from parity import Tuner, dev, host
 
 pytestmark = pytest.mark.gpu
 
@@ -30,38 +29,15 @@ def small_ints(shape, seed, lo=-4, hi=4):
     return rng.integers(lo, hi + 1, size=shape).astype(np.float32)
 
 
-class _Env:
-    """Sets library tuning variables (read per call) and restores them."""
-
-    def __init__(self):
-        self.saved = {}
-
-    def set(self, **kv):
-        for k, v in kv.items():
-            if k not in self.saved:
-                self.saved[k] = os.environ.get(k)
-            if v is None:
-                os.environ.pop(k, None)
-            else:
-                os.environ[k] = str(v)
-
-    def restore(self):
-        for k, v in self.saved.items():
-            if v is None:
-                os.environ.pop(k, None)
-            else:
-                os.environ[k] = v
-
-
 @pytest.fixture(params=["256", "128x256", "128", "64"])
 def tiled256(request):
-    """The TILED policy with one macro-tile forced (MIGEMM_TILE: 256x256, 128x256,
-    128x128, 64x64), direct loads forced wherever they apply (MIGEMM_DIRECT=2: also for split-K
-    ranges of 128-wide tiles, which the library's own choice runs register-staged)."""
+    """The TILED policy with one macro-tile forced (tuning key tile: 256x256, 128x256,
+    128x128, 64x64), direct loads forced wherever they apply (direct=2: also for split-K
+    ranges of 128x256 tiles, which the library's own choice runs register-staged)."""
     from my_pytchon_opencl_lib_amd import _native
-    env = _Env()
+    env = Tuner()
     prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_TILED)
-    env.set(MIGEMM_TILE=request.param, MIGEMM_DIRECT=2, MIGEMM_SPLITK=None)
+    env.set(tile=request.param, direct=2, splitk=None)
     yield env
     env.restore()
     _native.set_gemm_policy(prev)
@@ -132,7 +108,7 @@ def test_direct_batched_bias_accumulate(tiled256, ta, tb):
 def test_direct_split_ranges(tiled256, splits, ta, tb):
     """Forced split-K: ranges that start past k-tile 0, ranges of 1-2 tiles, the K tail in
     the last range; partial sums through the ordered reduce, with bias and accumulate."""
-    tiled256.set(MIGEMM_SPLITK=splits)
+    tiled256.set(splitk=splits)
     for M, K, N, bias, acc in [(516, 1036, 260, False, False), (256, 100, 512, True, True),
                                (300, 4100, 256, True, False)]:
         say("direct split", splits, M, K, N, ta, tb)
@@ -145,7 +121,7 @@ def test_direct_equals_staged_kernel(tiled256, ta, tb):
     """N(0,1) operands: the direct kernel and the register-staged kernel of the same tile
     (the same MFMA sequence per output) give identical bits. K is not split (the staged NT kernel
     counts ranges in 32-wide k-tiles, the direct kernel in 16-wide ones)."""
-    tiled256.set(MIGEMM_SPLITK=1)
+    tiled256.set(splitk=1)
     g = torch.Generator(device="cpu").manual_seed(77 + ta + 2 * tb)
     for M, K, N in [(768, 528, 1024), (1028, 1000, 516), (256, 4100, 768)]:
         say("direct vs staged", M, K, N, ta, tb)
@@ -153,8 +129,8 @@ def test_direct_equals_staged_kernel(tiled256, ta, tb):
         B = torch.randn((N, K) if tb else (K, N), generator=g).cuda()
         bias = torch.randn(N, generator=g).cuda()
         outs = []
-        for direct in (2, 0):
-            tiled256.set(MIGEMM_DIRECT=direct)
+        for direct in (2, 1):  # direct loads forced, then never
+            tiled256.set(direct=direct)
             c = torch.empty((M, N), device="cuda")
             gemm_ex(ta, tb, M, N, K, A, A.shape[1], 0, B, B.shape[1], 0, bias, c, N, 0, 1)
             outs.append(host(c))
@@ -196,15 +172,15 @@ def test_direct_unaligned_operands_exact(tiled256, M, K, N, ta, tb):
 def test_direct_unaligned_equals_staged_kernel(tiled256, ta, tb):
     """N(0,1) operands with odd K / M / N (4-byte loads into LDS) give the same bits as the
     register-staged kernel of the same tile (one split range)."""
-    tiled256.set(MIGEMM_SPLITK=1)
+    tiled256.set(splitk=1)
     g = torch.Generator(device="cpu").manual_seed(99 + ta + 2 * tb)
     for M, K, N in [(1000, 777, 3000), (131, 1001, 257)]:
         say("direct unaligned vs staged", M, K, N, ta, tb)
         A = torch.randn((K, M) if ta else (M, K), generator=g).cuda()
         B = torch.randn((N, K) if tb else (K, N), generator=g).cuda()
         outs = []
-        for direct in (2, 0):
-            tiled256.set(MIGEMM_DIRECT=direct)
+        for direct in (2, 1):  # direct loads forced, then never
+            tiled256.set(direct=direct)
             c = torch.empty((M, N), device="cuda")
             gemm_ex(ta, tb, M, N, K, A, A.shape[1], 0, B, B.shape[1], 0, None, c, N, 0, 1)
             outs.append(host(c))
@@ -214,18 +190,18 @@ def test_direct_unaligned_equals_staged_kernel(tiled256, ta, tb):
 @pytest.mark.parametrize("ta,tb", LAYOUTS)
 def test_small_kernel_32x32_tiles_exact(ta, tb):
     """The small-output kernel with 32x32 work-group tiles (2 x 2 blocks of 16x16; forced
-    with MIGEMM_SMALL_NB=2 in every layout): ragged M and N, K tails, k ranges split over
+    with the tuning key small_tiles=2 in every layout): ragged M and N, K tails, k ranges split over
     work-groups, batch strides, bias and the accumulating epilogue, exact."""
     from my_pytchon_opencl_lib_amd import _native
-    env = _Env()
+    env = Tuner()
     prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_SMALL)
     try:
-        env.set(MIGEMM_SMALL_NB=2, MIGEMM_SMALL_SPLITK=None)
+        env.set(small_tiles=2, small_splitk=None)
         for M, K, N, batch, bias, acc, splits in [
                 (64, 1536, 4096, 1, True, False, None), (100, 777, 300, 2, True, True, None),
                 (65, 4100, 33, 1, False, True, 5), (130, 40, 70, 3, True, False, None),
                 (64, 300, 50, 2, False, False, 3)]:
-            env.set(MIGEMM_SMALL_SPLITK=splits)
+            env.set(small_splitk=splits)
             say("small 32x32", M, K, N, batch, bias, acc, splits, ta, tb)
             got, expect = run_exact(M, K, N, ta, tb, batch=batch, bias=bias, acc=acc,
                                     seed=M + K + N + ta + 2 * tb)

@@ -4,6 +4,7 @@ Each case prints what it runs before the GPU call, so a failure names its shape.
 Exactness: small-integer operands make every partial sum exactly representable, so the
 MFMA result must equal the reference arithmetic bit-for-bit; random operands are held to
 the 1e-5*sqrt(K) relative bar against fp64."""
+import ctypes
 import itertools
 import json
 import os
@@ -13,7 +14,7 @@ import pytest
 import torch
 
 import oracle
-from parity import check_gemm, dev, host, sample_rows
+from parity import Tuner, check_gemm, dev, host, sample_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -253,8 +254,9 @@ def test_skinny_rows_and_bias(nncl, policy, M):
 
 
 def test_graph_capture_replays_match_eager(nncl):
-    """Callers may capture the GEMMs in a HIP graph. Replays are interleaved with eager
-    work and synchronisations, and every replay is compared with the eager result."""
+    """Callers may capture the GEMMs in a HIP graph. The capturing stream's workspace is
+    sized by running the same calls on it first; replays are interleaved with eager work and
+    synchronisations, and every replay is compared with the eager result."""
     dev_ = torch.device("cuda:0")
     A = dev(oracle.normal((64, 1536), 21, 0))
     W = dev(oracle.uniform((1536, 4096), 21, 1, -1 / 32, 1 / 32))
@@ -266,9 +268,13 @@ def test_graph_capture_replays_match_eager(nncl):
     y2 = torch.empty(1, 11008, device=dev_)
     eager1 = host(nncl.gemm(A, W, bias=bias)).copy()
     eager2 = host(nncl.gemm(x, Bv)).copy()
+    cap = torch.cuda.Stream()
+    with torch.cuda.stream(cap):  # sizes the capturing stream's own workspace
+        nncl.gemm(A, W, bias=bias, out=y1)
+        nncl.gemm(x, Bv, out=y2)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=cap):
         nncl.gemm(A, W, bias=bias, out=y1)
         nncl.gemm(x, Bv, out=y2)
     for i in range(3):
@@ -281,6 +287,103 @@ def test_graph_capture_replays_match_eager(nncl):
         assert np.array_equal(host(y1), eager1), f"replay {i}: gate GEMM differs"
         assert np.array_equal(host(y2), eager2), f"replay {i}: GEMV differs"
         del noise
+
+
+def test_graph_capture_needs_its_own_workspace(nncl):
+    """A split-K GEMM captured on a stream whose workspace was never sized fails with
+    MIGEMM_ERR_WORKSPACE (it does not borrow another stream's buffer); after
+    migemm_workspace_reserve on that stream the same capture succeeds."""
+    from my_pytchon_opencl_lib_amd import _native
+    W = dev(small_ints((8192, 1536), 91, -2, 2))
+    X = dev(small_ints((64, 8192), 92, -2, 2))
+    Y = torch.empty(64, 1536, device="cuda:0")
+    nncl.gemm(X, W, out=Y)  # sizes the default stream's workspace only
+    torch.cuda.synchronize()
+    say("graph capture without a sized workspace")
+    cap = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(_native.MigemmRuntimeError, match="WORKSPACE"):
+        with torch.cuda.graph(g, stream=cap):
+            nncl.gemm(X, W, out=Y)
+    torch.cuda.synchronize()
+    _native.call("migemm_workspace_reserve", ctypes.c_void_p(cap.cuda_stream), 64 << 20)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap):
+        nncl.gemm(X, W, out=Y)
+    Y.fill_(float("nan"))
+    g.replay()
+    expect = (host(X).astype(np.float64) @ host(W).astype(np.float64)).astype(np.float32)
+    assert np.array_equal(host(Y), expect)
+
+
+def test_graph_replay_overlaps_eager_split_k(nncl):
+    """A graph replay on one stream runs at the same time as eager split-K GEMMs of the
+    same shape on another stream, with no synchronisation between the two: each stream has
+    its own partial sums, so both results are exact."""
+    say("graph replay overlapping eager split-K on another stream")
+    W = dev(small_ints((8192, 1536), 93, -2, 2))
+    xs = [dev(small_ints((64, 8192), 94 + i, -2, 2)) for i in range(4)]
+    expect = [(host(x).astype(np.float64) @ host(W).astype(np.float64)).astype(np.float32)
+              for x in xs]
+    cap, other = torch.cuda.Stream(), torch.cuda.Stream()
+    y_graph = torch.empty(64, 1536, device="cuda:0")
+    with torch.cuda.stream(cap):
+        nncl.gemm(xs[0], W, out=y_graph)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap):
+        for _ in range(8):
+            nncl.gemm(xs[0], W, out=y_graph)
+    ys = [torch.empty(64, 1536, device="cuda:0") for _ in range(3)]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        y_graph.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(cap):
+            g.replay()
+        with torch.cuda.stream(other):
+            for i in range(3):
+                for _ in range(4):
+                    nncl.gemm(xs[1 + i], W, out=ys[i])
+        torch.cuda.synchronize()
+        assert np.array_equal(host(y_graph), expect[0]), f"replay {rep} differs"
+        for i in range(3):
+            assert np.array_equal(host(ys[i]), expect[1 + i]), f"eager {rep}/{i} differs"
+
+
+def test_stream_destroy_frees_its_workspace(nncl):
+    """migemm_stream_destroy waits for the stream's work and frees the workspace the
+    library held for it; migemm_workspace_release does the same for a caller's stream."""
+    from my_pytchon_opencl_lib_amd import _native
+    L = _native.load()
+    W = dev(small_ints((8192, 1536), 95, -2, 2))
+    X = dev(small_ints((64, 8192), 96, -2, 2))
+    Y = torch.empty(64, 1536, device="cuda:0")
+    expect = (host(X).astype(np.float64) @ host(W).astype(np.float64)).astype(np.float32)
+    torch.cuda.synchronize()
+    for release in (False, True):
+        s = ctypes.c_void_p()
+        _native.call("migemm_stream_create", ctypes.byref(s))
+        say("workspace freed with the stream" if not release else "workspace release")
+        _native.call("migemm_gemm_strided_batched", s, 0, 0, 64, 1536, 8192,
+                     ctypes.c_void_p(X.data_ptr()), 8192, 0, ctypes.c_void_p(W.data_ptr()),
+                     1536, 0, None, ctypes.c_void_p(Y.data_ptr()), 1536, 0, 1)
+        assert "splits=" in _native.last_plan() and "splits=1 " not in _native.last_plan()
+        size = ctypes.c_size_t(0)
+        _native.call("migemm_workspace_size", s, ctypes.byref(size))
+        assert size.value >= 64 * 1536 * 4 * 2
+        if release:
+            _native.call("migemm_workspace_release", s)
+            _native.call("migemm_workspace_size", s, ctypes.byref(size))
+            assert size.value == 0
+            assert np.array_equal(host(Y), expect)
+            _native.call("migemm_stream_destroy", s)
+        else:
+            _native.call("migemm_stream_destroy", s)
+            _native.call("migemm_workspace_size", s, ctypes.byref(size))
+            assert size.value == 0
+            assert np.array_equal(host(Y), expect)
+        assert L.migemm_last_error() == b""
 
 
 def test_split_k_on_two_streams_concurrently(nncl):
@@ -347,17 +450,14 @@ def test_unaligned_bases_and_leading_dims(nncl, policy, ta, tb):
 
 @pytest.fixture
 def forced_tile(request):
-    """Forces one macro-tile of the tiled kernel (the library's per-call MIGEMM_TILE tuning
-    override) under the TILED policy, restoring both afterwards."""
+    """Forces one macro-tile of the tiled kernel (the library's tile tuning override) under
+    the TILED policy, restoring both afterwards."""
     from my_pytchon_opencl_lib_amd import _native
-    prev_env = os.environ.get("MIGEMM_TILE")
+    tuner = Tuner()
     prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_TILED)
-    os.environ["MIGEMM_TILE"] = request.param
+    tuner.set(tile=request.param)
     yield request.param
-    if prev_env is None:
-        os.environ.pop("MIGEMM_TILE", None)
-    else:
-        os.environ["MIGEMM_TILE"] = prev_env
+    tuner.restore()
     _native.set_gemm_policy(prev)
 
 

@@ -13,13 +13,12 @@ epilogue. Small-integer operands make the exact answer known, so results must be
 The three pools take ~29 GB of device memory and are freed at the end.
 """
 import ctypes
-import os
 
 import numpy as np
 import pytest
 import torch
 
-from parity import dev, host
+from parity import Tuner, dev, host
 
 pytestmark = pytest.mark.gpu
 
@@ -46,22 +45,16 @@ def pools():
 def policy():
     from my_pytchon_opencl_lib_amd import _native
     prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_AUTO)
-    saved = {k: os.environ.get(k) for k in ("MIGEMM_DIRECT", "MIGEMM_SPLITK", "MIGEMM_TILE")}
+    tuner = Tuner()
 
-    def use(name, **env):
+    def use(name, **tune):
         _native.set_gemm_policy(getattr(_native, "MIGEMM_POLICY_" + name))
-        for k in saved:
-            os.environ.pop(k, None)
-        for k, v in env.items():
-            os.environ[k] = str(v)
+        tuner.set(tile=None, splitk=None, direct=None)
+        tuner.set(**tune)
 
     yield use
     _native.set_gemm_policy(prev)
-    for k, v in saved.items():
-        if v is None:
-            os.environ.pop(k, None)
-        else:
-            os.environ[k] = v
+    tuner.restore()
 
 
 def place(pool, X, stride, ld):
@@ -109,11 +102,11 @@ def run(pools, ta, tb, M, K, N, batch, sA, sB, sC, lda, ldb, ldc, bias=False, ac
 
 
 LAYOUTS = [(0, 0), (0, 1), (1, 0), (1, 1)]
-# Kernel families, each forced: the direct kernel in 64x64 and 256x256 tiles (MIGEMM_TILE; the
+# Kernel families, each forced: the direct kernel in 64x64 and 256x256 tiles (tuning key tile; the
 # dispatcher would take 32x32 tiles at these sizes), the register-staged kernel in 128x128
 # tiles and the small-output kernel.
-FAMILIES = [("TILED", {"MIGEMM_TILE": 64}), ("TILED", {"MIGEMM_TILE": 256}),
-            ("TILED", {"MIGEMM_TILE": 128, "MIGEMM_DIRECT": 0}), ("SMALL", {})]
+FAMILIES = [("TILED", {"tile": 64}), ("TILED", {"tile": 256}),
+            ("TILED", {"tile": 128, "direct": 1}), ("SMALL", {})]
 
 
 @pytest.mark.parametrize("fam", range(len(FAMILIES)))
@@ -136,7 +129,7 @@ def test_batch_entries_beyond_2_31(pools, policy, fam, ta, tb):
 def test_split_ranges_beyond_2_31(pools, policy, tile, ta, tb):
     """Split-K partial sums reduced into batch entries 2^31 + 1024 floats apart, C += result
     (direct loads into LDS, also for 128x128 ranges)."""
-    policy("TILED", MIGEMM_SPLITK=3, MIGEMM_TILE=tile, MIGEMM_DIRECT=2)
+    policy("TILED", splitk=3, tile=tile, direct=2)
     M, K, N = 260, 1036, 300
     lda = M if ta else K
     ldb = K if tb else N
