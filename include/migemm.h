@@ -90,6 +90,26 @@ int migemm_gemm_strided_batched_ex(void *stream, int transA, int transB,
                                    float *C, int64_t ldc, int64_t strideC,
                                    int batch, int flags);
 
+/* The same as migemm_gemm_strided_batched_ex, allocating nothing: no hipMalloc, hipFree or
+ * allocating library routine, on any call. It has no counterpart in the reference; it is
+ * for callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation). The kernels and results are those of
+ * migemm_gemm_strided_batched_ex; the partial sums that split-K GEMMs and sliced GEMVs keep
+ * go to a static device array of MIGEMM_NOALLOC_SCRATCH_BYTES that each GPU the library
+ * runs on holds until the process ends, instead of the stream's workspace. A call whose
+ * partial sums exceed it fails with MIGEMM_ERR_WORKSPACE before any launch (e.g. 8 k ranges
+ * of a 2048 x 2048 output; every BASELINE shape needs at most 0.7 MB). All calls on one GPU
+ * share that array: calls that overlap in time on one GPU (two streams, two threads) race
+ * on it, so callers order them (one stream, or events). */
+#define MIGEMM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int migemm_gemm_strided_batched_noalloc(void *stream, int transA, int transB,
+                                        int M, int N, int K,
+                                        const float *A, int64_t lda, int64_t strideA,
+                                        const float *B, int64_t ldb, int64_t strideB,
+                                        const float *bias,
+                                        float *C, int64_t ldc, int64_t strideC,
+                                        int batch, int flags);
+
 /* ------------------------------------------------------------------------------- */
 /* (2) Reference-shaped entry points: same argument lists and meaning as the OpenCL
  *     kernels (plus the stream, and the batch count that the reference passes as the

@@ -80,6 +80,9 @@ SIGNATURES = {
     "migemm_gemm_strided_batched_ex": ([_vp, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64,
                                         _vp, _i64, _i64, _vp, _vp, _i64, _i64, _i32, _i32],
                                        _i32),
+    "migemm_gemm_strided_batched_noalloc": ([_vp, _i32, _i32, _i32, _i32, _i32, _vp, _i64,
+                                             _i64, _vp, _i64, _i64, _vp, _vp, _i64, _i64,
+                                             _i32, _i32], _i32),
     "migemm_matmul_tiled": ([_vp, _vp, _vp, _vp, _i32, _i32, _i32], _i32),
     "migemm_bmm_tiled": ([_vp, _vp, _vp, _vp] + [_i32] * 7, _i32),
     "migemm_bmm_permute_tiled": ([_vp, _vp, _vp, _vp] + [_i32] * 9, _i32),

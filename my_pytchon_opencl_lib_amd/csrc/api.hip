@@ -142,8 +142,9 @@ float *partial_buffer(hipStream_t stream, const GemmDesc &d, size_t bytes, int *
     if (d.scratch == nullptr) return static_cast<float *>(workspace(stream, bytes, status, 0));
     if (bytes > d.scratch_bytes) {
         *status = set_error(MIGEMM_ERR_WORKSPACE,
-                            "this GEMM keeps %zu bytes of partial sums but the scratch it was "
-                            "given holds %zu", bytes, d.scratch_bytes);
+                            "this GEMM keeps %zu bytes of partial sums but the no-allocation "
+                            "entry point's static scratch holds %zu "
+                            "(MIGEMM_NOALLOC_SCRATCH_BYTES)", bytes, d.scratch_bytes);
         return nullptr;
     }
     *status = MIGEMM_OK;
@@ -163,6 +164,41 @@ static int release_workspace(hipStream_t stream) {
         g_ws.erase(it);
         if (!w.captured) MIGEMM_HIP(hipFree(w.ptr));
     }
+    return MIGEMM_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// Scratch of the no-allocation GEMM (migemm_gemm_strided_batched_noalloc): partial sums of
+// split GEMMs in a static device array instead of the stream's workspace, so that entry
+// point never allocates. Each GPU the library runs on holds its own copy until the process
+// ends. In host code the array's name is only a stand-in symbol, never a device address:
+// each device's address of it is looked up once, with that device current, and only that
+// pointer is passed to kernels.
+static __device__ __align__(256) float scratch[MIGEMM_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+static std::atomic<float *> g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mutex;
+
+// Device address of `scratch` on the current device (looked up on the first call there).
+static int scratch_address(float **out) {
+    int dev = 0;
+    MIGEMM_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices)
+        return set_error(MIGEMM_ERR_UNSUPPORTED, "device %d: the no-allocation entry point "
+                         "supports devices 0..%d", dev, kMaxDevices - 1);
+    float *p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lock(g_scratch_mutex);
+        p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (p == nullptr) {
+            void *addr = nullptr;
+            MIGEMM_HIP(hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)));
+            p = static_cast<float *>(addr);
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
     return MIGEMM_OK;
 }
 
@@ -300,6 +336,25 @@ int migemm_gemm_strided_batched_ex(void *stream, int transA, int transB, int M, 
                            ldc, strideC, batch, &d);
     if (rc != MIGEMM_OK) return rc;
     d.accumulate = (flags & MIGEMM_GEMM_ACCUMULATE) != 0;
+    return run_gemm(static_cast<hipStream_t>(stream), d);
+}
+
+int migemm_gemm_strided_batched_noalloc(void *stream, int transA, int transB, int M, int N,
+                                        int K, const float *A, int64_t lda, int64_t strideA,
+                                        const float *B, int64_t ldb, int64_t strideB,
+                                        const float *bias, float *C, int64_t ldc,
+                                        int64_t strideC, int batch, int flags) {
+    clear_error();
+    if ((flags & ~MIGEMM_GEMM_ACCUMULATE) != 0)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "gemm_noalloc: unknown flags 0x%x", flags);
+    GemmDesc d;
+    int rc = validate_gemm(transA, transB, M, N, K, A, lda, strideA, B, ldb, strideB, bias, C,
+                           ldc, strideC, batch, &d);
+    if (rc != MIGEMM_OK) return rc;
+    d.accumulate = (flags & MIGEMM_GEMM_ACCUMULATE) != 0;
+    rc = scratch_address(&d.scratch);
+    if (rc != MIGEMM_OK) return rc;
+    d.scratch_bytes = MIGEMM_NOALLOC_SCRATCH_BYTES;
     return run_gemm(static_cast<hipStream_t>(stream), d);
 }
 
