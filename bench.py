@@ -7,14 +7,29 @@ One step = the three GEMMs of BASELINE config 4 on synthetic N(0, 1/64) data res
   TN  dB = A^T * dC    (autograd gradient of B)
 each M = N = K = 4096, 2*4096^3 FLOP. `value` is the whole step's FLOP / wall time.
 
-Prints ONE JSON line on stdout. Extra per-configuration measurements (--configs all) go to
-stderr. The CPU baseline is the oracle's restatement of the reference matmul_tiled arithmetic
-(oracle/oracle.c, kind "port") timed on the host cores on a bounded row sample.
+Prints ONE JSON line on stdout. Besides the step it carries, by default:
+  configs            every other BASELINE config timed on this GPU (HIP events around HIP-graph
+                     replays of back-to-back calls), with its roofline fraction and the launch
+                     floor (a one-element fill kernel replayed the same way);
+  roofline           the dominant 4096^3 kernel, from HIP events in this run (frac) and from
+                     the committed rocprofv3 kernel trace of this bench (frac_profiled);
+  cpu_baseline       the oracle's restatement of the reference matmul_tiled arithmetic
+                     (oracle/oracle.c, kind "port") on the host cores, a bounded row sample;
+  reference_same_gpu the reference's own matmul.cl bmm_tiled, compiled from its source into
+                     oracle/_ref, run through ROCm OpenCL on this GPU (there is no CPU OpenCL
+                     device, PoCL, on the box).
+The extra legs run after the timed region.
+
+Profiling helpers: --pmc-target runs one workload for rocprofv3 --pmc passes, and
+--summarize-trace summarises a rocprofv3 --kernel-trace CSV of this bench (the committed
+profiles/*.md summaries are made with them).
 """
 import argparse
-import ctypes
+import csv
+import glob
 import json
 import os
+import re
 import sys
 import time
 
@@ -25,6 +40,24 @@ sys.path.insert(0, ROOT)
 
 PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense FP32 matrix peak (AMD public specification)
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+N4096 = 4096
+FLOP_4096 = 2.0 * N4096 ** 3
+TRACE_SUMMARY = os.path.join(ROOT, "profiles", "gemm_direct_4096_kernel_trace.md")
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemm_direct_4096_pmc.md")
+# GPU box: one GPU's share of the host is 16 threads (OMP_NUM_THREADS there)
+CPU_SHARE = 16
+
+# BASELINE configs other than the step: algorithmic FLOP and bytes per call (a broadcast
+# operand counted once, bias bytes included, bias adds not counted as FLOP)
+CONFIGS = {
+    "1_nn_256": (2 * 256 ** 3, 4 * 3 * 256 * 256, "mfma"),
+    "2a_bmm_qk": (2 * 32 * 128 * 128 * 64, 4 * 32 * (128 * 64 * 2 + 128 * 128), "hbm"),
+    "2b_bmm_pv": (2 * 32 * 128 * 128 * 64, 4 * 32 * (128 * 128 + 128 * 64 * 2), "hbm"),
+    "3_lstm_gate_step": (2 * 64 * 1536 * 4096,
+                         4 * (64 * 1536 + 1536 * 4096 + 64 * 4096 + 4096), "mfma"),
+    "5a_ragged": (2 * 1000 * 3000 * 777, 4 * (1000 * 777 + 777 * 3000 + 1000 * 3000), "mfma"),
+    "5b_gemv": (2 * 4096 * 11008, 4 * (4096 + 4096 * 11008 + 11008), "hbm"),
+}
 
 
 def parse():
@@ -32,26 +65,49 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--configs", default="main", choices=["main", "all"],
-                   help="'all' also measures every BASELINE config (reported on stderr)")
+    p.add_argument("--configs", default="all", choices=["main", "all"],
+                   help="'all' (default) also times every other BASELINE config")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="target duration of the bounded CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--pmc-target", nargs="?", const="4096", choices=["4096", "5a", "3"],
-                   help="run only a profiling target for rocprofv3 --pmc passes: '4096' (the "
-                        "default) the three 4096^3 forms 3x each, '5a' config 5a (1000x777x3000 "
-                        "NN) 3x, '3' the config-3 gate GEMM (64x1536x4096 + bias) over 3 "
-                        "timestep inputs; then a 256 MiB device copy 3x (the reference for "
-                        "scaling FETCH_SIZE / WRITE_SIZE to bytes)")
+    p.add_argument("--no-reference", action="store_true",
+                   help="skip the reference bmm_tiled run on this GPU")
+    p.add_argument("--pmc-target", nargs="?", const="4096",
+                   choices=["4096", "1", "2a", "2b", "3", "5a", "5b", "floor"],
+                   help="run only one workload for rocprofv3 --pmc passes, each 3 times: '4096' "
+                        "the three 4096^3 forms, '1' / '2a' / '2b' / '3' / '5a' / '5b' that "
+                        "BASELINE config, 'floor' the one-element fill kernel; then a 256 MiB "
+                        "device copy 3 times (the reference for scaling FETCH_SIZE / "
+                        "WRITE_SIZE to bytes)")
+    p.add_argument("--summarize-trace", metavar="DIR",
+                   help="summarise the rocprofv3 --kernel-trace CSV under DIR, made from "
+                        "'bench.py --steps S --warmup W' (pass the same --steps / --warmup)")
     return p.parse_args()
+
+
+def host_cpu():
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {"nproc": os.cpu_count() or 1, "usable": usable, "model": model}
 
 
 def cpu_baseline(target_s):
     """Oracle restatement of matmul_tiled (fp32 fma chains, ascending k) on host cores, on
     a growing row sample of the 4096^3 NN GEMM until ~target_s of CPU work."""
     import oracle
-    n = 4096
-    threads = min(16, os.cpu_count() or 1)
+    n = N4096
+    cpu = host_cpu()
+    threads = max(1, min(CPU_SHARE, cpu["usable"]))
     A = oracle.uniform((n, n), 3, 0)
     B = oracle.uniform((n, n), 3, 1)
     rows = max(threads, 16)
@@ -79,7 +135,35 @@ def cpu_baseline(target_s):
             "sample": f"{reps} x rows 0..{rows} of the 4096^3 NN GEMM ({flop / 1e9:.1f} GFLOP) "
                       f"with the oracle's matmul_tiled restatement (fp32 fma chains, ascending "
                       f"k; i-k-j order, AVX2), {threads} threads, {elapsed:.1f} s",
+            "host": {"nproc": cpu["nproc"], "usable_cpus": cpu["usable"],
+                     "cpu_model": cpu["model"],
+                     "threads_rule": f"min({CPU_SHARE}, usable CPUs): {CPU_SHARE} is one GPU's "
+                                     f"share of the GPU box's host (its OMP_NUM_THREADS)"},
             "openmp": bool(oracle.lib().oracle_openmp_enabled())}
+
+
+def reference_same_gpu(step_ms_nn):
+    """The reference kernel bmm_tiled (cl_kernels/matmul.cl:78-135) at 4096^3 on this GPU:
+    compiled from the reference source into oracle/_ref, launched with the reference host's
+    geometry (NnClGlob.cs:472-478) through ROCm OpenCL by oracle/ref_runner."""
+    try:
+        import oracle
+        from oracle import reference_gpu as ref
+        if not ref.available():
+            return {"available": False, "reason": "oracle/_ref was not built"}
+        A = oracle.uniform((N4096, N4096), 3, 0)
+        B = oracle.uniform((N4096, N4096), 3, 1)
+        _, info = ref.run("bmm_tiled", A, B, M=N4096, K=N4096, N=N4096, batch=1, reps=3)
+    except Exception as e:  # noqa: BLE001 -- reported, never fatal to the bench line
+        return {"available": False, "reason": f"{type(e).__name__}: {e}"}
+    ms = info["median_us"] / 1e3
+    tf = FLOP_4096 / (ms * 1e-3) / 1e12
+    return {"kernel": "bmm_tiled (cl_kernels/matmul.cl:78-135), reference source compiled "
+                      "for gfx950, ROCm OpenCL, 16x16 work-groups (NnClGlob.cs:472-478)",
+            "device": info["device"], "workload": "4096x4096x4096 NN, one launch",
+            "median_ms": round(ms, 3), "tflops": round(tf, 2),
+            "pct_of_fp32_matrix_peak": round(100 * tf / PEAK_FP32_MFMA_TFLOPS, 2),
+            "this_build_speedup": round(ms / step_ms_nn, 2), "reps": info["reps"]}
 
 
 class Timer:
@@ -104,6 +188,9 @@ class Timer:
 
 def main():
     args = parse()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace, args.steps, args.warmup)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: every GPU box here has one "
                                    "MI355X, and the matmul path shards without collectives "
@@ -119,8 +206,7 @@ def main():
         return
     nncl = NnClGlob("cuda:0")
     dev = torch.device("cuda:0")
-    n = 4096
-    flop = 2.0 * n * n * n
+    n = N4096
     gen = torch.Generator(device=dev)
     gen.manual_seed(3)
     std = 1.0 / 64.0
@@ -136,6 +222,10 @@ def main():
         "NT": lambda: nncl.gemm(dC, B, transB=True, out=dA),
         "TN": lambda: nncl.gemm(A, dC, transA=True, out=dB),
     }
+    plans = {}
+    for k, f in forms.items():
+        f()
+        plans[k] = _native.last_plan()
     timers = {k: Timer(torch) for k in forms}
 
     for _ in range(args.warmup):
@@ -154,20 +244,33 @@ def main():
     per_form = {}
     for k, t in timers.items():
         ms = t.mean_ms()
-        per_form[k] = {"ms": round(ms, 4), "tflops": round(flop / (ms * 1e-3) / 1e12, 2)}
+        per_form[k] = {"ms": round(ms, 4), "tflops": round(FLOP_4096 / (ms * 1e-3) / 1e12, 2),
+                       "kernel": plans[k]}
     dominant = max(per_form, key=lambda k: per_form[k]["ms"])
     dom_ms = per_form[dominant]["ms"]
-    achieved = flop / (dom_ms * 1e-3) / 1e12
-    value = 3 * flop / (ms_per_step * 1e-3) / 1e12
+    achieved = FLOP_4096 / (dom_ms * 1e-3) / 1e12
+    value = 3 * FLOP_4096 / (ms_per_step * 1e-3) / 1e12
 
-    extra = {}
-    if args.configs == "all":
-        extra = measure_all_configs(torch, nncl, _native)
-        print(json.dumps({"configs": extra}, indent=1), file=sys.stderr, flush=True)
+    configs = measure_all_configs(torch, nncl, _native) if args.configs == "all" else None
+    ref = None if args.no_reference else reference_same_gpu(per_form["NN"]["ms"])
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
 
-    cpu = None
-    if not args.no_cpu_baseline:
-        cpu = cpu_baseline(args.cpu_seconds)
+    prof = load_profiled()
+    roofline = {"bound": "mfma", "kernel": f"gemm_direct_kernel ({dominant} form, 256x256 tiles)",
+                "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+                "traffic": load_traffic(dominant),
+                "algorithmic_per_launch": {"flop": FLOP_4096, "bytes": 4 * 3 * n * n},
+                "measured_by": "HIP events around each launch on the launch stream, this run"}
+    if dominant in prof:
+        pus = prof[dominant]
+        roofline["profiled_us"] = pus
+        roofline["frac_profiled"] = round(FLOP_4096 / (pus * 1e-6) / 1e12 /
+                                          PEAK_FP32_MFMA_TFLOPS, 4)
+        roofline["profile"] = "profiles/gemm_direct_4096_kernel_trace.md (timed launches " \
+                              "under rocprofv3 --kernel-trace)"
+    roofline["traffic_source"] = "profiles/gemm_direct_4096_pmc.md (rocprofv3 --pmc " \
+                                 "FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)"
 
     line = {
         "metric": "fp32 GEMM/BMM TFLOP/s and % of MI355X FP32 matrix peak at 4096^3",
@@ -181,95 +284,167 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: A, B, dC ~ N(0, 1/64) fp32 in HBM (torch generator, seed 3)",
+        "data": "synthetic: A, B, dC ~ N(0, 1/64) fp32 in HBM (torch generator, seed 3); "
+                "other configs U[-1,1) / N(0,1) of their BASELINE shapes",
         "config": {"workload": "BASELINE config 4: fp32 4096x4096x4096 NN forward + NT "
                                "(dA = dC*B^T) + TN (dB = A^T*dC), one step = all three",
                    "M": n, "N": n, "K": n, "forms": per_form,
                    "pct_of_fp32_matrix_peak": round(100 * value / PEAK_FP32_MFMA_TFLOPS, 2),
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": f"{tiled_kernel_name()} ({dominant} form)",
-                     "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
-                     "traffic": load_traffic(dominant)},
+        "roofline": roofline,
+        "configs": configs,
+        "reference_same_gpu": ref,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 
 
 def pmc_target(torch, nncl, which="4096"):
+    """One workload, 3 launches, for rocprofv3 --pmc passes; then the copy reference."""
     g = torch.Generator(device="cuda:0")
-    if which == "3":
-        g.manual_seed(2)
-        X = torch.randn(3, 64, 1536, device="cuda:0", generator=g)
-        W = (torch.rand(1536, 4096, device="cuda:0", generator=g) * 2 - 1) / 32
-        bias = (torch.rand(4096, device="cuda:0", generator=g) * 2 - 1) / 32
-        Y = torch.empty(64, 4096, device="cuda:0")
-        for i in range(3):
-            nncl.gemm(X[i], W, bias=bias, out=Y)
+    g.manual_seed(0)
+    dev = torch.device("cuda:0")
+    r = lambda *s: torch.rand(*s, device=dev, generator=g) * 2 - 1
+    if which == "1":
+        A, B, C = r(256, 256), r(256, 256), torch.empty(256, 256, device=dev)
+        calls = [lambda: nncl.gemm(A, B, out=C)] * 3
+    elif which in ("2a", "2b"):
+        if which == "2a":
+            X, Y, Z = r(32, 128, 64), r(32, 64, 128), torch.empty(32, 128, 128, device=dev)
+        else:
+            X, Y, Z = r(32, 128, 128), r(32, 128, 64), torch.empty(32, 128, 64, device=dev)
+        calls = [lambda: nncl.gemm(X, Y, out=Z)] * 3
+    elif which == "3":
+        X = torch.randn(3, 64, 1536, device=dev, generator=g)
+        W = r(1536, 4096) / 32
+        bias = r(4096) / 32
+        Y = torch.empty(64, 4096, device=dev)
+        calls = [lambda i=i: nncl.gemm(X[i], W, bias=bias, out=Y) for i in range(3)]
     elif which == "5a":
-        g.manual_seed(4)
-        A = torch.rand(1000, 777, device="cuda:0", generator=g) * 2 - 1
-        B = torch.rand(777, 3000, device="cuda:0", generator=g) * 2 - 1
-        C = torch.empty(1000, 3000, device="cuda:0")
-        for _ in range(3):
-            nncl.gemm(A, B, out=C)
+        A, B, C = r(1000, 777), r(777, 3000), torch.empty(1000, 3000, device=dev)
+        calls = [lambda: nncl.gemm(A, B, out=C)] * 3
+    elif which == "5b":
+        x = r(1, 4096)
+        copies = [r(4096, 11008) for _ in range(3)]
+        y = torch.empty(1, 11008, device=dev)
+        calls = [lambda c=c: nncl.gemm(x, c, out=y) for c in copies]
+    elif which == "floor":
+        z = torch.empty(1, device=dev)
+        calls = [lambda: z.fill_(1.0)] * 3
     else:
-        n = 4096
-        g.manual_seed(3)
-        A = torch.randn(n, n, device="cuda:0", generator=g) / 64
-        B = torch.randn(n, n, device="cuda:0", generator=g) / 64
-        C = torch.empty(n, n, device="cuda:0")
-        for _ in range(3):
-            nncl.gemm(A, B, out=C)
-            nncl.gemm(A, B, transB=True, out=C)
-            nncl.gemm(A, B, transA=True, out=C)
-    src = torch.ones(64 * 1024 * 1024, device="cuda:0")
+        n = N4096
+        A = torch.randn(n, n, device=dev, generator=g) / 64
+        B = torch.randn(n, n, device=dev, generator=g) / 64
+        C = torch.empty(n, n, device=dev)
+        calls = [lambda: nncl.gemm(A, B, out=C), lambda: nncl.gemm(A, B, transB=True, out=C),
+                 lambda: nncl.gemm(A, B, transA=True, out=C)] * 3
+    torch.cuda.synchronize()
+    for f in calls:
+        f()
+    src = torch.ones(64 * 1024 * 1024, device=dev)
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print("pmc target done", flush=True)
+    print(f"pmc target {which} done", flush=True)
 
 
-def tiled_kernel_name():
-    """The kernel that runs the 4096^3 forms: 256x256 tiles with operands loaded straight
-    into LDS."""
-    return "gemm_direct_kernel"
-
-
-def load_traffic(kernel_substr):
+def load_traffic(form):
     """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, each
-    scaled by the copy-kernel factor) for the dominant kernel, from the committed profile
-    summary; None when no summary covers that kernel."""
-    name = "gemm_mfma_4096_pmc.md" if tiled_kernel_name() == "gemm_mfma_kernel" else \
-        "gemm_direct_4096_pmc.md"
-    path = os.path.join(ROOT, "profiles", name)
-    if not os.path.exists(path):
+    scaled by the copy-kernel factor) for the dominant form, from the committed profile
+    summary; None when no summary covers it."""
+    if not os.path.exists(PMC_SUMMARY):
         return None
-    for line in open(path):
+    for line in open(PMC_SUMMARY):
         if line.startswith("TRAFFIC_BYTES_PER_LAUNCH"):
-            _, form, nbytes = line.split()[:3]
-            if form == kernel_substr:
+            _, f, nbytes = line.split()[:3]
+            if f == form:
                 return int(nbytes)
     return None
 
 
+def load_profiled():
+    """Timed-launch average duration (us) of each 4096^3 form under rocprofv3, from the
+    committed kernel-trace summary of this bench."""
+    out = {}
+    if os.path.exists(TRACE_SUMMARY):
+        for line in open(TRACE_SUMMARY):
+            if line.startswith("PROFILED_US"):
+                _, f, us = line.split()[:3]
+                out[f] = float(us)
+    return out
+
+
+FORM_OF = {("true", "false"): "NN", ("true", "true"): "NT", ("false", "false"): "TN",
+           ("false", "true"): "TT"}
+
+
+def summarize_trace(directory, steps, warmup):
+    """Markdown summary of a rocprofv3 --kernel-trace CSV of 'bench.py --steps S --warmup W':
+    per kernel (name shortened to its template) launches and average duration, and for the
+    three 4096^3 forms the average over exactly the bench's timed launches (each form runs
+    once untimed to record its plan, W warm-up times, then S timed times)."""
+    paths = glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True)
+    if not paths:
+        sys.exit(f"no *kernel_trace.csv under {directory}")
+    rows = []
+    for p in paths:
+        with open(p) as f:
+            rows += list(csv.DictReader(f))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    by_kernel = {}
+    forms = {}
+    for r in rows:
+        name = r["Kernel_Name"]
+        short = re.sub(r"\(.*", "", name.replace("(anonymous namespace)", "{anon}"))
+        short = short.replace("void ", "")
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        by_kernel.setdefault(short, []).append(us)
+        m = re.search(r"gemm_direct_kernel<256, 256, \d+, \d+, (true|false), (true|false)", name)
+        if m:
+            forms.setdefault(FORM_OF[m.groups()], []).append(us)
+    print("| kernel | launches | average (us) | min (us) | max (us) |")
+    print("|---|---|---|---|---|")
+    for k, v in sorted(by_kernel.items(), key=lambda kv: -sum(kv[1])):
+        if len(k) > 140:
+            k = k[:137] + "..."
+        print(f"| `{k}` | {len(v)} | {np.mean(v):.2f} | {np.min(v):.2f} | {np.max(v):.2f} |")
+    print()
+    print("| form | timed launches | average (us) | TFLOP/s | fraction of 157.3 |")
+    print("|---|---|---|---|---|")
+    lines = []
+    for f in ("NN", "NT", "TN"):
+        v = forms.get(f, [])
+        timed = v[1 + warmup:1 + warmup + steps]
+        if not timed:
+            continue
+        us = float(np.mean(timed))
+        tf = FLOP_4096 / (us * 1e-6) / 1e12
+        print(f"| {f} | {len(timed)} | {us:.1f} | {tf:.2f} | {tf / PEAK_FP32_MFMA_TFLOPS:.4f} |")
+        lines.append(f"PROFILED_US {f} {us:.1f}")
+    print()
+    print("\n".join(lines))
+
+
 def measure_all_configs(torch, nncl, _native, reps=20):
     """Per-config device time per call, from HIP events around a HIP graph that replays
-    `reps` back-to-back calls (so host launch overhead is not measured). Inputs rotate
-    where the working set must exceed the 256 MB MALL."""
+    back-to-back calls (so host launch overhead is not measured), 5 replays averaged. Inputs
+    rotate where BASELINE repeats a config over many inputs (config 3: 100 timesteps) or the
+    working set must exceed the 256 MB MALL (config 5b: three copies of B). The launch floor
+    is a one-element fill kernel replayed the same way."""
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(0)
     out = {}
 
-    def timed(fns):
+    def timed(fns, per=None):
+        per = per or max(1, reps // len(fns))
         for f in fns:
             f()
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            for _ in range(reps // len(fns)):
+            for _ in range(per):
                 for f in fns:
                     f()
         graph.replay()
@@ -277,39 +452,51 @@ def measure_all_configs(torch, nncl, _native, reps=20):
         t = Timer(torch)
         for _ in range(5):
             t.around(graph.replay)
-        return t.mean_ms() / ((reps // len(fns)) * len(fns))
+        return t.mean_ms() / (per * len(fns))
 
-    def rec(name, ms, flop, byts):
-        out[name] = {"us": round(ms * 1e3, 2), "tflops": round(flop / (ms * 1e-3) / 1e12, 3),
-                     "pct_mfma_peak": round(100 * flop / (ms * 1e-3) / 1e12 /
-                                            PEAK_FP32_MFMA_TFLOPS, 2),
-                     "GBps": round(byts / (ms * 1e-3) / 1e9, 1),
-                     "pct_hbm_peak": round(100 * byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2)}
+    z = torch.empty(1, device=dev)
+    floor_us = timed([lambda: z.fill_(1.0)], per=100) * 1e3
+    out["launch_floor"] = {"us": round(floor_us, 2),
+                           "kernel": "torch fill of 1 element, graph-replayed back to back"}
+
+    def rec(name, ms, fns):
+        flop, byts, bound = CONFIGS[name]
+        tf = flop / (ms * 1e-3) / 1e12
+        gbs = byts / (ms * 1e-3) / 1e9
+        fns[0]()
+        out[name] = {"us": round(ms * 1e3, 2), "tflops": round(tf, 3),
+                     "pct_mfma_peak": round(100 * tf / PEAK_FP32_MFMA_TFLOPS, 2),
+                     "GBps": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
+                     "bound": bound,
+                     "frac": round((tf / PEAK_FP32_MFMA_TFLOPS) if bound == "mfma"
+                                   else (gbs / PEAK_HBM_GBS), 4),
+                     "x_launch_floor": round(ms * 1e3 / floor_us, 2),
+                     "kernel": _native.last_plan()}
 
     r = lambda *s: torch.rand(*s, device=dev, generator=g) * 2 - 1
     A, B, C = r(256, 256), r(256, 256), torch.empty(256, 256, device=dev)
-    rec("1_nn_256", timed([lambda: nncl.gemm(A, B, out=C)]), 2 * 256 ** 3, 4 * 3 * 256 * 256)
+    f1 = [lambda: nncl.gemm(A, B, out=C)]
+    rec("1_nn_256", timed(f1), f1)
     Q, Kt, P, V = r(32, 128, 64), r(32, 64, 128), r(32, 128, 128), r(32, 128, 64)
     S, O = torch.empty(32, 128, 128, device=dev), torch.empty(32, 128, 64, device=dev)
-    rec("2a_bmm_qk", timed([lambda: nncl.gemm(Q, Kt, out=S)]), 2 * 32 * 128 * 128 * 64,
-        4 * 32 * (128 * 64 * 2 + 128 * 128))
-    rec("2b_bmm_pv", timed([lambda: nncl.gemm(P, V, out=O)]), 2 * 32 * 128 * 128 * 64,
-        4 * 32 * (128 * 128 + 128 * 64 * 2))
-    X = r(20, 64, 1536)
+    f2a = [lambda: nncl.gemm(Q, Kt, out=S)]
+    rec("2a_bmm_qk", timed(f2a), f2a)
+    f2b = [lambda: nncl.gemm(P, V, out=O)]
+    rec("2b_bmm_pv", timed(f2b), f2b)
+    X = torch.randn(100, 64, 1536, device=dev, generator=g)
     W = r(1536, 4096) / 32
     bias = r(4096) / 32
     Y = torch.empty(64, 4096, device=dev)
-    rec("3_lstm_gate_step",
-        timed([lambda i=i: nncl.gemm(X[i], W, bias=bias, out=Y) for i in range(20)]),
-        2 * 64 * 1536 * 4096, 4 * (64 * 1536 + 1536 * 4096 + 64 * 4096 + 4096))
+    f3 = [lambda i=i: nncl.gemm(X[i], W, bias=bias, out=Y) for i in range(100)]
+    rec("3_lstm_gate_step", timed(f3, per=1), f3)
     A5, B5, C5 = r(1000, 777), r(777, 3000), torch.empty(1000, 3000, device=dev)
-    rec("5a_ragged", timed([lambda: nncl.gemm(A5, B5, out=C5)]), 2 * 1000 * 3000 * 777,
-        4 * (1000 * 777 + 777 * 3000 + 1000 * 3000))
+    f5a = [lambda: nncl.gemm(A5, B5, out=C5)]
+    rec("5a_ragged", timed(f5a), f5a)
     x = r(1, 4096)
     copies = [r(4096, 11008) for _ in range(3)]  # 541 MB > the 256 MB MALL
     y = torch.empty(1, 11008, device=dev)
-    rec("5b_gemv", timed([lambda c=c: nncl.gemm(x, c, out=y) for c in copies]),
-        2 * 4096 * 11008, 4 * (4096 + 4096 * 11008 + 11008))
+    f5b = [lambda c=c: nncl.gemm(x, c, out=y) for c in copies]
+    rec("5b_gemv", timed(f5b, per=7), f5b)
     return out
 
 

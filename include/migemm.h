@@ -51,7 +51,9 @@ enum {
     MIGEMM_ERR_HIP = 3,         /* a HIP runtime call failed (message in last error) */
     MIGEMM_ERR_NO_DEVICE = 4,   /* no usable gfx950 device                           */
     MIGEMM_ERR_WORKSPACE = 5,   /* internal workspace could not be allocated         */
-    MIGEMM_ERR_UNSUPPORTED = 6  /* valid request outside what this build implements  */
+    MIGEMM_ERR_UNSUPPORTED = 6, /* valid request outside what this build implements  */
+    MIGEMM_ERR_NO_QUEUE = 7     /* no queue registered on this thread (the reference's
+                                   InvalidOperationException, DeviceQueueRegistry.cs:30-36) */
 };
 
 /* ------------------------------------------------------------------------------- */
@@ -171,6 +173,18 @@ int migemm_lstm_gemm_grad_weights(void *stream, const float *X, const float *H_o
                                   float *grad_bias, int batch_size, int seq_len,
                                   int in_features, int hidden_size);
 
+/* The recurrent product of one timestep inside kernel lstm_recurrent_forward,
+ * cs/cl_kernels/lstm.cl:80-101 (enqueued by NnClGlob.Lstm, cs/compiler/NnClGlob.cs:912-928),
+ * as a GEMM over the whole batch, in place on the step's slice of XW:
+ *   XW[b, t, g] += sum_h H_out[b, t-1, h] * U[h, g]     for b < batch_size, g < 4*hidden
+ * XW [batch_size, seq_len, 4*hidden] (X*W + bias from lstm_gemm_xw), H_out
+ * [batch_size, seq_len, hidden], U [hidden, 4*hidden]. Afterwards XW[b, t, :] holds the
+ * step's raw gates, which the reference kernel stores in its workspace
+ * (workspace[(t*batch + b)*5H + g], lstm.cl:103-106) before applying the activations.
+ * At t == 0 the previous hidden state is zero (lstm.cl:57-60) and XW is left unchanged. */
+int migemm_lstm_recurrent_gates(void *stream, float *XW, const float *H_out, const float *U,
+                                int batch_size, int seq_len, int hidden_size, int t);
+
 /* Replaces kernel tensor_permute, cl_kernels/permute.cl:11-18, enqueued by
  * NnClGlob.Permute (cs/compiler/NnClGlob.cs:382-424) and nncl_glob.py:148-174.
  * dst = src.permute(axes); src_dims and axes are HOST int arrays of length num_dims
@@ -245,6 +259,55 @@ int migemm_workspace_size(void *stream, size_t *bytes);
 const char *migemm_last_error(void);
 /* Library version, e.g. "0.1.0". */
 const char *migemm_version(void);
+
+/* ------------------------------------------------------------------------------- */
+/* (3b) The reference host's runtime objects on HIP, for a host that keeps its object model:
+ *      a device context, the name-keyed buffer pool behind Tensor.DataBuffer and the
+ *      per-thread current queue. Buffers are HIP device memory, the pointers the compute
+ *      entry points take; queues are HIP streams (migemm_stream_create). */
+
+/* Replaces new ComputeContext(preferAccelerator: true) (cs/core/ComputeContext.cs:35-159):
+ * device -1 takes the first visible gfx950 device (the reference takes the first
+ * accelerator / GPU of the first platform, :53-96; these kernels are built for gfx950
+ * only), device >= 0 that device, which must be a gfx950. MIGEMM_ERR_NO_DEVICE when there
+ * is none (the reference's InvalidOperationException, :92-93). */
+int migemm_context_create(int device, void **ctx);
+/* Replaces ComputeContext.Dispose (:161-170): frees every pooled buffer of the context and
+ * clears this thread's current queue if it names the context. */
+int migemm_context_destroy(void *ctx);
+/* The device parameters ComputeContext exposes (:13-25, derived at :108-156): device index,
+ * architecture name, compute units, wavefront size (warp_size), MAX_WORK_GROUP_SIZE and the
+ * work-group shape MAX_WORK_GPOUP_SIZE_X / _Y the reference derives from them (Y = warp/8,
+ * X = MAX/Y), global memory. Any output pointer may be NULL. */
+int migemm_context_info(void *ctx, int *device, char *arch_name, size_t arch_name_len,
+                        int *compute_units, int *wavefront_size, int *max_work_group_size,
+                        int *work_group_x, int *work_group_y, size_t *global_mem_bytes);
+
+/* Replaces OpenCLBufferManager.GetOrCreateBuffer (cs/compiler/OpenCLBufferManager.cs:22-61):
+ * the device buffer called `name` if it belongs to `ctx` and holds >= bytes; otherwise the
+ * old one (if any) is freed -- after its device has finished the work queued so far, since
+ * kernels may still use it -- and a buffer of exactly `bytes` is allocated on the context's
+ * device. Errors as the reference's: null context, empty name, zero size (:24-26). */
+int migemm_buffer_get_or_create(void *ctx, const char *name, size_t bytes, void **ptr);
+/* Replaces OpenCLBufferManager.ReleaseBuffer (:66-75); an unknown name is not an error. */
+int migemm_buffer_release(const char *name);
+/* Replaces OpenCLBufferManager.DisposeAll (:81-91). */
+int migemm_buffer_release_all(void);
+/* Number of pooled buffers and their total size (either pointer may be NULL). */
+int migemm_buffer_count(size_t *count, size_t *total_bytes);
+
+/* Replaces DeviceQueueRegistry.RegisterCurrent (cs/core/DeviceQueueRegistry.cs:19-22): the
+ * calling thread's current queue is `stream` of `ctx`; a null stream is rejected (:21). */
+int migemm_queue_register_current(void *ctx, void *stream);
+/* Replaces DeviceQueueRegistry.GetCurrent (:28-38): MIGEMM_ERR_NO_QUEUE when this thread has
+ * registered none. Either output may be NULL. */
+int migemm_queue_get_current(void **ctx, void **stream);
+/* Replaces DeviceQueueRegistry.Clear (:43-46). */
+int migemm_queue_clear_current(void);
+/* Replaces the Tensor.DataBuffer getter (cs/core/Tensor.cs:41): the pooled buffer named
+ * tensor_id of the current queue's context (migemm_buffer_get_or_create), bytes =
+ * 4 * Size. MIGEMM_ERR_NO_QUEUE when this thread has registered no queue. */
+int migemm_tensor_buffer(const char *tensor_id, size_t bytes, void **ptr);
 
 /* ------------------------------------------------------------------------------- */
 /* (4) Kernel selection. The reference has one kernel per form (cl_kernels/matmul.cl:8,

@@ -18,6 +18,7 @@ MIGEMM_ERR_HIP = 3
 MIGEMM_ERR_NO_DEVICE = 4
 MIGEMM_ERR_WORKSPACE = 5
 MIGEMM_ERR_UNSUPPORTED = 6
+MIGEMM_ERR_NO_QUEUE = 7
 
 MIGEMM_GEMM_ACCUMULATE = 1  # migemm_gemm_strided_batched_ex flag: C += result
 
@@ -46,6 +47,7 @@ STATUS_NAMES = {
     MIGEMM_ERR_NO_DEVICE: "MIGEMM_ERR_NO_DEVICE",
     MIGEMM_ERR_WORKSPACE: "MIGEMM_ERR_WORKSPACE",
     MIGEMM_ERR_UNSUPPORTED: "MIGEMM_ERR_UNSUPPORTED",
+    MIGEMM_ERR_NO_QUEUE: "MIGEMM_ERR_NO_QUEUE",
 }
 
 
@@ -90,6 +92,7 @@ SIGNATURES = {
     "migemm_lstm_gemm_xw": ([_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32], _i32),
     "migemm_lstm_gemm_grad_x": ([_vp, _vp, _vp, _vp, _i32, _i32, _i32], _i32),
     "migemm_lstm_gemm_grad_weights": ([_vp] * 7 + [_i32] * 4, _i32),
+    "migemm_lstm_recurrent_gates": ([_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32], _i32),
     "migemm_tensor_permute": ([_vp, _vp, _vp, _ip, _ip, _i32], _i32),
     "migemm_linear_bias_backward": ([_vp, _vp, _vp, _i32, _i32], _i32),
     "migemm_reduce_sum_axis": ([_vp, _vp, _vp, _i32, _i32, _i32], _i32),
@@ -110,6 +113,18 @@ SIGNATURES = {
     "migemm_workspace_size": ([_vp, ctypes.POINTER(_sz)], _i32),
     "migemm_last_error": ([], ctypes.c_char_p),
     "migemm_version": ([], ctypes.c_char_p),
+    "migemm_context_create": ([_i32, ctypes.POINTER(_vp)], _i32),
+    "migemm_context_destroy": ([_vp], _i32),
+    "migemm_context_info": ([_vp, _ip, ctypes.c_char_p, _sz, _ip, _ip, _ip, _ip, _ip,
+                             ctypes.POINTER(_sz)], _i32),
+    "migemm_buffer_get_or_create": ([_vp, ctypes.c_char_p, _sz, ctypes.POINTER(_vp)], _i32),
+    "migemm_buffer_release": ([ctypes.c_char_p], _i32),
+    "migemm_buffer_release_all": ([], _i32),
+    "migemm_buffer_count": ([ctypes.POINTER(_sz), ctypes.POINTER(_sz)], _i32),
+    "migemm_queue_register_current": ([_vp, _vp], _i32),
+    "migemm_queue_get_current": ([ctypes.POINTER(_vp), ctypes.POINTER(_vp)], _i32),
+    "migemm_queue_clear_current": ([], _i32),
+    "migemm_tensor_buffer": ([ctypes.c_char_p, _sz, ctypes.POINTER(_vp)], _i32),
     "migemm_set_gemm_policy": ([_i32, _ip], _i32),
     "migemm_set_tuning": ([_i32, _i32, _ip], _i32),
     "migemm_last_plan": ([ctypes.c_char_p, _sz], _i32),

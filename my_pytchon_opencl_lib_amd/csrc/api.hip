@@ -484,6 +484,29 @@ int migemm_lstm_gemm_grad_weights(void *stream, const float *X, const float *H_o
                                           MIGEMM_GEMM_ACCUMULATE);
 }
 
+int migemm_lstm_recurrent_gates(void *stream, float *XW, const float *H_out, const float *U,
+                                int batch_size, int seq_len, int hidden_size, int t) {
+    clear_error();
+    if (XW == nullptr || H_out == nullptr || U == nullptr)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "lstm_recurrent_gates: null pointer argument");
+    if (batch_size < 1 || seq_len < 1 || hidden_size < 1)
+        return set_error(MIGEMM_ERR_INVALID_ARG,
+                         "lstm_recurrent_gates: sizes must be >= 1 (batch=%d seq=%d hidden=%d)",
+                         batch_size, seq_len, hidden_size);
+    if (t < 0 || t >= seq_len)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "lstm_recurrent_gates: step %d not in [0, %d)",
+                         t, seq_len);
+    const int64_t gates = (int64_t)4 * hidden_size;
+    if (gates > INT32_MAX)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "lstm_recurrent_gates: 4*hidden exceeds 2^31-1");
+    if (t == 0) return MIGEMM_OK;  // h_{-1} = 0: the gates are XW itself (lstm.cl:57-60)
+    // XW[:, t, :] += H_out[:, t-1, :] * U: rows b of the two slices sit seq_len rows apart
+    return migemm_gemm_strided_batched_ex(
+        stream, 0, 0, batch_size, (int)gates, hidden_size, H_out + (int64_t)(t - 1) * hidden_size,
+        (int64_t)seq_len * hidden_size, 0, U, gates, 0, nullptr, XW + (int64_t)t * gates,
+        (int64_t)seq_len * gates, 0, 1, MIGEMM_GEMM_ACCUMULATE);
+}
+
 int migemm_linear_weight_grad(void *stream, const float *X, const float *dY, float *dW, int M,
                               int K, int N, int batch) {
     clear_error();

@@ -192,6 +192,25 @@ class NnClGlob:
                 t, f, g)
         return xw
 
+    def LstmRecurrentGates(self, xw, hOut, u, t):
+        """The recurrent product of step t inside lstm_recurrent_forward (lstm.cl:80-101,
+        enqueued by NnClGlob.Lstm, NnClGlob.cs:912-928), in place on xw [B, S, 4H]:
+        xw[:, t] += hOut[:, t-1] @ u (u [H, 4H]); xw[:, t] then holds the step's raw gates
+        (the reference's workspace[t, b, :4H], lstm.cl:103-106). A no-op at t = 0."""
+        _check_tensor("xw", xw)
+        _check_tensor("hOut", hOut)
+        _check_tensor("u", u)
+        _require(xw.dim() == 3 and hOut.dim() == 3, "xw and hOut must be [Batch, Seq, *]")
+        b, s_, g = xw.shape
+        h = hOut.shape[2]
+        _require(g == 4 * h, f"xw must end in 4*hidden = {4 * h} gates (got {g})")
+        _require(hOut.shape[0] == b and hOut.shape[1] == s_, "xw and hOut batch/seq differ")
+        _require(list(u.shape) == [h, g], f"u must be [{h}, {g}] (got {list(u.shape)})")
+        _require(0 <= t < s_, f"step {t} is outside [0, {s_})")
+        _launch("migemm_lstm_recurrent_gates", (xw, hOut, u), _ptr(xw), _ptr(hOut), _ptr(u), b,
+                s_, h, int(t))
+        return xw
+
     def LstmGemmGradX(self, allGradGates, w, xShape):
         """grad_X (shape xShape) = allGradGates[T, 4H] @ w[F, 4H]^T: stage 2 of
         NnClGlob.LstmBackward (NnClGlob.cs:967-994, lstm_gemm_grad_x lstm.cl:372-457)."""

@@ -51,6 +51,7 @@ def lib():
         L.oracle_lstm_gemm_xw.argtypes = [f, f, f, f, i32, i32, i32]
         L.oracle_lstm_gemm_grad_x.argtypes = [f, f, f, i32, i32, i32]
         L.oracle_lstm_gemm_grad_weights.argtypes = [f] * 6 + [i32] * 4
+        L.oracle_lstm_recurrent_gates.argtypes = [f, f, f, f, i32, i32, i32, i32]
         L.oracle_tensor_permute.argtypes = [f, f, i, i, i32]
         L.oracle_reduce_sum_axis.argtypes = [f, f, i32, i32, i32]
         L.oracle_linear_bias_backward.argtypes = [f, f, i32, i32]
@@ -213,6 +214,17 @@ def lstm_gemm_grad_weights(X, H_out, G, grad_W, grad_U, grad_bias, batch_size, s
     lib().oracle_lstm_gemm_grad_weights(_fp(X), _fp(H_out), _fp(G), _fp(gW), _fp(gU), _fp(gB),
                                         batch_size, seq_len, F, H)
     return gW, gU, gB
+
+
+def lstm_recurrent_gates(XW, H_out, U, t):
+    """lstm.cl:80-101: the raw gates [B, 4H] of step t, XW [B, S, 4H] + h_{t-1} U with the
+    reference's fp32 arithmetic (an fma chain over h ascending, starting from the XW
+    value); h_{t-1} = H_out[:, t-1] (zero at t = 0)."""
+    B, S, Gt = XW.shape
+    H = U.shape[0]
+    gates = np.empty((B, Gt), dtype=np.float32)
+    lib().oracle_lstm_recurrent_gates(_fp(XW), _fp(H_out), _fp(U), _fp(gates), B, S, H, t)
+    return gates
 
 
 def tensor_permute(x, axes):

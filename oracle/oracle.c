@@ -29,6 +29,13 @@
  *    by the reference kernels themselves on the GPU (tests/test_reference_gpu.py), by exact
  *    small-integer products against independent numpy constructions, and by
  *    grad_x == bmm_permute_tiled(G, W, transB) bit for bit.
+ *  - oracle_lstm_recurrent_gates follows the recurrent product of
+ *    cs/cl_kernels/lstm.cl:80-101: the step's XW value as the accumulator's start, then an
+ *    fma chain over h ascending of h_{t-1}[h] * U[h][g]. Pinned by the reference kernel's
+ *    own stored gates (lstm_recurrent_forward's workspace, tests/test_reference_gpu.py and
+ *    the committed fixture tests/golden/reference_outputs.npz), by exact small-integer
+ *    products against an independent numpy construction, and by a planted mistake (the
+ *    hidden state of step t instead of t-1) that the known answers reject.
  *  - oracle_tensor_permute follows cl_kernels/permute.cl:11-50. Pinned by numpy.transpose.
  *  - oracle_reduce_sum_axis / oracle_linear_bias_backward follow
  *    cs/cl_kernels/reduce_sum_axis.cl:3-24 and cs/cl_kernels/linear.cl:149-168: sequential
@@ -226,6 +233,26 @@ void oracle_lstm_gemm_grad_weights(const float *X, const float *Hout, const floa
                 acc = fmaf(hv, g, acc);
             }
             gU[(int64_t)h * Gt + c] = gU[(int64_t)h * Gt + c] + acc;
+        }
+}
+
+/* lstm.cl:80-101 (inside lstm_recurrent_forward): the raw gates of step t of sequence b,
+ *   acc = XW[(b*seq_len + t)*4H + g]                                            :82-87
+ *   acc = fma(h_prev[h], U[h*4H + g], acc) for h = 0..H-1 ascending             :90-101
+ * with h_prev = H_out[(b*seq_len + t-1)*H + h] (the previous step's hidden state, which the
+ * kernel keeps in h_local, :122-123) and 0 at t == 0 (:57-60). The kernel stores acc in
+ * workspace[(t*batch + b)*5H + g] (:103-106); gates[b*4H + g] receives it here. */
+void oracle_lstm_recurrent_gates(const float *XW, const float *Hout, const float *U,
+                                 float *gates, int batch_size, int seq_len, int hidden, int t) {
+    const int Gt = 4 * hidden;
+    for (int b = 0; b < batch_size; ++b)
+        for (int g = 0; g < Gt; ++g) {
+            float acc = XW[((int64_t)b * seq_len + t) * Gt + g];
+            for (int h = 0; h < hidden; ++h) {
+                const float hv = t > 0 ? Hout[((int64_t)b * seq_len + t - 1) * hidden + h] : 0.0f;
+                acc = fmaf(hv, U[(int64_t)h * Gt + g], acc);
+            }
+            gates[(int64_t)b * Gt + g] = acc;
         }
 }
 

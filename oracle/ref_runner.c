@@ -20,6 +20,8 @@
  *   lstm_gemm_grad_x   global (ceil(F/64)*16, ceil(T/64)*16) local (16,16)  NnClGlob.cs:986-994
  *   lstm_gemm_grad_weights  global (ceil(4H/64)*16, ceil(max(F,H)/64)*16) local (16,16)
  *                      NnClGlob.cs:1017-1024
+ *   lstm_recurrent_forward  global (wg, 1, batch) local (wg, 1, 1) with
+ *                      wg = min(max work-group size, ceil(H/32)*32)  NnClGlob.cs:920-928
  *
  * Usage: ref_runner <code_object> <kernel> <M> <K> <N> <batch> <sA> <sB> <sC> <transA>
  *                   <transB> <A.f32> <B.f32|-> <bias.f32|-> <out.f32> [reps]
@@ -29,7 +31,9 @@
  *  lstm_gemm_grad_weights: M = batch_size, K = seq_len, N = in_features, batch = hidden;
  *  A = X, B = H_out, bias = grad_gates; <out>.init holds the initial grad_W | grad_U |
  *  grad_bias, which are re-uploaded before every repetition (the kernel accumulates), and
- *  <out> receives the three concatenated.)
+ *  <out> receives the three concatenated.
+ *  lstm_recurrent_forward: M = batch_size, K = seq_len, N = hidden; A = XW_in [B, S, 4H],
+ *  B = U [H, 4H]; <out> receives H_out [B, S, H] followed by workspace [S, B, 5H].)
  * Inputs are raw little-endian float32 files; the output file receives the kernel's output
  * buffer. One JSON line on stdout reports the median kernel time from OpenCL profiling
  * events. Exit status 3 means no OpenCL GPU device or the binary was refused (the caller
@@ -140,6 +144,9 @@ int main(int argc, char **argv) {
 
     const int is_permute = strcmp(kname, "tensor_permute") == 0;
     const int is_gw = strcmp(kname, "lstm_gemm_grad_weights") == 0;
+    const int is_rec = strcmp(kname, "lstm_recurrent_forward") == 0;
+    /* lstm_recurrent_forward: H_out [B, S, H] then workspace [S, B, 5H] */
+    const size_t rec_n[2] = {(size_t)M * K * N, (size_t)K * M * 5 * (size_t)N};
     size_t out_elems;
     /* lstm_gemm_grad_weights: sizes of grad_W, grad_U, grad_bias */
     const size_t gw_n[3] = {(size_t)N * 4 * (size_t)batch, (size_t)batch * 4 * (size_t)batch,
@@ -147,6 +154,8 @@ int main(int argc, char **argv) {
     void *hinit = NULL;
     if (is_permute) {
         out_elems = a_size / sizeof(float);
+    } else if (is_rec) {
+        out_elems = rec_n[0] + rec_n[1];
     } else if (is_gw) {
         out_elems = gw_n[0] + gw_n[1] + gw_n[2];
         char init_path[4096];
@@ -176,6 +185,7 @@ int main(int argc, char **argv) {
     CHECK(err, "buffer C");
 
     cl_mem gw_bufs[3] = {NULL, NULL, NULL};
+    cl_mem rec_ws = NULL;
     size_t gsz[3], lsz[3];
     cl_uint dims = 3;
     size_t *lptr = lsz;
@@ -288,6 +298,27 @@ int main(int argc, char **argv) {
         gsz[0] = (size_t)((4 * hidden + 63) / 64) * 16;
         gsz[1] = (size_t)((rows + 63) / 64) * 16;
         lsz[0] = lsz[1] = 16;
+    } else if (is_rec) {
+        /* (XW_in, U, H_out, workspace, batch_size, seq_len, hidden_size); H_out lives in the
+         * output buffer C, the workspace gets a buffer of its own */
+        rec_ws = clCreateBuffer(ctx, CL_MEM_READ_WRITE, rec_n[1] * sizeof(float), NULL, &err);
+        CHECK(err, "buffer workspace");
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &da);
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &db);
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &dc);
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &rec_ws);
+        clSetKernelArg(kern, t++, sizeof(int), &M);
+        clSetKernelArg(kern, t++, sizeof(int), &K);
+        clSetKernelArg(kern, t++, sizeof(int), &N);
+        size_t max_wg = 256;
+        clGetDeviceInfo(dev, CL_DEVICE_MAX_WORK_GROUP_SIZE, sizeof(max_wg), &max_wg, NULL);
+        size_t wg = (size_t)((N + 31) / 32) * 32;
+        if (wg > max_wg) wg = max_wg;
+        gsz[0] = wg;
+        gsz[1] = 1;
+        gsz[2] = (size_t)M;
+        lsz[0] = wg;
+        lsz[1] = lsz[2] = 1;
     } else if (is_permute) {
         /* B file holds int32 dims[M] then axes[M]; M = num_dims */
         const int nd = M;
@@ -356,6 +387,13 @@ int main(int argc, char **argv) {
                   "read grads");
             off += gw_n[i];
         }
+    } else if (is_rec) {
+        CHECK(clEnqueueReadBuffer(q, dc, CL_TRUE, 0, rec_n[0] * sizeof(float), hc, 0, NULL,
+                                  NULL),
+              "read H_out");
+        CHECK(clEnqueueReadBuffer(q, rec_ws, CL_TRUE, 0, rec_n[1] * sizeof(float),
+                                  hc + rec_n[0], 0, NULL, NULL),
+              "read workspace");
     } else {
         CHECK(clEnqueueReadBuffer(q, dc, CL_TRUE, 0, out_elems * sizeof(float), hc, 0, NULL,
                                   NULL),

@@ -27,6 +27,7 @@ CODE_OBJECT = {
     "lstm_gemm_xw": "lstm.co",
     "lstm_gemm_grad_x": "lstm.co",
     "lstm_gemm_grad_weights": "lstm.co",
+    "lstm_recurrent_forward": "lstm.co",
 }
 
 
@@ -85,3 +86,15 @@ def lstm_gemm_grad_weights(X, H_out, G, grad_W, grad_U, grad_bias, batch_size, s
     nW, nU = F * 4 * H, H * 4 * H
     return (res[:nW].reshape(F, 4 * H), res[nW:nW + nU].reshape(H, 4 * H),
             res[nW + nU:].reshape(4 * H)), info
+
+
+def lstm_recurrent_forward(XW, U, reps=1):
+    """Runs the reference lstm_recurrent_forward (cs/cl_kernels/lstm.cl:40-127) over all
+    steps of XW [B, S, 4H]; returns (H_out [B, S, H], raw gates [S, B, 4H], cell states
+    [S, B, H]) -- the kernel's workspace [S, B, 5H] split into its gate and cell parts."""
+    B, S, Gt = XW.shape
+    H = Gt // 4
+    res, info = run("lstm_recurrent_forward", XW, U, M=B, K=S, N=H, reps=reps)
+    n_h = B * S * H
+    ws = res[n_h:].reshape(S, B, 5 * H)
+    return res[:n_h].reshape(B, S, H), ws[:, :, :4 * H], ws[:, :, 4 * H:], info

@@ -15,7 +15,7 @@ BIN = os.path.join(HERE, "_bin", "c_abi_check")
 def build():
     os.makedirs(os.path.dirname(BIN), exist_ok=True)
     # rpath relative to the binary, so the tree can move (the GPU box copies it elsewhere)
-    subprocess.run(["gcc", "-std=c99", "-O2", "-Wall", "-Wextra", "-Werror", "-pedantic",
+    subprocess.run(["gcc", "-std=c99", "-O2", "-Wall", "-Wextra", "-Werror", "-pedantic", "-pthread",
                     "-I", os.path.join(ROOT, "include"), SRC, "-L", PKG, "-lmigemm",
                     "-Wl,-rpath,$ORIGIN/../../my_pytchon_opencl_lib_amd", "-o", BIN],
                    check=True)

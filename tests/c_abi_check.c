@@ -4,8 +4,13 @@
  *   c_abi_check validate   argument checks only; needs no GPU
  *   c_abi_check gpu        device memory, copies and the GEMM entry points on GPU 0,
  *                          checked exactly against a CPU loop on small-integer operands
+ *   c_abi_check runtime    the reference host's runtime objects on GPU 0: a context, the
+ *                          name-keyed buffer pool, one registered queue per POSIX thread,
+ *                          and Bmm -> BmmOp.Backward on pooled buffers with fresh names
  *
  * Exit status 0 on success; every failure prints what failed. */
+#define _POSIX_C_SOURCE 200809L
+#include <pthread.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -130,12 +135,155 @@ static int gpu(void) {
     return failures;
 }
 
+/* ---- runtime objects: context, pool, per-thread queues (cs/core/ComputeContext.cs,
+ *      cs/compiler/OpenCLBufferManager.cs, cs/core/DeviceQueueRegistry.cs) ---- */
+struct worker {
+    void *ctx;
+    void *stream;
+    int index;
+    int ok;
+    void *seen_stream;
+    float *buf;
+};
+
+/* Registers its own queue, reads it back, and fills its own pooled tensor with its index. */
+static void *worker_main(void *arg) {
+    struct worker *w = (struct worker *)arg;
+    void *c = NULL, *s = NULL, *p = NULL;
+    char name[32];
+    w->ok = migemm_queue_get_current(NULL, NULL) == MIGEMM_ERR_NO_QUEUE &&
+            migemm_queue_register_current(w->ctx, w->stream) == MIGEMM_OK &&
+            migemm_queue_get_current(&c, &s) == MIGEMM_OK && c == w->ctx;
+    w->seen_stream = s;
+    snprintf(name, sizeof(name), "worker%d", w->index);
+    if (w->ok && migemm_tensor_buffer(name, 256 * sizeof(float), &p) == MIGEMM_OK) {
+        float h[256];
+        for (int i = 0; i < 256; ++i) h[i] = (float)w->index;
+        w->ok = migemm_memcpy_h2d(s, p, h, sizeof(h)) == MIGEMM_OK &&
+                migemm_stream_synchronize(s) == MIGEMM_OK;
+        w->buf = (float *)p;
+    } else {
+        w->ok = 0;
+    }
+    migemm_queue_clear_current();
+    return NULL;
+}
+
+static int runtime(void) {
+    void *ctx = NULL, *other = NULL, *p0 = NULL, *p1 = NULL;
+    int dev = -1, wave = 0, wx = 0, wy = 0;
+    char arch[64];
+    CHECK(migemm_context_create(-1, &ctx) == MIGEMM_OK, "context_create: %s", migemm_last_error());
+    if (failures) return failures;
+    CHECK(migemm_context_info(ctx, &dev, arch, sizeof(arch), NULL, &wave, NULL, &wx, &wy, NULL) ==
+              MIGEMM_OK && dev >= 0 && wave == 64 && wy == 8 && strncmp(arch, "gfx950", 6) == 0,
+          "context_info: dev %d wave %d wx %d wy %d arch %s", dev, wave, wx, wy, arch);
+    /* pool: reuse while large enough, replace when larger or from another context */
+    CHECK(migemm_buffer_get_or_create(ctx, "x", 1024, &p0) == MIGEMM_OK, "pool: %s",
+          migemm_last_error());
+    CHECK(migemm_buffer_get_or_create(ctx, "x", 512, &p1) == MIGEMM_OK && p1 == p0, "pool reuse");
+    CHECK(migemm_buffer_get_or_create(ctx, "x", 4096, &p1) == MIGEMM_OK && p1 != NULL,
+          "pool growth: %s", migemm_last_error());
+    CHECK(migemm_context_create(-1, &other) == MIGEMM_OK, "second context");
+    CHECK(migemm_buffer_get_or_create(other, "x", 16, &p0) == MIGEMM_OK, "other context");
+    size_t n = 0, total = 0;
+    CHECK(migemm_buffer_count(&n, &total) == MIGEMM_OK && n == 1 && total == 16,
+          "count %zu %zu", n, total);
+    CHECK(migemm_context_destroy(other) == MIGEMM_OK, "context_destroy: %s", migemm_last_error());
+    CHECK(migemm_buffer_count(&n, &total) == MIGEMM_OK && n == 0, "destroy kept %zu", n);
+
+    /* one queue per thread */
+    enum { T = 4 };
+    pthread_t th[T];
+    struct worker w[T];
+    for (int i = 0; i < T; ++i) {
+        w[i].ctx = ctx;
+        w[i].index = i;
+        w[i].ok = 0;
+        w[i].buf = NULL;
+        CHECK(migemm_stream_create(&w[i].stream) == MIGEMM_OK, "stream_create");
+    }
+    for (int i = 0; i < T; ++i) pthread_create(&th[i], NULL, worker_main, &w[i]);
+    for (int i = 0; i < T; ++i) pthread_join(th[i], NULL);
+    CHECK(migemm_queue_get_current(NULL, NULL) == MIGEMM_ERR_NO_QUEUE, "main thread has a queue");
+    for (int i = 0; i < T; ++i) {
+        float h[256];
+        void *p = NULL;
+        char name[32];
+        snprintf(name, sizeof(name), "worker%d", i);
+        CHECK(w[i].ok && w[i].seen_stream == w[i].stream, "worker %d: %s", i, migemm_last_error());
+        CHECK(migemm_buffer_get_or_create(ctx, name, 1024, &p) == MIGEMM_OK && p == w[i].buf,
+              "worker %d buffer", i);
+        CHECK(migemm_memcpy_d2h(w[i].stream, h, p, sizeof(h)) == MIGEMM_OK && h[0] == (float)i &&
+                  h[255] == (float)i, "worker %d data", i);
+        CHECK(migemm_stream_destroy(w[i].stream) == MIGEMM_OK, "stream_destroy");
+    }
+
+    /* Bmm -> BmmOp.Backward on pooled buffers, a fresh name per output */
+    enum { B = 2, M = 24, K = 40, N = 16 };
+    void *q = NULL, *da, *db, *dg, *dc, *dga, *dgb;
+    CHECK(migemm_stream_create(&q) == MIGEMM_OK && migemm_queue_register_current(ctx, q) == MIGEMM_OK,
+          "register: %s", migemm_last_error());
+    static float hA[B * M * K], hB[B * K * N], hG[B * M * N], hC[B * M * N], hR[B * M * N];
+    static float hGA[B * M * K], hGB[B * K * N], rGA[B * M * K], rGB[B * K * N];
+    unsigned s = 7u;
+    for (int i = 0; i < B * M * K; ++i) { s = s * 1103515245u + 12345u; hA[i] = (float)((int)(s >> 16) % 7 - 3); }
+    for (int i = 0; i < B * K * N; ++i) { s = s * 1103515245u + 12345u; hB[i] = (float)((int)(s >> 16) % 7 - 3); }
+    for (int i = 0; i < B * M * N; ++i) { s = s * 1103515245u + 12345u; hG[i] = (float)((int)(s >> 16) % 7 - 3); }
+    CHECK(migemm_tensor_buffer("a", sizeof(hA), &da) == MIGEMM_OK &&
+              migemm_tensor_buffer("b", sizeof(hB), &db) == MIGEMM_OK &&
+              migemm_tensor_buffer("grad_c", sizeof(hG), &dg) == MIGEMM_OK, "tensor buffers");
+    migemm_memcpy_h2d(q, da, hA, sizeof(hA));
+    migemm_memcpy_h2d(q, db, hB, sizeof(hB));
+    migemm_memcpy_h2d(q, dg, hG, sizeof(hG));
+    CHECK(migemm_tensor_buffer("bmm_c#1", sizeof(hC), &dc) == MIGEMM_OK &&
+              migemm_bmm_tiled(q, da, db, dc, M, K, N, M * K, K * N, M * N, B) == MIGEMM_OK &&
+              migemm_stream_synchronize(q) == MIGEMM_OK, "Bmm: %s", migemm_last_error());
+    CHECK(migemm_tensor_buffer("bmm_c#2", sizeof(hGA), &dga) == MIGEMM_OK &&
+              migemm_bmm_permute_tiled(q, dg, db, dga, M, N, K, M * N, K * N, M * K, 0, 1, B) ==
+                  MIGEMM_OK, "gradA: %s", migemm_last_error());
+    CHECK(migemm_tensor_buffer("bmm_c#3", sizeof(hGB), &dgb) == MIGEMM_OK &&
+              migemm_bmm_permute_tiled(q, da, dg, dgb, K, M, N, M * K, M * N, K * N, 1, 0, B) ==
+                  MIGEMM_OK, "gradB: %s", migemm_last_error());
+    migemm_memcpy_d2h(q, hC, dc, sizeof(hC));
+    migemm_memcpy_d2h(q, hGA, dga, sizeof(hGA));
+    migemm_memcpy_d2h(q, hGB, dgb, sizeof(hGB));
+    ref_gemm(0, 0, M, N, K, hA, hB, NULL, hR, B, 0);
+    CHECK(memcmp(hC, hR, sizeof(hC)) == 0, "Bmm output differs");
+    for (int b = 0; b < B; ++b)
+        for (int i = 0; i < M; ++i)
+            for (int j = 0; j < K; ++j) {
+                double a = 0;
+                for (int k = 0; k < N; ++k)
+                    a += (double)hG[(b * M + i) * N + k] * hB[(b * K + j) * N + k];
+                rGA[(b * M + i) * K + j] = (float)a;
+            }
+    for (int b = 0; b < B; ++b)
+        for (int i = 0; i < K; ++i)
+            for (int j = 0; j < N; ++j) {
+                double a = 0;
+                for (int k = 0; k < M; ++k)
+                    a += (double)hA[(b * M + k) * K + i] * hG[(b * M + k) * N + j];
+                rGB[(b * K + i) * N + j] = (float)a;
+            }
+    CHECK(memcmp(hGA, rGA, sizeof(hGA)) == 0, "gradA did not survive gradB");
+    CHECK(memcmp(hGB, rGB, sizeof(hGB)) == 0, "gradB differs");
+    migemm_queue_clear_current();
+    CHECK(migemm_stream_destroy(q) == MIGEMM_OK, "stream_destroy");
+    CHECK(migemm_context_destroy(ctx) == MIGEMM_OK, "context_destroy: %s", migemm_last_error());
+    CHECK(migemm_buffer_count(&n, NULL) == MIGEMM_OK && n == 0, "buffers left: %zu", n);
+    return failures;
+}
+
 int main(int argc, char **argv) {
-    if (argc != 2 || (strcmp(argv[1], "validate") != 0 && strcmp(argv[1], "gpu") != 0)) {
-        fprintf(stderr, "usage: %s validate|gpu\n", argv[0]);
+    if (argc != 2 || (strcmp(argv[1], "validate") != 0 && strcmp(argv[1], "gpu") != 0 &&
+                      strcmp(argv[1], "runtime") != 0)) {
+        fprintf(stderr, "usage: %s validate|gpu|runtime\n", argv[0]);
         return 2;
     }
-    const int bad = strcmp(argv[1], "gpu") == 0 ? gpu() : validate();
+    const int bad = strcmp(argv[1], "gpu") == 0       ? gpu()
+                    : strcmp(argv[1], "runtime") == 0 ? runtime()
+                                                      : validate();
     printf("c_abi_check %s: %s\n", argv[1], bad ? "FAILED" : "ok");
     return bad ? 1 : 0;
 }

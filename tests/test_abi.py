@@ -46,8 +46,9 @@ def _arg_count(params):
 
 
 def test_pinvoke_block_binds_every_declared_function():
-    """INTEGRATION.md's C# P/Invoke block declares every function of include/migemm.h with
-    the header's argument count, so a maintainer can paste it as the host's binding."""
+    """The C# P/Invoke block of the integration notes declares every function of
+    include/migemm.h with the header's argument count, so a maintainer can paste it as the
+    host's binding."""
     header = open(HEADER).read()
     decl = {m.group(1): _arg_count(m.group(2)) for m in
             re.finditer(r"^(?:int|const char \*)\s*(migemm_\w+)\(([^)]*)\);", header, re.M)}
@@ -188,3 +189,69 @@ def test_c_caller_compiles_and_validates_without_gpu():
     r = c_abi.run("validate")
     assert r.returncode == 0, r.stdout + r.stderr
     assert "c_abi_check validate: ok" in r.stdout
+
+
+def test_runtime_services_validate_without_gpu(lib):
+    """The runtime objects' argument checks (the reference's ArgumentNullException /
+    ArgumentException / InvalidOperationException paths, OpenCLBufferManager.cs:24-26,
+    DeviceQueueRegistry.cs:21,30-36) run before any HIP call."""
+    import threading
+    NO_QUEUE = _native.MIGEMM_ERR_NO_QUEUE
+    out = ctypes.c_void_p()
+    expect(lib.migemm_buffer_get_or_create(NULL, b"x", 16, ctypes.byref(out)), INVALID,
+           "null context")
+    expect(lib.migemm_buffer_get_or_create(P[0], b"", 16, ctypes.byref(out)), INVALID,
+           "empty buffer name")
+    expect(lib.migemm_buffer_get_or_create(P[0], b"x", 0, ctypes.byref(out)), INVALID,
+           "size must be > 0")
+    expect(lib.migemm_buffer_get_or_create(P[0], b"x", 16, ctypes.byref(out)), INVALID,
+           "unknown context")
+    expect(lib.migemm_queue_register_current(P[0], NULL), INVALID, "must not be null")
+    expect(lib.migemm_queue_register_current(P[0], P[1]), INVALID, "unknown context")
+    expect(lib.migemm_context_create(-2, ctypes.byref(out)), INVALID, "device -2")
+    expect(lib.migemm_context_info(P[0], None, None, 0, None, None, None, None, None, None),
+           INVALID, "unknown context")
+
+    results = {}
+
+    def fresh_thread():  # a thread that registered nothing
+        results["get"] = lib.migemm_queue_get_current(None, None)
+        results["get_msg"] = _native.last_error()
+        results["buf"] = lib.migemm_tensor_buffer(b"t0", 64, ctypes.byref(ctypes.c_void_p()))
+    th = threading.Thread(target=fresh_thread)
+    th.start()
+    th.join()
+    assert results["get"] == NO_QUEUE and "no queue is registered" in results["get_msg"]
+    assert results["buf"] == NO_QUEUE
+    assert lib.migemm_queue_clear_current() == 0
+    n, b = ctypes.c_size_t(9), ctypes.c_size_t(9)
+    assert lib.migemm_buffer_count(ctypes.byref(n), ctypes.byref(b)) == 0 and n.value == 0
+    assert lib.migemm_buffer_release(b"never-created") == 0
+
+
+def test_runtime_mirror_maps_no_queue_to_runtime_error():
+    from my_pytchon_opencl_lib_amd import runtime
+    import threading
+    err = {}
+
+    def t():
+        try:
+            runtime.DeviceQueueRegistry.GetCurrent()
+        except Exception as e:  # noqa: BLE001
+            err["e"] = e
+    th = threading.Thread(target=t)
+    th.start()
+    th.join()
+    assert isinstance(err["e"], _native.MigemmRuntimeError)
+    assert err["e"].status == _native.MIGEMM_ERR_NO_QUEUE
+    with pytest.raises(_native.MigemmArgumentError):
+        runtime.ComputeContext(preferAccelerator=False)
+
+
+def test_lstm_recurrent_gates_rejects_bad_arguments(lib):
+    f = lib.migemm_lstm_recurrent_gates
+    expect(f(NULL, NULL, P[1], P[2], 2, 3, 4, 1), INVALID, "null pointer")
+    expect(f(NULL, P[0], P[1], P[2], 0, 3, 4, 1), INVALID, "sizes must be >= 1")
+    expect(f(NULL, P[0], P[1], P[2], 2, 3, 4, 3), INVALID, "step 3 not in [0, 3)")
+    expect(f(NULL, P[0], P[1], P[2], 2, 3, 4, -1), INVALID, "step -1")
+    assert f(NULL, P[0], P[1], P[2], 2, 3, 4, 0) == 0  # step 0: no work, no HIP call

@@ -17,6 +17,11 @@ def say(*a):
     print(*a, flush=True)
 
 
+def small_ints(shape, seed, lo=-3, hi=3):
+    rng = np.random.default_rng(seed)
+    return rng.integers(lo, hi + 1, size=shape).astype(np.float32)
+
+
 def test_matmul_tiled_reference_shape(nncl):
     """tests/test_matrix_ops.py:87-131 (Test 2): M,K,N = 64,128,96."""
     A = oracle.normal((64, 128), 10, 0)
@@ -86,6 +91,47 @@ def test_linear_via_permute_and_bmm(nncl):
     y = host(nncl.bmm(dev(x.reshape(1, 8, 16)), wt.unsqueeze(0).contiguous()))
     ref = torch.nn.functional.linear(torch.from_numpy(x), torch.from_numpy(w)).numpy()
     np.testing.assert_allclose(y.reshape(-1, 8), ref.reshape(-1, 8), rtol=1e-4, atol=1e-4)
+
+
+def test_linear_layer_runs_nt_without_permute(nncl, monkeypatch):
+    """core/layers.py:21-33 at the tests/test_layers.py:88-112 shape (Linear(16 -> 8) on 2x4
+    tokens) through layers.Linear: one NT GEMM on the [out, in] weight, no tensor_permute
+    launch. Within 1e-5*sqrt(K) of fp64 and of the reference's permute + bmm path; exact on
+    small integers. Also the Linear(500 -> 6565) shape of the reference's largest caller."""
+    from my_pytchon_opencl_lib_amd import NnClGlob, _native, layers
+    x = oracle.normal((2, 4, 16), 42, 0)
+    bound = 1.0 / np.sqrt(16)
+    w = oracle.uniform((8, 16), 42, 1, -bound, bound)
+    ref_path = host(nncl.bmm(dev(x.reshape(1, 8, 16)),
+                             nncl.permute(dev(w), [1, 0]).unsqueeze(0).contiguous()))
+
+    def no_permute(*a, **k):
+        raise AssertionError("Linear.forward must not materialise the weight transpose")
+    monkeypatch.setattr(NnClGlob, "Permute", no_permute)
+    monkeypatch.setattr(NnClGlob, "permute", no_permute)
+    say("layers.Linear 16 -> 8")
+    lin = layers.Linear(16, 8, nncl, weight=w)
+    y = host(lin.forward(dev(x)))
+    assert y.shape == (2, 4, 8)
+    plan = _native.last_plan()
+    assert plan.endswith(" NT") and "K=16" in plan and "N=8" in plan, plan
+    check_gemm(y.reshape(8, 8), x.reshape(8, 16), w, 0, 1, M=8, N=8, K=16, lda=16, ldb=16)
+    ap = oracle.gemm_absprod(x.reshape(8, 16), w, 0, 1, None, M=8, N=8, K=16, lda=16,
+                             ldb=16)[0]
+    d = np.abs(y.reshape(8, 8).astype(np.float64) - ref_path.reshape(8, 8)) / ap
+    assert np.max(d) <= oracle.tolerance(16)
+    ref = torch.nn.functional.linear(torch.from_numpy(x), torch.from_numpy(w)).numpy()
+    np.testing.assert_allclose(y, ref, rtol=1e-4, atol=1e-4)  # the reference test's bar
+    xi = small_ints((3, 7, 33), 5)
+    wi = small_ints((20, 33), 6)
+    yi = host(layers.Linear(33, 20, nncl, weight=wi)(dev(xi)))
+    assert np.array_equal(yi, (xi.astype(np.int64) @ wi.T.astype(np.int64)).astype(np.float32))
+    say("layers.Linear 500 -> 6565 on [8, 1500, 500]")
+    xb = oracle.normal((8, 1500, 500), 43, 0)
+    wb = oracle.uniform((6565, 500), 43, 1, -1 / np.sqrt(500), 1 / np.sqrt(500))
+    yb = host(layers.Linear(500, 6565, nncl, weight=wb)(dev(xb))).reshape(12000, 6565)
+    check_gemm(yb, xb.reshape(12000, 500), wb, 0, 1, M=12000, N=6565, K=500, lda=500, ldb=500,
+               rows=sample_rows(12000, 12))
 
 
 def test_linear_op_backward(nncl):

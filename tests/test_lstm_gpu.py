@@ -128,3 +128,46 @@ def test_lstm_gemms_at_baseline_size(nncl):
     ref = Gr.astype(np.float64).sum(axis=0)
     bound = (256 - 1 + 25 - 1) * 2.0 ** -24 * np.abs(Gr.astype(np.float64)).sum(axis=0)
     assert np.all(np.abs(host(tB) - ref) <= bound)
+
+
+def test_lstm_recurrent_gates_over_steps(nncl):
+    """The per-step recurrent product of lstm_recurrent_forward (lstm.cl:80-101) at the LSTM of
+    BASELINE config 3 (batch 64, hidden 1024): XW[:, t] += h_{t-1} U in place, one GEMM per
+    step. Each step is within 1e-5*sqrt(H) of fp64 (denominator |XW| + |h||U|) and of the
+    restated reference arithmetic; the other steps' slices are untouched, step 0 is a no-op."""
+    B, S, H = 64, 5, 1024
+    XW = oracle.normal((B, S, 4 * H), 41, 0)
+    U = oracle.uniform((H, 4 * H), 41, 1, -1 / 32, 1 / 32)
+    Ho = oracle.uniform((B, S, H), 41, 2)
+    xw, ho, u = dev(XW), dev(Ho), dev(U)
+    for t in range(S):
+        say("lstm recurrent gates step", t)
+        before = host(xw).copy()
+        nncl.LstmRecurrentGates(xw, ho, u, t)
+        got = host(xw)
+        others = [s for s in range(S) if s != t]
+        assert np.array_equal(got[:, others], before[:, others]), f"step {t}: other steps changed"
+        g = got[:, t].astype(np.float64)
+        restated = oracle.lstm_recurrent_gates(XW, Ho, U, t).astype(np.float64)
+        prev = Ho[:, t - 1].astype(np.float64) if t > 0 else np.zeros((B, H))
+        exact = XW[:, t].astype(np.float64) + prev @ U.astype(np.float64)
+        den = np.abs(XW[:, t]).astype(np.float64) + np.abs(prev) @ np.abs(U.astype(np.float64))
+        tol = oracle.tolerance(H)
+        assert np.max(np.abs(g - exact) / den) <= tol, t
+        assert np.max(np.abs(g - restated) / den) <= 2 * tol, t
+        nw = np.linalg.norm(g - exact) / np.linalg.norm(exact)
+        assert nw <= tol, t
+        if t == 0:
+            assert np.array_equal(got[:, 0], XW[:, 0])
+
+
+def test_lstm_recurrent_gates_small_ints_exact(nncl):
+    """Ragged sizes (batch 5, hidden 33) with small integers: exact at every step."""
+    B, S, H = 5, 4, 33
+    XW = small_ints((B, S, 4 * H), 42)
+    U = small_ints((H, 4 * H), 43)
+    Ho = small_ints((B, S, H), 44)
+    xw = dev(XW)
+    for t in range(S):
+        nncl.LstmRecurrentGates(xw, dev(Ho), dev(U), t)
+        assert np.array_equal(host(xw)[:, t], oracle.lstm_recurrent_gates(XW, Ho, U, t)), t

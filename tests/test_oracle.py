@@ -184,7 +184,7 @@ def test_reduce_sum_axis_sequential():
                           np.add.accumulate(g.reshape(-1, 6), axis=0, dtype=np.float32)[-1])
 
 
-# ---------------------------------------- the reference's own test shapes (SURVEY 4)
+# ---------------------------------------- the reference's own test shapes
 @pytest.mark.parametrize("batch,M,K,N", [(1, 64, 128, 96), (4, 32, 64, 32), (4, 32, 64, 48),
                                          (1, 8, 16, 8), (1, 4, 8, 8)])
 def test_reference_test_shapes_within_tolerance(batch, M, K, N):
@@ -303,3 +303,140 @@ def test_lstm_gemm_grad_weights_vs_fp64():
                           (gU, P.T @ G64, np.abs(P).T @ np.abs(G64))]:
         assert np.max(np.abs(got - ref) / np.maximum(den, 1e-30)) <= tol
     assert np.max(np.abs(gB - G64.sum(axis=0)) / np.abs(G64).sum(axis=0)) <= tol
+
+
+# ------------------------------------------------------------ LSTM recurrent step
+@pytest.mark.parametrize("B,S,H", [(3, 4, 5), (2, 7, 17), (4, 3, 33)])
+def test_lstm_recurrent_gates_exact(B, S, H):
+    """lstm.cl:80-101: the gates of step t are XW[:, t] + h_{t-1} U with h_{-1} = 0. Small
+    integers keep every partial sum exact, so the restatement must equal an independent
+    numpy construction bit for bit at every step."""
+    XW = small_ints((B, S, 4 * H), 70 + H)
+    U = small_ints((H, 4 * H), 71 + H)
+    Ho = small_ints((B, S, H), 72 + H)
+    for t in range(S):
+        prev = Ho[:, t - 1].astype(np.int64) if t > 0 else np.zeros((B, H), np.int64)
+        expect = (XW[:, t].astype(np.int64) + prev @ U.astype(np.int64)).astype(np.float32)
+        assert np.array_equal(oracle.lstm_recurrent_gates(XW, Ho, U, t), expect), t
+
+
+def test_lstm_recurrent_gates_catch_planted_mistakes():
+    """A restatement that used the current step's hidden state (h_t instead of h_{t-1}), or
+    started the chain from zero instead of the XW value, fails the known answers."""
+    B, S, H = 2, 5, 6
+    XW = small_ints((B, S, 4 * H), 80)
+    U = small_ints((H, 4 * H), 81)
+    Ho = small_ints((B, S, H), 82)
+
+    def expect(t):
+        prev = Ho[:, t - 1].astype(np.int64) if t > 0 else np.zeros((B, H), np.int64)
+        return (XW[:, t].astype(np.int64) + prev @ U.astype(np.int64)).astype(np.float32)
+
+    def current_h(t):  # h_t instead of h_{t-1}
+        shifted = np.ascontiguousarray(np.concatenate([Ho[:, 1:], Ho[:, :1]], axis=1))
+        return oracle.lstm_recurrent_gates(XW, shifted, U, t)
+
+    def from_zero(t):  # bias / input projection dropped
+        return oracle.lstm_recurrent_gates(np.zeros_like(XW), Ho, U, t)
+
+    for bad in (current_h, from_zero):
+        assert any(not np.array_equal(bad(t), expect(t)) for t in range(S)), bad.__name__
+    assert all(np.array_equal(oracle.lstm_recurrent_gates(XW, Ho, U, t), expect(t))
+               for t in range(S))
+
+
+def test_lstm_recurrent_gates_vs_fp64():
+    """N(0,1) gates at hidden 256: the fp32 chain stays within 1e-5*sqrt(H) of fp64."""
+    B, S, H = 4, 3, 256
+    XW = oracle.normal((B, S, 4 * H), 83, 0)
+    U = oracle.uniform((H, 4 * H), 83, 1, -1 / 16, 1 / 16)
+    Ho = oracle.uniform((B, S, H), 83, 2)
+    for t in range(S):
+        g = oracle.lstm_recurrent_gates(XW, Ho, U, t).astype(np.float64)
+        prev = Ho[:, t - 1].astype(np.float64) if t > 0 else np.zeros((B, H))
+        ref = XW[:, t].astype(np.float64) + prev @ U.astype(np.float64)
+        den = np.abs(XW[:, t]).astype(np.float64) + np.abs(prev) @ np.abs(U.astype(np.float64))
+        assert np.max(np.abs(g - ref) / den) <= oracle.tolerance(H)
+
+
+# ------------------------------------------------- the reference kernels' own outputs
+REF_FIXTURE = os.path.join(os.path.dirname(__file__), "golden", "reference_outputs.npz")
+
+
+def _restate(kernel, inp, a):
+    """The oracle's restatement of one reference kernel, on a fixture's inputs."""
+    if kernel == "matmul_tiled":
+        return oracle.matmul_tiled(inp["A"], inp["B"])
+    if kernel == "bmm_tiled":
+        return oracle.bmm_tiled(inp["A"], inp["B"], a["M"], a["K"], a["N"], a["sA"], a["sB"],
+                                a["sC"], a["batch"])
+    if kernel == "bmm_permute_tiled":
+        return oracle.bmm_permute(inp["A"], inp["B"], bool(a["transA"]), bool(a["transB"]))
+    if kernel == "linear_forward_tiled":
+        return oracle.linear_forward(inp["A"], inp["B"], inp["bias"])
+    if kernel == "tensor_permute":
+        nd = a["M"]
+        return oracle.tensor_permute(inp["A"], [int(v) for v in inp["B"][nd:]])
+    if kernel == "lstm_gemm_xw":
+        return oracle.lstm_gemm_xw(inp["A"], inp["B"], inp["bias"])
+    if kernel == "lstm_gemm_grad_x":
+        return oracle.lstm_gemm_grad_x(inp["A"], inp["B"])
+    raise KeyError(kernel)
+
+
+def test_restatement_equals_reference_fixture():
+    """tests/golden/reference_outputs.npz holds the outputs of the reference's own kernels
+    (its OpenCL sources compiled for gfx950, run on the GPU by
+    tests/golden/make_reference_golden.py): matmul_tiled, bmm_tiled (with a broadcast B),
+    bmm_permute_tiled in all four layouts, linear_forward_tiled, tensor_permute, the three
+    lstm.cl GEMMs and lstm_recurrent_forward's stored gates. The restatement reproduces every
+    one of them bit for bit, here on the CPU."""
+    import json
+    d = np.load(REF_FIXTURE, allow_pickle=False)
+    meta = json.loads(bytes(d["_meta"]).decode())
+    assert meta["device"].startswith("gfx950")
+    kernels = set()
+    for name, m in meta["cases"].items():
+        kernel, a = m["kernel"], m["args"]
+        kernels.add(kernel)
+        if kernel == "lstm_gemm_grad_weights":
+            g = {k: d[f"{name}.{k}"] for k in ("X", "H_out", "G", "gW0", "gU0", "gB0")}
+            oW, oU, oB = oracle.lstm_gemm_grad_weights(g["X"], g["H_out"], g["G"], g["gW0"],
+                                                       g["gU0"], g["gB0"], a["batch_size"],
+                                                       a["seq_len"])
+            for ours, key in ((oW, "gW"), (oU, "gU"), (oB, "gB")):
+                assert np.array_equal(ours, d[f"{name}.{key}"]), (name, key)
+        elif kernel == "lstm_recurrent_forward":
+            XW, U, Ho, gates = (d[f"{name}.{k}"] for k in ("XW", "U", "H_out", "gates"))
+            for t in range(a["S"]):
+                assert np.array_equal(oracle.lstm_recurrent_gates(XW, Ho, U, t), gates[t]), \
+                    (name, t)
+        else:
+            inp = {k: d[f"{name}.{k}"] for k in ("A", "B", "bias") if f"{name}.{k}" in d}
+            out = d[f"{name}.out"]
+            ours = np.ravel(_restate(kernel, inp, a))
+            assert ours.shape == out.shape and np.array_equal(ours, out), name
+    assert kernels == {"matmul_tiled", "bmm_tiled", "bmm_permute_tiled", "linear_forward_tiled",
+                       "tensor_permute", "lstm_gemm_xw", "lstm_gemm_grad_x",
+                       "lstm_gemm_grad_weights", "lstm_recurrent_forward"}
+
+
+def test_reference_fixture_catches_planted_mistakes():
+    """The fixture tells a faithful restatement from plausible mistakes: the same ascending
+    chain without the fused multiply-add (product and sum rounded separately, as a compiler
+    that does not contract `acc += a*b` would give), the sum in pairwise order, and a
+    transposed operand."""
+    d = np.load(REF_FIXTURE, allow_pickle=False)
+    name = "matmul_tiled_64x128x96"
+    A, B, out = d[f"{name}.A"], d[f"{name}.B"], d[f"{name}.out"]
+    assert np.array_equal(np.ravel(oracle.matmul_tiled(A, B)), out)
+    unfused = np.zeros((A.shape[0], B.shape[1]), np.float32)
+    for k in range(A.shape[1]):
+        unfused = unfused + A[:, k, None] * B[None, k, :]  # float32 product, then float32 add
+    assert not np.array_equal(np.ravel(unfused), out)
+    pairwise = np.sum(A[:, :, None] * B[None, :, :], axis=1, dtype=np.float32)
+    assert not np.array_equal(np.ravel(pairwise), out)
+    name = "bmm_permute_tiled_t01_b2_33x47x29"
+    A, B, out = d[f"{name}.A"], d[f"{name}.B"], d[f"{name}.out"]
+    wrong = oracle.bmm_permute(A, np.ascontiguousarray(B.reshape(2, 47, 29)), False, False)
+    assert not np.array_equal(np.ravel(wrong), out)

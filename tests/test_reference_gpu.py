@@ -8,7 +8,10 @@ geometry. Two claims are checked on identical seeded inputs:
      restatement's fp32 fma-chain arithmetic against the reference itself);
   2. the HIP path is within 1e-5*sqrt(K) (relative, componentwise |A||B|) of the
      reference's output, and of fp64.
-Skipped (with the reason) when oracle/_ref was not built or no OpenCL GPU device exists.
+A GPU run without oracle/_ref fails: the prebuilt reference kernels travel with the tree
+(built where the reference sources are mounted). Skipped (with the reason) only when the box
+has no OpenCL GPU device; tests/golden/reference_outputs.npz keeps the restatement pinned to
+these kernels' outputs on the CPU either way (tests/test_oracle.py).
 """
 import numpy as np
 import pytest
@@ -25,10 +28,18 @@ def say(*a):
 
 
 def run_ref(*args, **kw):
+    if not ref.available():
+        pytest.fail("oracle/_ref is missing: build it where the reference sources are mounted "
+                    "(__graft_entry__.build()) so the reference kernels travel with the tree")
     try:
         return ref.run(*args, **kw)
     except ref.Unavailable as e:
         pytest.skip(f"reference OpenCL kernels unavailable: {e}")
+
+
+def require_ref():
+    if not ref.available():
+        pytest.fail("oracle/_ref is missing: build it where the reference sources are mounted")
 
 
 def ulp_report(a, b):
@@ -175,6 +186,7 @@ def test_lstm_gemm_kernels_reference(nncl):
     gU0 = oracle.normal((H, G), 31, 6)
     gB0 = oracle.normal((G,), 31, 7)
     say("reference lstm_gemm_grad_weights")
+    require_ref()
     try:
         (rW, rU, rB), _ = ref.lstm_gemm_grad_weights(X, Hout, Gr, gW0, gU0, gB0, batch, seq)
     except ref.Unavailable as e:
@@ -229,6 +241,7 @@ def test_lstm_gemm_kernels_reference_at_baseline_size(nncl):
     Hout = oracle.uniform((T, H), 32, 3, -1.0, 1.0)
     say("reference lstm_gemm_grad_weights", batch, seq, F, H)
     z = np.zeros
+    require_ref()
     try:
         (rW, rU, rB), info = ref.lstm_gemm_grad_weights(
             X, Hout, Gr, z((F, G), np.float32), z((H, G), np.float32), z(G, np.float32), batch,
@@ -237,3 +250,69 @@ def test_lstm_gemm_kernels_reference_at_baseline_size(nncl):
         pytest.skip(f"reference OpenCL kernels unavailable: {e}")
     say(info)
     check_gemm(rW, X, Gr, 1, 0, M=F, N=G, K=T, lda=F, ldb=G, rows=sample_rows(F, 6))
+
+
+def test_lstm_recurrent_forward_reference(nncl):
+    """The reference lstm_recurrent_forward (lstm.cl:40-127) over several steps at batch 64
+    with hidden 64, where its work-group is one wavefront: its stored raw gates
+    (workspace[t, b, :4H], lstm.cl:103-106) are reproduced bit for bit by the restatement
+    given its H_out as h_{t-1}, and the HIP per-step product (migemm_lstm_recurrent_gates)
+    on the same H_out is within 1e-5*sqrt(H) of them and of fp64."""
+    B, S, H = 64, 5, 64
+    XW = oracle.normal((B, S, 4 * H), 45, 0)
+    U = oracle.uniform((H, 4 * H), 45, 1, -1 / 8, 1 / 8)
+    say("reference lstm_recurrent_forward", B, S, H)
+    require_ref()
+    try:
+        Ho, gates, cells, info = ref.lstm_recurrent_forward(XW, U)
+    except ref.Unavailable as e:
+        pytest.skip(f"reference OpenCL kernels unavailable: {e}")
+    say(info)
+    assert np.all(np.abs(Ho) < 1) and np.any(Ho != 0)
+    xw, ho, u = dev(XW), dev(Ho), dev(U)
+    for t in range(S):
+        restated = oracle.lstm_recurrent_gates(XW, Ho, U, t)
+        assert np.array_equal(restated, gates[t]), \
+            f"step {t}: restatement differs by {ulp_report(restated, gates[t])} ulp"
+        nncl.LstmRecurrentGates(xw, ho, u, t)
+        got = host(xw)[:, t].astype(np.float64)
+        prev = Ho[:, t - 1].astype(np.float64) if t > 0 else np.zeros((B, H))
+        den = np.abs(XW[:, t]).astype(np.float64) + np.abs(prev) @ np.abs(U.astype(np.float64))
+        exact = XW[:, t].astype(np.float64) + prev @ U.astype(np.float64)
+        assert rel_distance(got, gates[t], den) <= oracle.tolerance(H), t
+        assert rel_distance(got, exact, den) <= oracle.tolerance(H), t
+
+
+def test_lstm_recurrent_forward_reference_races_beyond_one_wavefront(nncl):
+    """A defect of the reference kernel, kept visible: lstm_recurrent_forward writes
+    h_local[hid] (the new h_t) inside the step (lstm.cl:122) with no barrier before the same
+    thread's next hidden unit, and the other wavefronts, read h_local[h] as h_{t-1} (:91).
+    With hidden 1024 (BASELINE config 3's LSTM) its work-group holds several wavefronts and
+    each thread several hidden units, so its stored gates are not XW + h_{t-1} U: at step 0,
+    where h_{-1} = 0 and the gates must equal XW exactly, the units after each thread's first
+    read h_0 values and deviate. The HIP product follows the mathematics (XW exactly at step
+    0, fp64 within tolerance at step 1 given the reference's own H_out)."""
+    B, S, H = 64, 2, 1024
+    XW = oracle.normal((B, S, 4 * H), 46, 0)
+    U = oracle.uniform((H, 4 * H), 46, 1, -1 / 32, 1 / 32)
+    say("reference lstm_recurrent_forward (race)", B, S, H)
+    require_ref()
+    try:
+        Ho, gates, cells, info = ref.lstm_recurrent_forward(XW, U)
+    except ref.Unavailable as e:
+        pytest.skip(f"reference OpenCL kernels unavailable: {e}")
+    say(info)
+    dev_ = np.abs(gates[0].astype(np.float64) - XW[:, 0]) / (
+        np.abs(XW[:, 0]).astype(np.float64) + np.abs(U).sum(axis=0)[None, :])
+    worst = float(np.max(dev_))
+    say("reference step-0 gates: worst deviation from XW", worst)
+    assert worst > 10 * oracle.tolerance(H)  # rounding alone stays below 1x
+    xw, ho, u = dev(XW), dev(Ho), dev(U)
+    nncl.LstmRecurrentGates(xw, ho, u, 0)
+    assert np.array_equal(host(xw)[:, 0], XW[:, 0])
+    nncl.LstmRecurrentGates(xw, ho, u, 1)
+    got = host(xw)[:, 1].astype(np.float64)
+    prev = Ho[:, 0].astype(np.float64)
+    den = np.abs(XW[:, 1]).astype(np.float64) + np.abs(prev) @ np.abs(U.astype(np.float64))
+    exact = XW[:, 1].astype(np.float64) + prev @ U.astype(np.float64)
+    assert rel_distance(got, exact, den) <= oracle.tolerance(H)
