@@ -437,13 +437,16 @@ def measure_all_configs(torch, nncl, _native, reps=20):
     g.manual_seed(0)
     out = {}
 
+    cap = torch.cuda.Stream()  # the capturing stream: its own library workspace
+
     def timed(fns, per=None):
         per = per or max(1, reps // len(fns))
-        for f in fns:
-            f()
+        with torch.cuda.stream(cap):  # sizes cap's workspace before the capture
+            for f in fns:
+                f()
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        with torch.cuda.graph(graph, stream=cap):
             for _ in range(per):
                 for f in fns:
                     f()
