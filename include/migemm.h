@@ -320,6 +320,9 @@ int migemm_tensor_buffer(const char *tensor_id, size_t bytes, void **ptr);
 #define MIGEMM_POLICY_SMALL 2  /* k-split 16x16x4 MFMA small-output kernel for every shape */
 #define MIGEMM_POLICY_SKINNY 3 /* fp32-FMA kernel wherever it applies (M <= 4, B not
                                   transposed), otherwise the AUTO choice */
+#define MIGEMM_POLICY_PANEL 4  /* 32x32-tile panel kernel wherever it applies (A not
+                                  transposed, B not transposed, K % 8 == 0, N % 4 == 0,
+                                  16-byte aligned rows), otherwise the AUTO choice */
 /* Sets the policy; *previous (if not NULL) receives the one it replaces. Calls already
  * enqueued are unaffected. */
 int migemm_set_gemm_policy(int policy, int *previous);

@@ -27,6 +27,7 @@ MIGEMM_POLICY_AUTO = 0
 MIGEMM_POLICY_TILED = 1
 MIGEMM_POLICY_SMALL = 2
 MIGEMM_POLICY_SKINNY = 3
+MIGEMM_POLICY_PANEL = 4
 
 # Tuning keys (migemm_set_tuning); 0 = the dispatcher's choice
 MIGEMM_TUNE_TILE = 1

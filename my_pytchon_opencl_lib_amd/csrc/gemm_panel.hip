@@ -1,0 +1,288 @@
+// Panel fp32 GEMM for gfx950: C = A * B (+ bias) for outputs with few rows, A K-contiguous
+// (an activation panel such as the 64 x 1536 input of the LSTM gate GEMM, lstm_gemm_xw,
+// cs/cl_kernels/lstm.cl:273, or the h_{t-1} rows of its recurrent product, lstm.cl:80-101)
+// and B N-contiguous (a weight matrix [K, N]); "cs/" = csharp/cstorchcl/cstorchcl/.
+//
+// Such a GEMM has too few output tiles for the tiled kernel, and every 32x32 tile of C needs
+// its 32-row slice of A and 32-column slice of B over the whole K (393 KB at K = 1536).
+//  * A work-group owns a 32x32 tile of C and has NW wavefronts (8, two per SIMD, when K has
+//    8 or more k-groups of 32); wavefront w multiplies the w-th contiguous share of the
+//    k-groups and the NW partial tiles are added in LDS in the order w = 0..NW-1
+//    (deterministic).
+//  * The product is computed as C^T = B^T A^T with v_mfma_f32_32x32x2_f32: the MFMA's first
+//    operand is B (lane l supplies column n0 + l%32), its second A (lane l supplies row
+//    m0 + l%32). In step s of each 8-wide sub-group, lanes 0-31 supply k = s and lanes 32-63
+//    k = 4 + s, for both operands, so a lane's four A values of a sub-group are one 16-byte
+//    read and B's are four 4-byte reads of consecutive k-rows.
+//  * Every operand byte moves with global_load_lds_dwordx4 (16 bytes per lane, straight
+//    into LDS). A k-group of 32 is 4 KB of each operand, 8 load instructions per wavefront,
+//    each covering 8 whole 128-byte lines: with 8-wide k-groups every line of A was fetched
+//    by 4 instructions and the loads ran at ~23 bytes per clock per CU.
+//  * Each wavefront keeps its own LDS ring of D k-groups (shipped D = 1: one k-group in
+//    flight while the previous one is multiplied) and waits for its own loads
+//    (s_waitcnt vmcnt), so the k loop has no barrier. The fragments of k-group i+1 are read
+//    into a second register set during k-group i's last MFMAs. Past the end the loads
+//    re-read the last k-group (never multiplied), so the wait count is constant.
+//  * A rows are stored with chunk c of row r in slot c ^ ((r / 2) % 8), which makes the
+//    128-bit fragment reads conflict-free.
+//  * Work-groups are dealt to the 8 XCDs in contiguous chunks, both row tiles of a column
+//    block on one XCD, so each XCD's L2 holds a contiguous 1/8 of B (3.1 MB for the gate
+//    GEMM) and B is fetched into L2 once.
+//  * Edges: rows beyond M and columns beyond N are clamped on load and not stored. The
+//    kernel needs K % 32 == 0, N % 4 == 0 and 16-byte aligned rows (the dispatcher checks).
+//  * Epilogue as the other kernels: bias after the k sum (linear.cl:119-122), then C is
+//    written or added to.
+#include "gemm_direct.h"
+
+namespace migemm {
+namespace {
+
+struct PanelArgs {
+    const float *A;
+    const float *B;
+    const float *bias;
+    float *C;
+    int64_t lda, ldb, ldc;
+    int64_t sA, sB, sC;
+    int M, N, K;
+    int tiles_m, tiles_n, batch, total;
+    int accumulate;
+};
+
+constexpr int PT = 32;         // output tile edge
+constexpr int PKG = 32;        // k per k-group: 4 KB of each operand, whole 128-byte lines
+constexpr int PSTAGE = 2048;   // floats per ring stage: B 32 k-rows x 32, then A 32 rows x 32
+constexpr int PRED = PT * 33;  // floats per wavefront's partial tile in the reduction
+
+// A rows in LDS: 32 floats (8 chunks of 16 bytes) per row; chunk c of row r is stored in
+// slot c ^ ((r / 2) % 8), so the 16 rows a 128-bit fragment read phase covers fall on 16
+// distinct bank groups.
+__device__ __forceinline__ int pa_swz(int r) { return (r >> 1) & 7; }
+
+template <int NW, int D>
+__global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
+    static_assert(NW * D * PSTAGE >= NW * PRED, "the reduction reuses the rings");
+    static_assert(8 * (D - 1) < 64, "vmcnt range");
+    __shared__ float ring[NW * D * PSTAGE];
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+    // ---- work-group -> (batch, tile); both row tiles of a column block on one XCD ----
+    int pid = blockIdx.x;
+    if ((p.total & 7) == 0) pid = (pid & 7) * (p.total >> 3) + (pid >> 3);
+    const int per_batch = p.tiles_m * p.tiles_n;
+    const int b = pid / per_batch;
+    const int t = pid - b * per_batch;
+    const int tn = t / p.tiles_m;
+    const int tm = t - tn * p.tiles_m;
+    const int m0 = __builtin_amdgcn_readfirstlane(tm * PT);
+    const int n0 = __builtin_amdgcn_readfirstlane(tn * PT);
+    const int bb = __builtin_amdgcn_readfirstlane(b);
+
+    // ---- this wavefront's k-groups ----
+    const int G = p.K / PKG;
+    const int per = (G + NW - 1) / NW;
+    const int g0 = min(G, w * per);
+    const int ng = min(G, g0 + per) - g0;
+
+    float *my = ring + w * D * PSTAGE;
+    f16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+
+    if (ng > 0) {
+        // Load instruction q (0..3) of an operand fills 1 KB: lane L the 16 bytes at LDS
+        // float 256 q + 4 L.
+        // B (k-rows of 32 columns): lane L loads k-row 8q + L/8, columns n0 + 4 (L % 8) .. +3
+        // (clamped to the last whole chunk).
+        int bcol = n0 + 4 * (lane & 7);
+        bcol = bcol < p.N - 4 ? bcol : p.N - 4;
+        const uint32_t bvoff0 =
+            (uint32_t)((((uint32_t)(lane >> 3)) * (uint32_t)p.ldb + (uint32_t)bcol) * 4u);
+        const uint32_t bq = (uint32_t)(8 * p.ldb * 4);  // bytes between instructions
+        const char *bbase = reinterpret_cast<const char *>(
+            p.B + (int64_t)bb * p.sB + (int64_t)g0 * PKG * p.ldb);
+        const int64_t bstep = (int64_t)PKG * p.ldb * 4;  // bytes per k-group
+        // A (rows of 32 k): lane L loads row 8q + L/8 (clamped) into slot L % 8, the row's k
+        // chunk (L % 8) ^ pa_swz(row).
+        const int arl = lane >> 3;  // row within the instruction
+        uint32_t avoff[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int r = 8 * q + arl;
+            int arow = m0 + r;
+            arow = arow < p.M - 1 ? arow : p.M - 1;
+            const int chunk = (lane & 7) ^ pa_swz(r);
+            avoff[q] = (uint32_t)((((uint32_t)(arow - m0)) * (uint32_t)p.lda + 4u * chunk) * 4u);
+        }
+        const char *abase = reinterpret_cast<const char *>(
+            p.A + (int64_t)bb * p.sA + (int64_t)m0 * p.lda + (int64_t)g0 * PKG);
+        constexpr int64_t astep = PKG * 4;
+
+        auto issue = [&](int j, int slot) {
+            const int g = j < ng ? j : ng - 1;
+            const char *bg = bbase + (int64_t)g * bstep;
+            const char *ag = abase + (int64_t)g * astep;
+            float *st = my + slot * PSTAGE;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) dma16(bg, bvoff0 + q * bq, st + 256 * q);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) dma16(ag, avoff[q], st + 1024 + 256 * q);
+        };
+        // Fragments of sub-group j (k = 8j .. 8j+7 of the k-group), step s: B lane l holds
+        // k-row 8j + s + 4(l/32), column l%32; A lane l holds row l%32, k 8j + 4(l/32) .. +3.
+        const int lo = lane & 31;
+        const int hi = lane >> 5;
+        const int boff = 4 * hi * PT + lo;
+        auto aoff = [&](int j) { return 1024 + lo * PT + 4 * ((2 * j + hi) ^ pa_swz(lo)); };
+
+        struct Frags {
+            float b[4][4];
+            f4 a[4];
+        };
+        auto read = [&](int slot, Frags &f) {
+            const float *st = my + slot * PSTAGE;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) f.b[j][s] = st[boff + (8 * j + s) * PT];
+                f.a[j] = dl_load16(st + aoff(j));
+            }
+        };
+        auto mma = [&](const Frags &f, int j) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(f.b[j][s], f.a[j][s], acc, 0, 0, 0);
+        };
+        // D k-groups in flight; k-group i+1's fragments are read into a second register set
+        // while k-group i's last MFMAs run, so LDS latency is not exposed.
+#pragma unroll
+        for (int j = 0; j < D; ++j) issue(j, j);
+        Frags cur, nxt;
+        wait_vmcnt<8 * (D - 1)>();  // k-group 0 has landed
+        read(0, cur);
+        for (int i = 0; i < ng; ++i) {
+            mma(cur, 0);
+            mma(cur, 1);
+            mma(cur, 2);
+            __builtin_amdgcn_sched_barrier(0);
+            // cur's reads of slot i%D are complete (its MFMAs consumed them): refill it
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            issue(i + D, i % D);
+            wait_vmcnt<8 * (D - 1)>();  // k-group i+1 has landed
+            read((i + 1) % D, nxt);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(cur, 3);
+            cur = nxt;
+        }
+        wait_vmcnt<0>();
+    }
+
+    // ---- combine the NW wavefronts in order, add the bias, store ----
+    // acc register r of lane l: C^T row (= column of C) 8(r/4) + 4(l/32) + r%4, C^T
+    // column (= row of C) l%32.
+    __syncthreads();  // every ring is drained and read
+    float *red = ring + w * PRED;
+    {
+        const int lo = lane & 31;
+        const int hi = lane >> 5;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            red[lo * 33 + 8 * (r >> 2) + 4 * hi + (r & 3)] = acc[r];
+    }
+    __syncthreads();
+    float *Cb = p.C + (int64_t)bb * p.sC;
+    for (int e = threadIdx.x; e < PT * PT; e += NW * 64) {
+        const int mi = e >> 5;
+        const int ni = e & 31;
+        float v = ring[mi * 33 + ni];
+#pragma unroll
+        for (int q = 1; q < NW; ++q) v += ring[q * PRED + mi * 33 + ni];
+        const int m = m0 + mi;
+        const int n = n0 + ni;
+        if (m < p.M && n < p.N) {
+            if (p.bias != nullptr) v = v + p.bias[n];
+            float *c = Cb + (int64_t)m * p.ldc + n;
+            *c = p.accumulate ? *c + v : v;
+        }
+    }
+}
+
+bool aligned16(const float *p, int64_t ld, int64_t stride) {
+    return ((uintptr_t)p & 15) == 0 && ld % 4 == 0 && stride % 4 == 0;
+}
+
+}  // namespace
+
+bool panel_supported(const GemmDesc &d) {
+    // A K-contiguous and B N-contiguous; whole 32-wide k-groups and 16-byte chunks of B;
+    // every row 16-byte aligned; each lane's load offset within a k-group fits 32 bits:
+    // A's is below 32 lda * 4 bytes, B's below (31 ldb + N) * 4 <= 128 ldb bytes.
+    return !d.transA && !d.transB && d.K % PKG == 0 && d.N % 4 == 0 && d.N >= 4 &&
+           aligned16(d.A, d.lda, d.sA) && aligned16(d.B, d.ldb, d.sB) &&
+           d.lda <= ((int64_t)1 << 25) && d.ldb <= ((int64_t)1 << 25);
+}
+
+// Where the panel kernel beats the other families (graph replay, NN, M in 16..256, N in
+// 512..8192, K in 256..4096, 246 shapes; us, panel / the previous choice): one to three
+// rounds of 32x32 tiles, 128-768 tiles (64 x 1536 x 4096 10.3 / 13.3, 96 x 1536 x 2048 9.8 /
+// 18.1 split 64x64 tiles, 256 x 512 x 2048 8.7 / 13.9, 96 x 4096 x 8192 59.5 / 76.4); fewer
+// tiles while K is short enough that one CU per tile is not the bottleneck (64 x 1024 x 1024
+// 7.2 / 8.5, 128 x 512 x 512 5.3 / 7.0; but 32 x 1024 x 512 7.0 / 6.4 and 64 x 4096 x 1024
+// 19.0 / 12.7 with K split over work-groups). It loses at K = 256 below 192 tiles (4.1-4.4
+// against 3.4-4.0: its fixed cost is higher), above 768 tiles (256 x 512 x 4096 16.1 / 13.7
+// in 64x64 tiles) and at M <= 16, where half of each 32-row tile is empty.
+bool panel_preferred(const GemmDesc &d) {
+    if (d.M <= 16 || !panel_supported(d)) return false;
+    const int64_t tiles = (int64_t)((d.M + PT - 1) / PT) * ((d.N + PT - 1) / PT) * d.batch;
+    if (tiles < 16 || tiles > 768) return false;
+    if (d.K < (tiles < 192 ? 512 : 256)) return false;
+    const int kmax = tiles < 32 ? 512 : tiles < 64 ? 1024 : tiles < 128 ? 1536
+                     : tiles < 192 ? 2048 : 1 << 30;
+    return d.K <= kmax;
+}
+
+int launch_gemm_panel(hipStream_t stream, const GemmDesc &d) {
+    PanelArgs a;
+    a.A = d.A;
+    a.B = d.B;
+    a.bias = d.bias;
+    a.C = d.C;
+    a.lda = d.lda;
+    a.ldb = d.ldb;
+    a.ldc = d.ldc;
+    a.sA = d.sA;
+    a.sB = d.sB;
+    a.sC = d.sC;
+    a.M = d.M;
+    a.N = d.N;
+    a.K = d.K;
+    a.tiles_m = (d.M + PT - 1) / PT;
+    a.tiles_n = (d.N + PT - 1) / PT;
+    a.batch = d.batch;
+    const int64_t total = (int64_t)a.tiles_m * a.tiles_n * d.batch;
+    if (total > 0x7fffffff)
+        return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm_panel: %lld work-groups", (long long)total);
+    a.total = (int)total;
+    a.accumulate = d.accumulate;
+    // NW wavefronts split the k-groups (8, two per SIMD, unless K has fewer k-groups), each
+    // with one k-group (8 KB) in flight while it multiplies the previous one: 64 KB of LDS.
+    // Measured at 64 x 1536 x 4096 (100 rotating inputs, graph replay, us): 8 wavefronts
+    // with 1 / 2 k-groups in flight 9.65 / 10.24, 4 with 2 / 3 / 4 10.86 / 11.01 / 11.86, 16
+    // with 1 10.8; loads issued before instead of after the first 12 MFMAs of each
+    // k-group 10.02 against 10.13. Deeper queues do not pay: the k loop alone (no loads)
+    // runs at ~91 % of the MFMA rate, and more loads in flight only slowed the loads.
+    const int G = d.K / PKG;
+    int nw = G >= 8 ? 8 : (G >= 4 ? 4 : (G >= 2 ? 2 : 1));
+    switch (nw) {
+        case 8: hipLaunchKernelGGL((gemm_panel_kernel<8, 1>), dim3(a.total), dim3(8 * 64), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL((gemm_panel_kernel<4, 1>), dim3(a.total), dim3(4 * 64), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((gemm_panel_kernel<2, 1>), dim3(a.total), dim3(2 * 64), 0, stream, a); break;
+        default: hipLaunchKernelGGL((gemm_panel_kernel<1, 1>), dim3(a.total), dim3(64), 0, stream, a); break;
+    }
+    record_plan("panel", d, PT, PT, 1, 16);
+    return hip_check(hipGetLastError(), "gemm_panel_kernel launch");
+}
+
+}  // namespace migemm

@@ -69,6 +69,12 @@ bool skinny_supported(const GemmDesc &d);
 // Supported and B large enough (>= 64 MB) for the streaming kernel to beat the others.
 bool skinny_preferred(const GemmDesc &d);
 int launch_gemm_small(hipStream_t stream, const GemmDesc &d);
+// A K-contiguous, B N-contiguous, K % 8 == 0, N % 4 == 0, 16-byte aligned rows
+// (gemm_panel_kernel: 32x32 tiles, operands loaded straight into LDS).
+bool panel_supported(const GemmDesc &d);
+// Supported, and a shape where it beats the small and tiled families.
+bool panel_preferred(const GemmDesc &d);
+int launch_gemm_panel(hipStream_t stream, const GemmDesc &d);
 // True when C has too few 64x64 tiles to occupy the 256 CUs (gemm_small_kernel).
 bool small_preferred(const GemmDesc &d);
 

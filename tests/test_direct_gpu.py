@@ -209,3 +209,41 @@ def test_small_kernel_32x32_tiles_exact(ta, tb):
     finally:
         env.restore()
         _native.set_gemm_policy(prev)
+
+
+# The panel kernel (gemm_panel_kernel: 32x32 tiles, NN, K % 32 == 0, N % 4 == 0): ragged M
+# (1, 17, 33, 63, 65) and N (4, 36, 260), K with 1, 2, 4, 8 and more k-groups (so 1, 2, 4
+# and 8 wavefronts, uneven shares), batches with bias and the accumulating epilogue.
+PANEL_SHAPES = [(1, 32, 4, 1, False, False), (17, 64, 36, 2, True, False),
+                (33, 128, 260, 3, False, True), (63, 256, 100, 1, True, True),
+                (65, 1536, 4096, 1, True, False), (64, 800, 516, 2, False, False),
+                (128, 2048, 260, 1, True, True), (40, 4096, 68, 1, False, False)]
+
+
+@pytest.mark.parametrize("M,K,N,batch,bias,acc", PANEL_SHAPES)
+def test_panel_kernel_exact(M, K, N, batch, bias, acc):
+    from my_pytchon_opencl_lib_amd import _native
+    prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_PANEL)
+    try:
+        say("panel exact", M, K, N, batch, bias, acc)
+        got, expect = run_exact(M, K, N, 0, 0, batch=batch, bias=bias, acc=acc,
+                                seed=M + 3 * K + 7 * N)
+        assert _native.last_plan().startswith("panel"), _native.last_plan()
+        assert np.array_equal(got, expect)
+    finally:
+        _native.set_gemm_policy(prev)
+
+
+def test_panel_kernel_falls_back_outside_its_shapes():
+    """K % 32 != 0, N % 4 != 0, a transposed operand or unaligned rows: the PANEL policy
+    runs the dispatcher's own choice instead, with the same result."""
+    from my_pytchon_opencl_lib_amd import _native
+    prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_PANEL)
+    try:
+        for M, K, N, ta, tb in [(64, 100, 256, 0, 0), (64, 128, 258, 0, 0), (64, 128, 256, 1, 0),
+                                (64, 128, 256, 0, 1)]:
+            got, expect = run_exact(M, K, N, ta, tb, seed=K + N + ta)
+            assert not _native.last_plan().startswith("panel"), (M, K, N, ta, tb)
+            assert np.array_equal(got, expect)
+    finally:
+        _native.set_gemm_policy(prev)

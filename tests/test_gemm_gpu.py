@@ -570,7 +570,8 @@ def test_random_strided_batched_exact(nncl, policy):
     C's padding is NaN as well and must stay NaN (no write outside [M x N])."""
     import ctypes
     from my_pytchon_opencl_lib_amd import _native
-    rng = np.random.default_rng(20260 + {"auto": 0, "small": 1, "tiled": 2, "skinny": 3}[policy])
+    seeds = {"auto": 0, "small": 1, "tiled": 2, "skinny": 3, "panel": 4}
+    rng = np.random.default_rng(20260 + seeds[policy])
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     for i in range(60):
         c = _random_case(rng)
