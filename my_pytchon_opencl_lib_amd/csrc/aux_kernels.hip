@@ -13,16 +13,62 @@ namespace {
 
 constexpr int MAXD = 10;
 
+// Division by an invariant divisor 1 <= d < 2^31 for numerators n < 2^31 (Granlund and
+// Montgomery, "Division by Invariant Integers using Multiplication", PLDI 1994, with the
+// round-up multiplier): with l = ceil(log2 d) and p = 31 + l, mult = ceil(2^p / d) fits 32
+// bits and n / d = floor(n * mult / 2^p), because the excess n * (mult * d - 2^p) / (d * 2^p)
+// is below n / 2^p < 2^-l <= 1 / d. One multiply-high and a shift instead of the long
+// software sequence of a 64-bit division (d = 1 passes n through: l would be 0).
+struct FastDiv {
+    uint32_t d, mult, shift;  // shift = p - 32
+};
+
+FastDiv make_fastdiv(uint32_t d) {
+    FastDiv f{d, 0, 0};
+    if (d <= 1) return f;
+    uint32_t l = 0;
+    while (((uint64_t)1 << l) < d) ++l;
+    const uint64_t p = 31 + l;
+    f.mult = (uint32_t)((((uint64_t)1 << p) + d - 1) / d);
+    f.shift = (uint32_t)(p - 32);
+    return f;
+}
+
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv &f) {
+    return f.d == 1 ? n : (__umulhi(n, f.mult) >> f.shift);
+}
+
 struct PermuteArgs {
     const float *src;
     float *dst;
     int64_t total;
     int ndim;
+    int narrow;  // total < 2^31: every index and offset fits 32 bits
     int64_t dst_dims[MAXD];
     int64_t src_stride_of_dst_axis[MAXD];  // stride in src of the axis placed at dst axis i
+    FastDiv div[MAXD];                     // dst_dims as invariant divisors (narrow only)
 };
 
+// dst[t] = src[offset of t's destination coordinates], coordinates from the last axis
+// (permute.cl:2-8,11-50). Tensors under 2^31 elements unpack t with 32-bit invariant
+// divisions: with one 64-bit division and remainder per axis per element the kernel was
+// bound by integer arithmetic, not by memory.
 __global__ void __launch_bounds__(256) permute_gather_kernel(PermuteArgs a) {
+    if (a.narrow) {
+        const uint32_t total = (uint32_t)a.total;
+        const uint32_t step = gridDim.x * blockDim.x;
+        for (uint32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < total; t += step) {
+            uint32_t rem = t;
+            uint32_t off = 0;
+            for (int i = a.ndim - 1; i >= 0; --i) {
+                const uint32_t q = fast_div(rem, a.div[i]);
+                off += (rem - q * a.div[i].d) * (uint32_t)a.src_stride_of_dst_axis[i];
+                rem = q;
+            }
+            a.dst[t] = a.src[off];
+        }
+        return;
+    }
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
     for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < a.total; t += step) {
         int64_t rem = t;
@@ -87,7 +133,8 @@ __global__ void __launch_bounds__(256) column_sum_kernel(const float *__restrict
     const int vecs = (inner + VW - 1) / VW;
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= (int64_t)outer * vecs) return;
-    const int o = (int)(t / vecs);
+    // 32-bit division where it fits (a 64-bit one is a long software sequence)
+    const int o = t <= INT32_MAX ? (int)((uint32_t)t / (uint32_t)vecs) : (int)(t / vecs);
     const int i0 = (int)(t - (int64_t)o * vecs) * VW;
     const int cnt = inner - i0 < VW ? inner - i0 : VW;
     const int c = blockIdx.y;
@@ -132,9 +179,12 @@ __global__ void __launch_bounds__(256) shift_rows_kernel(const float *__restrict
     const int64_t step = (int64_t)gridDim.x * blockDim.x * VW;
     for (int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * VW; i < total;
          i += step) {
-        const int64_t t = i / hidden;
+        // token index, by 32-bit division where it fits
+        const int64_t t = i <= INT32_MAX ? (int64_t)((uint32_t)i / (uint32_t)hidden) : i / hidden;
+        const int step_in_seq = t <= INT32_MAX ? (int)((uint32_t)t % (uint32_t)seq_len)
+                                               : (int)(t % seq_len);
         vec v = {};
-        if (t % seq_len != 0) __builtin_memcpy(&v, H + i - hidden, sizeof(vec));
+        if (step_in_seq != 0) __builtin_memcpy(&v, H + i - hidden, sizeof(vec));
         __builtin_memcpy(Hp + i, &v, sizeof(vec));
     }
 }
@@ -172,9 +222,11 @@ int launch_permute(hipStream_t stream, const float *src, float *dst, const int *
         src_strides[i] = st;
         st *= src_dims[i];
     }
+    a.narrow = total <= INT32_MAX;
     for (int i = 0; i < MAXD; ++i) {
         a.dst_dims[i] = i < num_dims ? src_dims[axes[i]] : 1;
         a.src_stride_of_dst_axis[i] = i < num_dims ? src_strides[axes[i]] : 0;
+        a.div[i] = make_fastdiv(a.narrow ? (uint32_t)a.dst_dims[i] : 1u);
     }
     int64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;

@@ -192,6 +192,19 @@ def test_permute_generic_and_transpose(nncl):
     assert np.array_equal(host(nncl.Permute(dev(x), [0, 2, 1])), x.transpose(0, 2, 1))
 
 
+@pytest.mark.parametrize("shape,axes", [((3, 100003, 2), (1, 2, 0)),
+                                        ((70001, 3, 5), (2, 0, 1)),
+                                        ((2, 3, 65537, 4), (2, 3, 1, 0)),
+                                        ((1, 2097153), (1, 0)),
+                                        ((7, 1, 1, 131071), (3, 0, 2, 1))])
+def test_permute_large_axes(nncl, shape, axes):
+    """Axes of 65537-2097153 (odd, prime, 2^k + 1 sizes) through the generic gather: its
+    invariant-divisor index unpacking must equal numpy's transpose exactly."""
+    x = np.arange(int(np.prod(shape)), dtype=np.float32).reshape(shape)
+    say("permute large", shape, axes)
+    assert np.array_equal(host(nncl.Permute(dev(x), list(axes))), x.transpose(axes))
+
+
 def test_sum_and_bias_backward_bit_exact(nncl):
     """Up to 256 summed rows the library adds in the reference's order (one ascending
     chain from +0.0f, reduce_sum_axis.cl:3-27, linear.cl:149-168): bit-identical."""
