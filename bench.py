@@ -26,6 +26,7 @@ profiles/*.md summaries are made with them).
 """
 import argparse
 import csv
+import ctypes
 import glob
 import json
 import os
@@ -57,6 +58,11 @@ CONFIGS = {
                          4 * (64 * 1536 + 1536 * 4096 + 64 * 4096 + 4096), "mfma"),
     "5a_ragged": (2 * 1000 * 3000 * 777, 4 * (1000 * 777 + 777 * 3000 + 1000 * 3000), "mfma"),
     "5b_gemv": (2 * 4096 * 11008, 4 * (4096 + 4096 * 11008 + 11008), "hbm"),
+    # tensor_permute (cl_kernels/permute.cl:11-50): not a BASELINE config, but the path's
+    # layout row; read + write of the tensor. [1,0] of a 4096^2 operand is what BmmOp.Backward
+    # materialised for config 4 (BmmOp.cs:44-60); the 4-D head split runs the generic gather.
+    "a5_permute_4096_t": (0, 2 * 4 * 4096 * 4096, "hbm"),
+    "a5_permute_heads_0213": (0, 2 * 4 * 32 * 128 * 16 * 64, "hbm"),
 }
 
 
@@ -73,10 +79,11 @@ def parse():
     p.add_argument("--no-reference", action="store_true",
                    help="skip the reference bmm_tiled run on this GPU")
     p.add_argument("--pmc-target", nargs="?", const="4096",
-                   choices=["4096", "1", "2a", "2b", "3", "5a", "5b", "floor"],
+                   choices=["4096", "1", "2a", "2b", "3", "5a", "5b", "a5t", "a5h", "floor"],
                    help="run only one workload for rocprofv3 --pmc passes, each 3 times: '4096' "
                         "the three 4096^3 forms, '1' / '2a' / '2b' / '3' / '5a' / '5b' that "
-                        "BASELINE config, 'floor' the one-element fill kernel; then a 256 MiB "
+                        "BASELINE config, 'a5t' / 'a5h' the 4096^2 [1,0] and the [0,2,1,3] "
+                        "head-split permutes, 'floor' the one-element fill kernel; then a 256 MiB "
                         "device copy 3 times (the reference for scaling FETCH_SIZE / "
                         "WRITE_SIZE to bytes)")
     p.add_argument("--summarize-trace", metavar="DIR",
@@ -328,6 +335,12 @@ def pmc_target(torch, nncl, which="4096"):
         copies = [r(4096, 11008) for _ in range(3)]
         y = torch.empty(1, 11008, device=dev)
         calls = [lambda c=c: nncl.gemm(x, c, out=y) for c in copies]
+    elif which == "a5t":
+        T = r(4096, 4096)
+        calls = [lambda: nncl.Permute(T, [1, 0])] * 3
+    elif which == "a5h":
+        H = r(32, 128, 16, 64)
+        calls = [lambda: nncl.Permute(H, [0, 2, 1, 3])] * 3
     elif which == "floor":
         z = torch.empty(1, device=dev)
         calls = [lambda: z.fill_(1.0)] * 3
@@ -500,6 +513,27 @@ def measure_all_configs(torch, nncl, _native, reps=20):
     y = torch.empty(1, 11008, device=dev)
     f5b = [lambda c=c: nncl.gemm(x, c, out=y) for c in copies]
     rec("5b_gemv", timed(f5b, per=7), f5b)
+    del copies
+
+    def permute_into(src, dst, axes):
+        dims = (ctypes.c_int * src.dim())(*src.shape)
+        ax = (ctypes.c_int * src.dim())(*axes)
+        _native.call("migemm_tensor_permute",
+                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream),
+                     ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), dims, ax,
+                     src.dim())
+
+    T, Tt = r(4096, 4096), torch.empty(4096, 4096, device=dev)
+    fpt = [lambda: permute_into(T, Tt, [1, 0])]
+    rec("a5_permute_4096_t", timed(fpt), fpt)
+    H, Hp = r(32, 128, 16, 64), torch.empty(32, 16, 128, 64, device=dev)
+    fph = [lambda: permute_into(H, Hp, [0, 2, 1, 3])]
+    rec("a5_permute_heads_0213", timed(fph), fph)
+    # the floor of a kernel that must read its input before it writes: a torch device copy
+    # of 256 KB (one 256^2 operand) replayed the same way
+    c0, c1 = r(256, 256), torch.empty(256, 256, device=dev)
+    out["copy_floor"] = {"us": round(timed([lambda: c1.copy_(c0)], per=100) * 1e3, 2),
+                         "kernel": "torch copy of 256 KB, graph-replayed back to back"}
     return out
 
 

@@ -50,10 +50,16 @@ struct PermuteArgs {
 };
 
 // dst[t] = src[offset of t's destination coordinates], coordinates from the last axis
-// (permute.cl:2-8,11-50). Tensors under 2^31 elements unpack t with 32-bit invariant
-// divisions: with one 64-bit division and remainder per axis per element the kernel was
-// bound by integer arithmetic, not by memory.
+// (permute.cl:2-8,11-50), on the canonical form built by launch_permute. Element t is a
+// group of VW floats (VW = 4 when the innermost destination axis is contiguous in the source
+// too); total, dims and strides are in those units. Tensors under 2^31 elements unpack t
+// with 32-bit invariant divisions: with one 64-bit division and remainder per axis per
+// element the kernel was bound by integer arithmetic, not by memory.
+template <int VW>
 __global__ void __launch_bounds__(256) permute_gather_kernel(PermuteArgs a) {
+    typedef float vec __attribute__((ext_vector_type(VW)));
+    const vec *src = reinterpret_cast<const vec *>(a.src);
+    vec *dst = reinterpret_cast<vec *>(a.dst);
     if (a.narrow) {
         const uint32_t total = (uint32_t)a.total;
         const uint32_t step = gridDim.x * blockDim.x;
@@ -65,7 +71,7 @@ __global__ void __launch_bounds__(256) permute_gather_kernel(PermuteArgs a) {
                 off += (rem - q * a.div[i].d) * (uint32_t)a.src_stride_of_dst_axis[i];
                 rem = q;
             }
-            a.dst[t] = a.src[off];
+            dst[t] = src[off];
         }
         return;
     }
@@ -79,7 +85,7 @@ __global__ void __launch_bounds__(256) permute_gather_kernel(PermuteArgs a) {
             rem /= d;
             off += c * a.src_stride_of_dst_axis[i];
         }
-        a.dst[t] = a.src[off];
+        dst[t] = src[off];
     }
 }
 
@@ -193,45 +199,81 @@ __global__ void __launch_bounds__(256) shift_rows_kernel(const float *__restrict
 
 int launch_permute(hipStream_t stream, const float *src, float *dst, const int *src_dims,
                    const int *axes, int num_dims, int64_t total) {
-    // Batched transpose of the last two axes with every leading axis in place.
-    bool last2 = num_dims >= 2 && axes[num_dims - 1] == num_dims - 2 &&
-                 axes[num_dims - 2] == num_dims - 1;
-    for (int i = 0; i + 2 < num_dims && last2; ++i) last2 = axes[i] == i;
-    if (last2) {
-        const int R = src_dims[num_dims - 2];
-        const int Cc = src_dims[num_dims - 1];
-        int64_t batch = 1;
-        for (int i = 0; i + 2 < num_dims; ++i) batch *= src_dims[i];
-        const int tiles_r = (R + 31) / 32;
-        const int tiles_c = (Cc + 31) / 32;
-        if (batch <= 65535 && (int64_t)tiles_r * tiles_c <= INT32_MAX) {
-            hipLaunchKernelGGL(transpose_kernel, dim3(tiles_r * tiles_c, (unsigned)batch),
-                               dim3(256), 0, stream, src, dst, R, Cc, tiles_c);
-            record_plan(PlanRecord{"transpose", 32, 32, 1, 0, R, Cc, 0, (int)batch, false, false});
-            return hip_check(hipGetLastError(), "transpose_kernel launch");
-        }
-    }
-    PermuteArgs a;
-    a.src = src;
-    a.dst = dst;
-    a.total = total;
-    a.ndim = num_dims;
+    // Canonical form: size-1 axes dropped, and each run of destination axes that lie
+    // consecutively and in order in the source merged into one axis (the outer one's source
+    // stride is the inner one's stride times its size). [32,128,16,64] by (0,2,1,3) stays
+    // 4-D; [B,R,C] by (0,2,1) is a batched transpose; an identity permutation is one axis.
     int64_t src_strides[MAXD];
     int64_t st = 1;
     for (int i = num_dims - 1; i >= 0; --i) {
         src_strides[i] = st;
         st *= src_dims[i];
     }
-    a.narrow = total <= INT32_MAX;
+    int64_t cd[MAXD], cs[MAXD];
+    int nd = 0;
+    for (int i = 0; i < num_dims; ++i) {
+        const int64_t d = src_dims[axes[i]];
+        const int64_t str = src_strides[axes[i]];
+        if (d == 1) continue;
+        if (nd > 0 && cs[nd - 1] == str * d) {
+            cd[nd - 1] *= d;
+            cs[nd - 1] = str;
+        } else {
+            cd[nd] = d;
+            cs[nd] = str;
+            ++nd;
+        }
+    }
+    if (nd == 0) {  // a single element
+        cd[0] = 1;
+        cs[0] = 1;
+        nd = 1;
+    }
+    // Batched transpose of the last two axes with every leading axis in place: [R, C] ->
+    // [C, R] is dst axes (C: stride 1, R: stride C), leading batch axis of stride R * C.
+    const bool t2 = nd == 2 && cs[0] == 1 && cs[1] == cd[0];
+    const bool t3 = nd == 3 && cs[1] == 1 && cs[2] == cd[1] && cs[0] == cd[1] * cd[2];
+    if (t2 || t3) {
+        const int64_t batch = t3 ? cd[0] : 1;
+        const int64_t R = cd[nd - 1], Cc = cd[nd - 2];
+        const int64_t tiles_r = (R + 31) / 32;
+        const int64_t tiles_c = (Cc + 31) / 32;
+        if (batch <= 65535 && tiles_r * tiles_c <= INT32_MAX) {
+            hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)(tiles_r * tiles_c),
+                                                      (unsigned)batch),
+                               dim3(256), 0, stream, src, dst, (int)R, (int)Cc, (int)tiles_c);
+            record_plan(PlanRecord{"transpose", 32, 32, 1, 0, (int)R, (int)Cc, 0, (int)batch,
+                                   false, false});
+            return hip_check(hipGetLastError(), "transpose_kernel launch");
+        }
+    }
+    // 16-byte elements when the innermost destination axis is the source's contiguous one
+    // and holds whole groups of 4 (every other stride is then a multiple of 4 as well)
+    const int vw = (cs[nd - 1] == 1 && cd[nd - 1] % 4 == 0 && ((uintptr_t)src & 15) == 0 &&
+                    ((uintptr_t)dst & 15) == 0)
+                       ? 4
+                       : 1;
+    PermuteArgs a;
+    a.src = src;
+    a.dst = dst;
+    a.total = total / vw;
+    a.ndim = nd;
+    a.narrow = a.total <= INT32_MAX;
     for (int i = 0; i < MAXD; ++i) {
-        a.dst_dims[i] = i < num_dims ? src_dims[axes[i]] : 1;
-        a.src_stride_of_dst_axis[i] = i < num_dims ? src_strides[axes[i]] : 0;
+        a.dst_dims[i] = i < nd ? (i == nd - 1 ? cd[i] / vw : cd[i]) : 1;
+        // in units of vw floats; with vw = 4 the innermost axis is contiguous (stride 1)
+        a.src_stride_of_dst_axis[i] = i < nd ? cs[i] / (i == nd - 1 ? 1 : vw) : 0;
         a.div[i] = make_fastdiv(a.narrow ? (uint32_t)a.dst_dims[i] : 1u);
     }
-    int64_t blocks = (total + 255) / 256;
+    int64_t blocks = (a.total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(permute_gather_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
-    record_plan(PlanRecord{"permute_gather", 0, 0, 1, 0, 0, 0, 0, num_dims, false, false});
+    if (vw == 4)
+        hipLaunchKernelGGL(permute_gather_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                           a);
+    else
+        hipLaunchKernelGGL(permute_gather_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                           a);
+    record_plan(PlanRecord{"permute_gather", 0, 0, 1, 4 * vw, 0, 0, 0, nd, false, false});
     return hip_check(hipGetLastError(), "permute_gather_kernel launch");
 }
 

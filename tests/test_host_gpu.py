@@ -192,6 +192,25 @@ def test_permute_generic_and_transpose(nncl):
     assert np.array_equal(host(nncl.Permute(dev(x), [0, 2, 1])), x.transpose(0, 2, 1))
 
 
+def test_permute_canonical_forms(nncl):
+    """Size-1 axes, runs of axes that stay adjacent (merged into one), identity permutations,
+    batched transposes that only appear after merging, the 16-byte path (innermost axis
+    contiguous in both layouts, a multiple of 4 long) and a source 4 bytes off 16-byte
+    alignment (which must take the 4-byte path): each equals numpy exactly."""
+    cases = [((32, 128, 16, 64), (0, 2, 1, 3)), ((4, 1, 5), (0, 2, 1)), ((1, 1, 1), (2, 0, 1)),
+             ((6, 7, 8), (0, 1, 2)), ((2, 3, 4, 5), (0, 1, 3, 2)), ((2, 3, 4, 5), (2, 3, 0, 1)),
+             ((3, 1, 4, 1, 8), (4, 2, 0, 3, 1)), ((5, 6, 7, 8), (1, 0, 2, 3)),
+             ((2, 2, 3, 3, 4), (3, 4, 0, 1, 2)), ((9, 12), (1, 0)), ((7, 5, 12), (1, 0, 2))]
+    for shape, axes in cases:
+        x = np.arange(int(np.prod(shape)), dtype=np.float32).reshape(shape)
+        say("permute canonical", shape, axes)
+        assert np.array_equal(host(nncl.Permute(dev(x), list(axes))), x.transpose(axes))
+        base = torch.empty(x.size + 1, dtype=torch.float32, device="cuda:0")
+        xs = base[1:].view(shape)  # data pointer 4 bytes past a 16-byte boundary
+        xs.copy_(torch.from_numpy(x))
+        assert np.array_equal(host(nncl.Permute(xs, list(axes))), x.transpose(axes))
+
+
 @pytest.mark.parametrize("shape,axes", [((3, 100003, 2), (1, 2, 0)),
                                         ((70001, 3, 5), (2, 0, 1)),
                                         ((2, 3, 65537, 4), (2, 3, 1, 0)),
