@@ -439,9 +439,10 @@ def summarize_trace(directory, steps, warmup):
     print("\n".join(lines))
 
 
-def measure_all_configs(torch, nncl, _native, reps=20):
+def measure_all_configs(torch, nncl, _native, calls=100):
     """Per-config device time per call, from HIP events around a HIP graph that replays
-    back-to-back calls (so host launch overhead is not measured), 5 replays averaged. Inputs
+    `calls` back-to-back calls (so host launch overhead is not measured, and the graph's own
+    launch, ~8 us, is spread over 100 calls as for the floor), 5 replays averaged. Inputs
     rotate where BASELINE repeats a config over many inputs (config 3: 100 timesteps) or the
     working set must exceed the 256 MB MALL (config 5b: three copies of B). The launch floor
     is a one-element fill kernel replayed the same way."""
@@ -453,7 +454,7 @@ def measure_all_configs(torch, nncl, _native, reps=20):
     cap = torch.cuda.Stream()  # the capturing stream: its own library workspace
 
     def timed(fns, per=None):
-        per = per or max(1, reps // len(fns))
+        per = per or max(1, calls // len(fns))
         with torch.cuda.stream(cap):  # sizes cap's workspace before the capture
             for f in fns:
                 f()
@@ -471,7 +472,7 @@ def measure_all_configs(torch, nncl, _native, reps=20):
         return t.mean_ms() / (per * len(fns))
 
     z = torch.empty(1, device=dev)
-    floor_us = timed([lambda: z.fill_(1.0)], per=100) * 1e3
+    floor_us = timed([lambda: z.fill_(1.0)]) * 1e3
     out["launch_floor"] = {"us": round(floor_us, 2),
                            "kernel": "torch fill of 1 element, graph-replayed back to back"}
 
@@ -512,7 +513,7 @@ def measure_all_configs(torch, nncl, _native, reps=20):
     copies = [r(4096, 11008) for _ in range(3)]  # 541 MB > the 256 MB MALL
     y = torch.empty(1, 11008, device=dev)
     f5b = [lambda c=c: nncl.gemm(x, c, out=y) for c in copies]
-    rec("5b_gemv", timed(f5b, per=7), f5b)
+    rec("5b_gemv", timed(f5b), f5b)
     del copies
 
     def permute_into(src, dst, axes):
@@ -532,7 +533,7 @@ def measure_all_configs(torch, nncl, _native, reps=20):
     # the floor of a kernel that must read its input before it writes: a torch device copy
     # of 256 KB (one 256^2 operand) replayed the same way
     c0, c1 = r(256, 256), torch.empty(256, 256, device=dev)
-    out["copy_floor"] = {"us": round(timed([lambda: c1.copy_(c0)], per=100) * 1e3, 2),
+    out["copy_floor"] = {"us": round(timed([lambda: c1.copy_(c0)]) * 1e3, 2),
                          "kernel": "torch copy of 256 KB, graph-replayed back to back"}
     return out
 

@@ -13,31 +13,7 @@ namespace {
 
 constexpr int MAXD = 10;
 
-// Division by an invariant divisor 1 <= d < 2^31 for numerators n < 2^31 (Granlund and
-// Montgomery, "Division by Invariant Integers using Multiplication", PLDI 1994, with the
-// round-up multiplier): with l = ceil(log2 d) and p = 31 + l, mult = ceil(2^p / d) fits 32
-// bits and n / d = floor(n * mult / 2^p), because the excess n * (mult * d - 2^p) / (d * 2^p)
-// is below n / 2^p < 2^-l <= 1 / d. One multiply-high and a shift instead of the long
-// software sequence of a 64-bit division (d = 1 passes n through: l would be 0).
-struct FastDiv {
-    uint32_t d, mult, shift;  // shift = p - 32
-};
-
-FastDiv make_fastdiv(uint32_t d) {
-    FastDiv f{d, 0, 0};
-    if (d <= 1) return f;
-    uint32_t l = 0;
-    while (((uint64_t)1 << l) < d) ++l;
-    const uint64_t p = 31 + l;
-    f.mult = (uint32_t)((((uint64_t)1 << p) + d - 1) / d);
-    f.shift = (uint32_t)(p - 32);
-    return f;
-}
-
-__device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv &f) {
-    return f.d == 1 ? n : (__umulhi(n, f.mult) >> f.shift);
-}
-
+// FastDiv / make_fastdiv / fast_div: migemm_internal.h.
 struct PermuteArgs {
     const float *src;
     float *dst;

@@ -387,6 +387,7 @@ int launch_direct(hipStream_t s, TiledArgs &a) {
         return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm: %lld tiles exceed one launch",
                          (long long)total);
     a.total = (int)total;
+    set_tile_divisors(a);
     hipLaunchKernelGGL((gemm_direct_kernel<BM, BN, WM, WN, AKC, BKC, BK, S, D, OCC, WA, WB>),
                        dim3(a.total),
                        dim3(WM * WN * 64), 0, s, a);

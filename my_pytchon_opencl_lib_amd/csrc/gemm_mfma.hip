@@ -476,6 +476,7 @@ int launch_tiles(hipStream_t s, TiledArgs &a, bool akc, bool bkc, bool av, bool 
         return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm: %lld tiles exceed one launch",
                          (long long)total);
     a.total = (int)total;
+    set_tile_divisors(a);
     if constexpr (ONLY >= 0)
         return launch_vec<BM, BN, BK, WM, WN, (ONLY >> 1) != 0, (ONLY & 1) != 0>(s, a, av, bv);
     else

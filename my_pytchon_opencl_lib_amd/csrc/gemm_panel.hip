@@ -47,6 +47,8 @@ struct PanelArgs {
     int M, N, K;
     int tiles_m, tiles_n, batch, total;
     int accumulate;
+    FastDiv per_batch;  // tiles_m * tiles_n (multiply-high division in the prologue)
+    FastDiv tm_div;     // tiles_m
 };
 
 constexpr int PT = 32;         // output tile edge
@@ -70,11 +72,11 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
 
     // ---- work-group -> (batch, tile); both row tiles of a column block on one XCD ----
     int pid = blockIdx.x;
-    if ((p.total & 7) == 0) pid = (pid & 7) * (p.total >> 3) + (pid >> 3);
-    const int per_batch = p.tiles_m * p.tiles_n;
-    const int b = pid / per_batch;
-    const int t = pid - b * per_batch;
-    const int tn = t / p.tiles_m;
+    // (a select, not a branch: a branch here splits the kernel-argument loads in two rounds)
+    pid = (p.total & 7) == 0 ? (pid & 7) * (p.total >> 3) + (pid >> 3) : pid;
+    const int b = (int)fast_div((uint32_t)pid, p.per_batch);
+    const int t = pid - b * (int)p.per_batch.d;
+    const int tn = (int)fast_div((uint32_t)t, p.tm_div);
     const int tm = t - tn * p.tiles_m;
     const int m0 = __builtin_amdgcn_readfirstlane(tm * PT);
     const int n0 = __builtin_amdgcn_readfirstlane(tn * PT);
@@ -266,6 +268,8 @@ int launch_gemm_panel(hipStream_t stream, const GemmDesc &d) {
         return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm_panel: %lld work-groups", (long long)total);
     a.total = (int)total;
     a.accumulate = d.accumulate;
+    a.per_batch = make_fastdiv((uint32_t)(a.tiles_m * a.tiles_n));
+    a.tm_div = make_fastdiv((uint32_t)a.tiles_m);
     // NW wavefronts split the k-groups (8, two per SIMD, unless K has fewer k-groups), each
     // with one k-group (8 KB) in flight while it multiplies the previous one: 64 KB of LDS.
     // Measured at 64 x 1536 x 4096 (100 rotating inputs, graph replay, us): 8 wavefronts

@@ -55,6 +55,12 @@ struct SmallArgs {
     float *partial;        // [splits][batch][M][N] when splits > 1
     int accumulate;        // C += result instead of C = result
     int m_fast;            // consecutive tiles step along M (else along N)
+    // launch-invariant divisors of the work-group decomposition (multiply-high divisions:
+    // with hardware-less 32-bit divisions the prologue before the first load took ~0.6 us
+    // of the 256^3 GEMM's 2.4 us)
+    FastDiv per_split;     // tiles_m * tiles_n * batch
+    FastDiv per_batch;     // tiles_m * tiles_n
+    FastDiv fast;          // tiles_m if m_fast, else tiles_n
 };
 
 constexpr int KG = 16;       // k values per k-group (4 MFMA steps of 4)
@@ -89,21 +95,16 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(SmallArgs p) {
     // ---- work-group -> (split, batch, tile); consecutive tiles share an XCD ----
     int pid = blockIdx.x;
     const int total = p.total;
-    if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
-    const int per_batch = p.tiles_m * p.tiles_n;
-    const int per_split = per_batch * p.batch;
-    const int split = pid / per_split;
-    pid -= split * per_split;
-    const int b = pid / per_batch;
-    const int t = pid - b * per_batch;
-    int tm, tn;
-    if (p.m_fast) {
-        tn = t / p.tiles_m;
-        tm = t - tn * p.tiles_m;
-    } else {
-        tm = t / p.tiles_n;
-        tn = t - tm * p.tiles_n;
-    }
+    // (a select, not a branch: a branch here splits the kernel-argument loads in two rounds)
+    pid = (total & 7) == 0 ? (pid & 7) * (total >> 3) + (pid >> 3) : pid;
+    const int split = (int)fast_div((uint32_t)pid, p.per_split);
+    pid -= split * (int)p.per_split.d;
+    const int b = (int)fast_div((uint32_t)pid, p.per_batch);
+    const int t = pid - b * (int)p.per_batch.d;
+    const int slow = (int)fast_div((uint32_t)t, p.fast);
+    const int quick = t - slow * (int)p.fast.d;
+    const int tm = p.m_fast ? quick : slow;
+    const int tn = p.m_fast ? slow : quick;
     const int m0 = tm * 16 * MB;
     const int n0 = tn * 16 * NB;
 
@@ -211,7 +212,10 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(SmallArgs p) {
         // groups of an XCD, which read the same A (or B) panel, do not all request the
         // same lines from the same L2 channels at the same time.
         const int nfg = gend - glo;
-        const int rot = (int)((blockIdx.x * 5u) % (unsigned)nfg);
+        // rotation in [0, nfg): the top 10 bits of a multiplicative hash of the work-group
+        // id, scaled (a remainder would be another division in the prologue)
+        const unsigned hash = (blockIdx.x * 2654435761u) >> 22;
+        const int rot = (int)((hash * (unsigned)nfg) >> 10);
         auto kgroup = [&](int i) {  // i-th k-group of the range, i < nfg
             const int x = i + rot;
             return glo + (x >= nfg ? x - nfg : x);
@@ -451,6 +455,9 @@ int launch_gemm_small(hipStream_t stream, const GemmDesc &d) {
     if (total > 0x7fffffff)
         return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm_small: %lld work-groups", (long long)total);
     a.total = (int)total;
+    a.per_split = make_fastdiv((uint32_t)(pl.wgs));
+    a.per_batch = make_fastdiv((uint32_t)(a.tiles_m * a.tiles_n));
+    a.fast = make_fastdiv((uint32_t)(a.m_fast ? a.tiles_m : a.tiles_n));
     a.partial = nullptr;
     if (a.splits > 1) {
         int st = MIGEMM_OK;

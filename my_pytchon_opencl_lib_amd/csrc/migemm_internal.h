@@ -21,6 +21,34 @@ int hip_check(hipError_t e, const char *what);
         if (_rc != MIGEMM_OK) return _rc;                  \
     } while (0)
 
+// Division by an invariant divisor 1 <= d < 2^31 for numerators n < 2^31 (Granlund and
+// Montgomery, "Division by Invariant Integers using Multiplication", PLDI 1994, the
+// n + mulhi form): with l = ceil(log2 d) and m = floor(2^32 (2^l - d) / d) + 1 (< 2^32),
+//   n / d = (mulhi(n, m) + n) >> l,
+// i.e. floor(n * M / 2^(32+l)) with M = 2^32 + m = floor(2^(32+l) / d) + 1, whose excess
+// e = M d - 2^(32+l) <= d keeps n e / 2^(32+l) < 2^31 2^l / 2^(32+l) < 1 / d below the gap
+// to the next multiple of d. The sum cannot overflow (mulhi(n, m) < n < 2^31), and d = 1
+// (m = 1, l = 0) needs no special case, so the division is three instructions without a
+// branch, against the long dependent sequence the GPU runs for a 32-bit division. Kernels
+// take FastDiv values computed on the host for their launch-invariant divisors.
+struct FastDiv {
+    uint32_t d, mult, shift;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+    FastDiv f{d, 1, 0};
+    if (d == 0) return f;
+    uint32_t l = 0;
+    while (((uint64_t)1 << l) < d) ++l;
+    f.mult = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << l) - d)) / d + 1);
+    f.shift = l;
+    return f;
+}
+
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv &f) {
+    return (__umulhi(n, f.mult) + n) >> f.shift;
+}
+
 // Description of one (possibly batched, possibly transposed) fp32 GEMM after
 // validation: C_b = opA(A_b) * opB(B_b) (+ bias).
 struct GemmDesc {

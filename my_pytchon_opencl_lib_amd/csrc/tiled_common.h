@@ -28,7 +28,23 @@ struct TiledArgs {
     int kt_per_split;      // k-tiles per range
     float *partial;        // [splits][batch][M][N] partial sums when splits > 1
     int accumulate;        // C += result instead of C = result
+    // launch-invariant divisors of tile_coord (multiply-high divisions), set by
+    // set_tile_divisors once tiles_m, tiles_n, batch are final
+    FastDiv per_split;     // tiles_m * tiles_n * batch
+    FastDiv per_batch;     // tiles_m * tiles_n
+    FastDiv in_group;      // GROUP * tiles_n
+    FastDiv last_group;    // rows of tiles in the last group of 8 (tiles_m % 8, or 8)
 };
+
+constexpr int TILE_GROUP = 8;  // tile-rows rastered together
+
+inline void set_tile_divisors(TiledArgs &a) {
+    a.per_batch = make_fastdiv((uint32_t)(a.tiles_m * a.tiles_n));
+    a.per_split = make_fastdiv((uint32_t)(a.tiles_m * a.tiles_n * a.batch));
+    a.in_group = make_fastdiv((uint32_t)(TILE_GROUP * a.tiles_n));
+    const int rem = a.tiles_m % TILE_GROUP;
+    a.last_group = make_fastdiv((uint32_t)(rem == 0 ? TILE_GROUP : rem));
+}
 
 struct TileCoord {
     int split, b, m0, n0;
@@ -41,20 +57,24 @@ struct TileCoord {
 template <int BM, int BN>
 __device__ __forceinline__ TileCoord tile_coord(const TiledArgs &p, int pid) {
     const int total = p.total;
-    if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
-    const int per_batch = p.tiles_m * p.tiles_n;
-    const int per_split = per_batch * p.batch;
+    // (a select, not a branch: a branch here splits the kernel-argument loads in two rounds)
+    pid = (total & 7) == 0 ? (pid & 7) * (total >> 3) + (pid >> 3) : pid;
     TileCoord tc;
-    tc.split = pid / per_split;
-    pid -= tc.split * per_split;
-    tc.b = pid / per_batch;
-    const int t = pid - tc.b * per_batch;
-    constexpr int GROUP = 8;
-    const int in_group = GROUP * p.tiles_n;
-    const int first_m = (t / in_group) * GROUP;
-    const int gsz = min(p.tiles_m - first_m, GROUP);
-    const int tm = first_m + (t % in_group) % gsz;
-    const int tn = (t % in_group) / gsz;
+    tc.split = (int)fast_div((uint32_t)pid, p.per_split);
+    pid -= tc.split * (int)p.per_split.d;
+    tc.b = (int)fast_div((uint32_t)pid, p.per_batch);
+    const int t = pid - tc.b * (int)p.per_batch.d;
+    const int grp = (int)fast_div((uint32_t)t, p.in_group);
+    const int first_m = grp * TILE_GROUP;
+    const int tg = t - grp * (int)p.in_group.d;  // index within the group
+    int tm, tn;
+    if (p.tiles_m - first_m >= TILE_GROUP) {  // a whole group of 8 tile-rows
+        tm = first_m + (tg & (TILE_GROUP - 1));
+        tn = tg / TILE_GROUP;
+    } else {  // the last, shorter group
+        tn = (int)fast_div((uint32_t)tg, p.last_group);
+        tm = first_m + tg - tn * (int)p.last_group.d;
+    }
     tc.m0 = tm * BM;
     tc.n0 = tn * BN;
     return tc;
