@@ -206,6 +206,42 @@ def test_config3_lstm_gate_gemm(nncl):
                ref=oracle.lstm_gemm_xw(X, W, bias))
 
 
+def test_config3_all_100_timesteps_and_graph_replay(nncl):
+    """BASELINE config 3 as the bench runs it: 100 timestep inputs x[t] (64 x 1536) through
+    gemm + bias with one W [1536, 4096]. Every step is checked against fp64 (sampled rows of
+    the stacked 6400 x 4096 output, tolerance 1e-5 sqrt(K)); then the 100 calls are captured
+    in a HIP graph and each of three replays must reproduce the eager outputs bit for bit
+    (the kernels are deterministic, and the graph path must not change the plan)."""
+    steps = 100
+    X = oracle.normal((steps * 64, 1536), 22, 0)
+    W = oracle.uniform((1536, 4096), 22, 1, -1 / 32, 1 / 32)
+    bias = oracle.uniform((4096,), 22, 2, -1 / 32, 1 / 32)
+    say("config3 100 timesteps")
+    x, w, b = dev(X).view(steps, 64, 1536), dev(W), dev(bias)
+    eager = torch.empty((steps, 64, 4096), device="cuda:0")
+    for t in range(steps):
+        nncl.gemm(x[t], w, bias=b, out=eager[t])
+    Y = host(eager).reshape(steps * 64, 4096)
+    check_gemm(Y, X, W, 0, 0, bias=bias, M=steps * 64, N=4096, K=1536, lda=1536, ldb=4096,
+               rows=sample_rows(steps * 64, 96))
+    out = torch.full((steps, 64, 4096), float("nan"), device="cuda:0")
+    cap = torch.cuda.Stream()
+    with torch.cuda.stream(cap):
+        for t in range(steps):
+            nncl.gemm(x[t], w, bias=b, out=out[t])
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        for t in range(steps):
+            nncl.gemm(x[t], w, bias=b, out=out[t])
+    for rep in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep} differs from the eager steps"
+
+
 @pytest.mark.parametrize("form", ["NN", "NT", "TN"])
 def test_config4_4096_cube(nncl, form):
     n = 4096
