@@ -111,6 +111,12 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(SmallArgs p) {
     const float *Ab = p.A + (int64_t)b * p.sA;
     const float *Bb = p.B + (int64_t)b * p.sB;
 
+    // The bias of this thread's output column (every element it stores in the epilogue is
+    // in column n0 + tid % (16 NB)), loaded now so its latency overlaps the k loop.
+    const int ncol = n0 + tid % (16 * NB);
+    const float bias_v =
+        p.bias != nullptr && p.splits == 1 && ncol < p.N ? p.bias[ncol] : 0.f;
+
     // Per-lane operand pointers at k-group 0 (rows / columns clamped).
     // AKC: A(i, k) = Ab[i*lda + k]; else A(i, k) = Ab[k*lda + i]. BKC: B(k, n) = Bb[n*ldb + k];
     // else B(k, n) = Bb[k*ldb + n].
@@ -292,7 +298,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_small_kernel(SmallArgs p) {
         const int n = n0 + col;
         if (m < p.M && n < p.N) {
             if (p.splits == 1) {
-                if (p.bias != nullptr) v = v + p.bias[n];
+                if (p.bias != nullptr) v = v + bias_v;  // n = ncol: NW * 64 % (16 NB) == 0
                 float *c = p.C + (int64_t)b * p.sC + (int64_t)m * p.ldc + n;
                 *c = p.accumulate ? *c + v : v;
             } else {
