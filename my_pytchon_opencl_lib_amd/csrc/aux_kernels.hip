@@ -214,7 +214,8 @@ int launch_permute(hipStream_t stream, const float *src, float *dst, const int *
         const int64_t R = cd[nd - 1], Cc = cd[nd - 2];
         const int64_t tiles_r = (R + 31) / 32;
         const int64_t tiles_c = (Cc + 31) / 32;
-        if (batch <= 65535 && tiles_r * tiles_c <= INT32_MAX) {
+        if (batch <= 65535 && R <= INT32_MAX && Cc <= INT32_MAX &&
+            tiles_r * tiles_c <= INT32_MAX) {
             hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)(tiles_r * tiles_c),
                                                       (unsigned)batch),
                                dim3(256), 0, stream, src, dst, (int)R, (int)Cc, (int)tiles_c);
