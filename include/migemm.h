@@ -312,7 +312,7 @@ int migemm_tensor_buffer(const char *tensor_id, size_t bytes, void **ptr);
 /* ------------------------------------------------------------------------------- */
 /* (4) Kernel selection. The reference has one kernel per form (cl_kernels/matmul.cl:8,
  *     :78; cs/cl_kernels/bmm_permute_tiled.cl:7); this library chooses per shape among
- *     three kernel families. The policy is process-wide and exists for tests and tuning:
+ *     kernel families. The policy is process-wide and exists for tests and tuning:
  *     every policy computes the same product within the fp32 tolerance, only the kernel
  *     family (and so the association order of the sums) changes. */
 #define MIGEMM_POLICY_AUTO 0   /* choice by shape (default) */
@@ -321,8 +321,11 @@ int migemm_tensor_buffer(const char *tensor_id, size_t bytes, void **ptr);
 #define MIGEMM_POLICY_SKINNY 3 /* fp32-FMA kernel wherever it applies (M <= 4, B not
                                   transposed), otherwise the AUTO choice */
 #define MIGEMM_POLICY_PANEL 4  /* 32x32-tile panel kernel wherever it applies (A not
-                                  transposed, B not transposed, K % 8 == 0, N % 4 == 0,
-                                  16-byte aligned rows), otherwise the AUTO choice */
+                                  transposed, B not transposed, K % 32 == 0, N % 4 == 0,
+                                  16-byte aligned rows, lda and ldb <= 2^25), otherwise
+                                  the AUTO choice */
+#define MIGEMM_POLICY_TINY 5   /* one wavefront per 16x16 tile over the whole K wherever
+                                  it applies (K <= 80), otherwise the AUTO choice */
 /* Sets the policy; *previous (if not NULL) receives the one it replaces. Calls already
  * enqueued are unaffected. */
 int migemm_set_gemm_policy(int policy, int *previous);

@@ -28,6 +28,7 @@ MIGEMM_POLICY_TILED = 1
 MIGEMM_POLICY_SMALL = 2
 MIGEMM_POLICY_SKINNY = 3
 MIGEMM_POLICY_PANEL = 4
+MIGEMM_POLICY_TINY = 5
 
 # Tuning keys (migemm_set_tuning); 0 = the dispatcher's choice
 MIGEMM_TUNE_TILE = 1

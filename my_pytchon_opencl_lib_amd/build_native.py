@@ -13,7 +13,8 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_PATH = os.path.join(PKG_DIR, "libmigemm.so")
 SOURCES = ["gemm_direct_256.hip", "gemm_direct_128x256.hip", "gemm_direct_128.hip",
            "gemm_direct_64.hip", "gemm_mfma.hip", "api.hip", "gemm_direct.hip", "gemm_small.hip",
-           "gemm_skinny.hip", "aux_kernels.hip", "runtime.hip", "gemm_panel.hip"]
+           "gemm_skinny.hip", "aux_kernels.hip", "runtime.hip", "gemm_panel.hip",
+           "gemm_tiny.hip"]
 ARCH = "gfx950"
 
 

@@ -302,9 +302,13 @@ static int run_gemm(hipStream_t stream, const GemmDesc &desc) {
         case MIGEMM_POLICY_PANEL:
             if (panel_supported(d)) return launch_gemm_panel(stream, d);
             break;
+        case MIGEMM_POLICY_TINY:
+            if (tiny_supported(d)) return launch_gemm_tiny(stream, d);
+            break;
         default: break;
     }
     if (skinny_preferred(d)) return launch_gemm_skinny(stream, d);
+    if (tiny_preferred(d)) return launch_gemm_tiny(stream, d);
     if (panel_preferred(d)) return launch_gemm_panel(stream, d);
     if (small_preferred(d)) return launch_gemm_small(stream, d);
     return launch_gemm_tiled(stream, d);
@@ -772,7 +776,7 @@ int migemm_last_plan(char *buf, size_t len) {
 
 int migemm_set_gemm_policy(int policy, int *previous) {
     clear_error();
-    if (policy < MIGEMM_POLICY_AUTO || policy > MIGEMM_POLICY_PANEL)
+    if (policy < MIGEMM_POLICY_AUTO || policy > MIGEMM_POLICY_TINY)
         return set_error(MIGEMM_ERR_INVALID_ARG, "set_gemm_policy: unknown policy %d", policy);
     const int old = g_policy.exchange(policy);
     if (previous != nullptr) *previous = old;

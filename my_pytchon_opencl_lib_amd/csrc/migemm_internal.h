@@ -102,6 +102,11 @@ int launch_gemm_small(hipStream_t stream, const GemmDesc &d);
 bool panel_supported(const GemmDesc &d);
 // Supported, and a shape where it beats the small and tiled families.
 bool panel_preferred(const GemmDesc &d);
+
+// Short-K kernel (gemm_tiny.hip): one wavefront per 16x16 tile over the whole K <= 80.
+bool tiny_supported(const GemmDesc &d);
+bool tiny_preferred(const GemmDesc &d);
+int launch_gemm_tiny(hipStream_t stream, const GemmDesc &d);
 int launch_gemm_panel(hipStream_t stream, const GemmDesc &d);
 // True when C has too few 64x64 tiles to occupy the 256 CUs (gemm_small_kernel).
 bool small_preferred(const GemmDesc &d);

@@ -20,7 +20,7 @@ def nncl():
     return NnClGlob("cuda:0")
 
 
-POLICIES = {"auto": 0, "tiled": 1, "small": 2, "skinny": 3, "panel": 4}
+POLICIES = {"auto": 0, "tiled": 1, "small": 2, "skinny": 3, "panel": 4, "tiny": 5}
 
 
 @pytest.fixture(params=sorted(POLICIES))

@@ -156,7 +156,7 @@ def test_gemm_policy_set_and_rejected(lib):
     assert prev.value == 0
     assert lib.migemm_set_gemm_policy(0, ctypes.byref(prev)) == 0
     assert prev.value == 2
-    expect(lib.migemm_set_gemm_policy(5, None), INVALID, "policy")
+    expect(lib.migemm_set_gemm_policy(6, None), INVALID, "policy")
     expect(lib.migemm_set_gemm_policy(-1, None), INVALID, "policy")
     assert lib.migemm_set_gemm_policy(0, None) == 0
 

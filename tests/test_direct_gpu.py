@@ -15,7 +15,8 @@ import numpy as np
 import pytest
 import torch
 
-from parity import Tuner, dev, host
+import oracle
+from parity import Tuner, check_gemm, dev, host
 
 pytestmark = pytest.mark.gpu
 
@@ -247,3 +248,54 @@ def test_panel_kernel_falls_back_outside_its_shapes():
             assert np.array_equal(got, expect)
     finally:
         _native.set_gemm_policy(prev)
+
+
+# (M, K, N, batch, bias, accumulate) for the short-K kernel: K = 1, 15, 16, 17 (no full
+# k-group, one, one plus a partial), 33, 64 (config 2a), 79 and 80 (the longest), with ragged
+# M and N around the 16-wide tiles, a batch of 32 and both epilogues.
+TINY_SHAPES = [(1, 1, 1, 1, False, False), (17, 15, 33, 2, True, False),
+               (16, 16, 16, 1, False, True), (33, 17, 47, 3, True, True),
+               (128, 64, 128, 32, False, False), (100, 33, 70, 8, True, False),
+               (255, 79, 129, 1, False, True), (64, 80, 1000, 2, True, True)]
+
+
+@pytest.mark.parametrize("M,K,N,batch,bias,acc", TINY_SHAPES)
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_tiny_kernel_exact(M, K, N, batch, bias, acc, ta, tb):
+    from my_pytchon_opencl_lib_amd import _native
+    prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_TINY)
+    try:
+        say("tiny exact", M, K, N, batch, bias, acc, ta, tb)
+        got, expect = run_exact(M, K, N, ta, tb, batch=batch, bias=bias, acc=acc,
+                                seed=M + 3 * K + 7 * N + ta + 2 * tb)
+        assert _native.last_plan().startswith("tiny"), _native.last_plan()
+        assert np.array_equal(got, expect)
+    finally:
+        _native.set_gemm_policy(prev)
+
+
+def test_tiny_kernel_falls_back_above_k_80():
+    """K = 81: the TINY policy runs the dispatcher's own choice, with the same result."""
+    from my_pytchon_opencl_lib_amd import _native
+    prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_TINY)
+    try:
+        got, expect = run_exact(64, 81, 64, 0, 0, seed=81)
+        assert not _native.last_plan().startswith("tiny"), _native.last_plan()
+        assert np.array_equal(got, expect)
+    finally:
+        _native.set_gemm_policy(prev)
+
+
+def test_tiny_is_the_config2a_choice():
+    """BASELINE config 2a (32 x 128x64 @ 64x128) runs on the short-K kernel under AUTO, and
+    its result is within 1e-5 sqrt(K) of fp64."""
+    from my_pytchon_opencl_lib_amd import _native
+    Q = oracle.normal((32, 128, 64), 1, 0)
+    Kt = oracle.normal((32, 64, 128), 1, 1)
+    say("config 2a plan")
+    c = torch.empty((32, 128, 128), device="cuda")
+    gemm_ex(0, 0, 128, 128, 64, dev(Q), 64, 128 * 64, dev(Kt), 128, 64 * 128, None, c, 128,
+            128 * 128, 32, 0)
+    assert _native.last_plan().startswith("tiny"), _native.last_plan()
+    check_gemm(host(c), Q, Kt, 0, 0, M=128, N=128, K=64, lda=64, ldb=128, sA=128 * 64,
+               sB=64 * 128, batch=32)

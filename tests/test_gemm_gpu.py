@@ -606,7 +606,7 @@ def test_random_strided_batched_exact(nncl, policy):
     C's padding is NaN as well and must stay NaN (no write outside [M x N])."""
     import ctypes
     from my_pytchon_opencl_lib_amd import _native
-    seeds = {"auto": 0, "small": 1, "tiled": 2, "skinny": 3, "panel": 4}
+    seeds = {"auto": 0, "small": 1, "tiled": 2, "skinny": 3, "panel": 4, "tiny": 5}
     rng = np.random.default_rng(20260 + seeds[policy])
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     for i in range(60):
