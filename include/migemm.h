@@ -324,8 +324,9 @@ int migemm_tensor_buffer(const char *tensor_id, size_t bytes, void **ptr);
                                   transposed, B not transposed, K % 32 == 0, N % 4 == 0,
                                   16-byte aligned rows, lda and ldb <= 2^25), otherwise
                                   the AUTO choice */
-#define MIGEMM_POLICY_TINY 5   /* one wavefront per 16x16 tile over the whole K wherever
-                                  it applies (K <= 80), otherwise the AUTO choice */
+#define MIGEMM_POLICY_TINY 5   /* 16x16 tiles of 1, 2 or 4 wavefronts with all operands in
+                                  registers wherever it applies (K <= 80, or K = 96, 128,
+                                  160, 192, 256, 320), otherwise the AUTO choice */
 /* Sets the policy; *previous (if not NULL) receives the one it replaces. Calls already
  * enqueued are unaffected. */
 int migemm_set_gemm_policy(int policy, int *previous);

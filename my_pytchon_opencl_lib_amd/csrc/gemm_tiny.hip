@@ -1,26 +1,26 @@
 // Short-K fp32 GEMM for gfx950 (v_mfma_f32_16x16x4_f32): C = op(A) * op(B) (+ bias) with
-// K <= 80, such as the batch-32 attention score product Q * K^T of matmul.cl:78-135 at
-// BASELINE config 2a (K = 64) or a narrow Linear layer.
+// K <= 320, such as the batch-32 attention products of matmul.cl:78-135 at BASELINE config 2
+// (Q * K^T with K = 64, P * V with K = 128) or a narrow Linear layer.
 //
-// With so short a K the small-output kernel's division of K over the wavefronts of a work-
-// group buys a chain of a few MFMAs per wavefront at the price of an LDS reduction and a
-// barrier, and its wavefronts spend most of their lifetime waiting (wave-level counters).
-// Here one wavefront owns one 16x16 tile of C over the whole K:
-//  * every operand value goes from global memory (L2) straight to registers, all loads of
-//    the wavefront issued before its first MFMA (K <= 80: at most five 16-wide k-groups,
-//    8 to 40 registers);
+// With so short a K the small-output kernel's division of K over eight wavefronts buys a
+// chain of a few MFMAs per wavefront at the price of lane permutations, an LDS reduction and
+// a barrier, and its wavefronts spend most of their lifetime waiting (wave-level counters).
+// Here a 16x16 tile of C is computed by KS = 1, 2 or 4 wavefronts of one work-group, each over
+// a contiguous 1/KS of K (at most five 16-wide k-groups, K <= 80 per wavefront):
+//  * every operand value of a wavefront goes from global memory (L2) straight to registers,
+//    all its loads issued before its first MFMA (8 to 40 registers);
 //  * fragments in the MFMA's own order: in step j of k-group g, lane l supplies row / column
 //    l % 16 at k = 16 g + 4 (l / 16) + j. A K-contiguous operand is one 16-byte load per
 //    k-group (4 rows x 64 contiguous bytes per 16 lanes); an M- or N-contiguous one is four
 //    4-byte loads, 16 lanes covering 64 contiguous bytes of one k-row;
-//  * one accumulator, MFMAs in ascending k: a fixed association order (one fp32 chain per
-//    output over k-steps of 4), no cross-wavefront reduction, no LDS, no barrier;
-//  * four independent tiles per work-group (consecutive tiles along N, so the four
-//    wavefronts read the same rows of A), work-groups dealt to the XCDs in contiguous
-//    chunks;
-//  * edges: rows beyond M and columns beyond N are clamped on load and not stored; the last,
-//    partial k-group (K % 16 != 0) is loaded element by element with k >= K zero in both
-//    operands; bias after the k sum (linear.cl:119-122), then C is written or added to.
+//  * one accumulator per wavefront, MFMAs in ascending k; with KS > 1 the wavefronts' partial
+//    tiles are added through LDS in k order after one barrier: a fixed association order;
+//  * 4 / KS tiles per work-group (consecutive along N, so the wavefronts read the same rows of
+//    A), work-groups dealt to the XCDs in contiguous chunks;
+//  * edges: rows beyond M and columns beyond N are clamped on load and not stored; with KS = 1
+//    the last, partial k-group (K % 16 != 0) is loaded element by element with k >= K zero in
+//    both operands (KS > 1 takes only K a multiple of 16 KS); bias after the k sum
+//    (linear.cl:119-122), then C is written or added to.
 #include <type_traits>
 
 #include "migemm_internal.h"
@@ -44,23 +44,28 @@ struct TinyArgs {
     FastDiv tiles_n;    // tiles along N
 };
 
-constexpr int TT = 16;   // tile edge
-constexpr int TWG = 4;   // wavefronts (tiles) per work-group
-constexpr int TG_MAX = 5;  // full 16-wide k-groups at most (K <= 80)
+constexpr int TT = 16;     // tile edge
+constexpr int TWG = 4;     // wavefronts per work-group
+constexpr int TG_MAX = 5;  // full 16-wide k-groups per wavefront at most (80 values of K)
 
-// G: number of full k-groups (K / 16), a template parameter so every load and MFMA of the
-// wavefront is straight-line code.
-template <bool AKC, bool BKC, int G>
+// G: full k-groups per wavefront (K / (16 KS), or K / 16 plus a partial group with KS = 1),
+// a template parameter so every load and MFMA of the wavefront is straight-line code. KS:
+// wavefronts per tile, each over k in [kp 16 G, (kp + 1) 16 G).
+template <bool AKC, bool BKC, int G, int KS>
 __global__ void __launch_bounds__(TWG * 64) gemm_tiny_kernel(TinyArgs p) {
+    __shared__ f4 red[KS > 1 ? TWG : 1][64];
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
+    const int kp = w % KS;  // this wavefront's part of K
     const int nwg = gridDim.x;
     int wg = blockIdx.x;
     wg = (nwg & 7) == 0 ? (wg & 7) * (nwg >> 3) + (wg >> 3) : wg;
-    const int tile = wg * TWG + w;
-    if (tile >= p.total) return;  // the whole wavefront (the last work-group's spare tiles)
-    const int b = (int)fast_div((uint32_t)tile, p.per_batch);
-    const int t = tile - b * (int)p.per_batch.d;
+    const int tile = wg * (TWG / KS) + w / KS;
+    const bool live = tile < p.total;  // false only for the last work-group's spare tiles
+    if (KS == 1 && !live) return;      // (with KS > 1 every wavefront reaches the barrier)
+    const int tile_c = live ? tile : p.total - 1;
+    const int b = (int)fast_div((uint32_t)tile_c, p.per_batch);
+    const int t = tile_c - b * (int)p.per_batch.d;
     const int tm = (int)fast_div((uint32_t)t, p.tiles_n);
     const int tn = t - tm * (int)p.tiles_n.d;
     const int m0 = tm * TT;
@@ -74,9 +79,12 @@ __global__ void __launch_bounds__(TWG * 64) gemm_tiny_kernel(TinyArgs p) {
     const float *Ab = p.A + (int64_t)b * p.sA;
     const float *Bb = p.B + (int64_t)b * p.sB;
     // A(i, k) = Ab[i*lda + k] (AKC) or Ab[k*lda + i]; B(k, n) = Bb[n*ldb + k] (BKC) or
-    // Bb[k*ldb + n]. pa / pb: this lane's row / column at k = 4 * lq.
-    const float *pa = AKC ? Ab + (int64_t)row * p.lda + 4 * lq : Ab + (int64_t)(4 * lq) * p.lda + row;
-    const float *pb = BKC ? Bb + (int64_t)col * p.ldb + 4 * lq : Bb + (int64_t)(4 * lq) * p.ldb + col;
+    // Bb[k*ldb + n]. pa / pb: this lane's row / column at k = k0 + 4 * lq.
+    const int k0 = kp * G * TT;
+    const float *pa = AKC ? Ab + (int64_t)row * p.lda + k0 + 4 * lq
+                          : Ab + (int64_t)(k0 + 4 * lq) * p.lda + row;
+    const float *pb = BKC ? Bb + (int64_t)col * p.ldb + k0 + 4 * lq
+                          : Bb + (int64_t)(k0 + 4 * lq) * p.ldb + col;
     const int64_t a_g = AKC ? TT : (int64_t)TT * p.lda;  // per k-group
     const int64_t b_g = BKC ? TT : (int64_t)TT * p.ldb;
 
@@ -94,8 +102,8 @@ __global__ void __launch_bounds__(TWG * 64) gemm_tiny_kernel(TinyArgs p) {
         else
             fb[g] = f4{qb[0], qb[p.ldb], qb[2 * p.ldb], qb[3 * p.ldb]};
     }
-    // the partial k-group, issued with the others
-    const bool part = G * TT < p.K;
+    // the partial k-group (KS = 1 only), issued with the others
+    const bool part = KS == 1 && G * TT < p.K;
     f4 xa = {0.f, 0.f, 0.f, 0.f}, xb = {0.f, 0.f, 0.f, 0.f};
     if (part) {
 #pragma unroll
@@ -117,6 +125,14 @@ __global__ void __launch_bounds__(TWG * 64) gemm_tiny_kernel(TinyArgs p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[j], xb[j], acc, 0, 0, 0);
+    }
+
+    if constexpr (KS > 1) {  // add the other parts' tiles in k order
+        red[w][lane] = acc;
+        __syncthreads();
+        if (kp != 0 || !live) return;
+#pragma unroll
+        for (int q = 1; q < KS; ++q) acc += red[w + q][lane];
     }
 
     // lane l, register r: row 4 (l / 16) + r, column l % 16 of the tile
@@ -145,17 +161,18 @@ __global__ void __launch_bounds__(TWG * 64) gemm_tiny_kernel(TinyArgs p) {
     }
 }
 
-template <int G>
+template <int G, int KS>
 int launch_g(hipStream_t st, const TinyArgs &a, bool akc, bool bkc) {
-    const dim3 grid((unsigned)((a.total + TWG - 1) / TWG)), block(TWG * 64);
+    constexpr int TPW = TWG / KS;  // tiles per work-group
+    const dim3 grid((unsigned)((a.total + TPW - 1) / TPW)), block(TWG * 64);
     if (akc && bkc)
-        hipLaunchKernelGGL((gemm_tiny_kernel<true, true, G>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((gemm_tiny_kernel<true, true, G, KS>), grid, block, 0, st, a);
     else if (akc)
-        hipLaunchKernelGGL((gemm_tiny_kernel<true, false, G>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((gemm_tiny_kernel<true, false, G, KS>), grid, block, 0, st, a);
     else if (bkc)
-        hipLaunchKernelGGL((gemm_tiny_kernel<false, true, G>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((gemm_tiny_kernel<false, true, G, KS>), grid, block, 0, st, a);
     else
-        hipLaunchKernelGGL((gemm_tiny_kernel<false, false, G>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((gemm_tiny_kernel<false, false, G, KS>), grid, block, 0, st, a);
     return hip_check(hipGetLastError(), "gemm_tiny_kernel launch");
 }
 
@@ -163,31 +180,56 @@ int64_t tiles16(const GemmDesc &d) {
     return (int64_t)((d.M + TT - 1) / TT) * ((d.N + TT - 1) / TT) * d.batch;
 }
 
+// Wavefronts per tile: 1 for K <= 80 (any K), 2 for K = 96, 128, 160, 4 for K = 192, 256,
+// 320 (whole 16-wide k-groups, at most five per wavefront); 0: not supported.
+int tiny_parts(const GemmDesc &d) {
+    if (d.K <= TG_MAX * TT) return 1;
+    if (d.K % (2 * TT) == 0 && d.K <= 2 * TG_MAX * TT) return 2;
+    if (d.K % (4 * TT) == 0 && d.K <= 4 * TG_MAX * TT) return 4;
+    return 0;
+}
+
 }  // namespace
 
 bool tiny_supported(const GemmDesc &d) {
-    return d.K <= TG_MAX * TT && tiles16(d) <= (int64_t)0x7fffffff - TWG;
+    return tiny_parts(d) > 0 && tiles16(d) <= (int64_t)0x7fffffff - TWG;
 }
 
-// Where the tiny kernel beats the previous choice (graph replay, 50 calls, us, previous /
-// tiny; K in 16..80, M x N from 64 x 64 x 64 batches to 4096 x 4096, NN, NT, TN):
-// 32 x 128 x 64 @ 64 x 128 (config 2a) 4.37 / 3.83; 1024 x 32 x 1024 5.44 / 4.32 (tiled);
-// 32 x 128 x 80 @ 80 x 128 6.63 / 4.06 (the register-staged tiled kernel); 32 x 64 x 128
-// TN 4.65 / 3.62. It loses with few tiles, where the small kernel's k division shortens
-// each wavefront's MFMA chain (64 x 64 x 64 2.18 / 2.78; 256 x 64 x 512 2.86 / 3.03), and on
-// large outputs, where the tiled kernels reuse operands from LDS (2048 x 32 x 2048 9.83 /
-// 10.59; 1024 x 64 x 2048 8.02 / 9.11) -- except at K = 16 (4096 x 16 x 4096 24.5 / 20.5).
+// Where the tiny kernel beats the other families (graph replay, 50 calls, us, previous
+// choice / tiny):
+//  * K <= 80, one wavefront per tile (K in 16..80, M x N from 64 x 64 x 64 batches to
+//    4096 x 4096, NN, NT, TN): 32 x 128 x 64 @ 64 x 128 (config 2a) 4.37 / 3.83; 1024 x 32 x
+//    1024 5.44 / 4.32 (tiled); 32 x 128 x 80 @ 80 x 128 6.63 / 4.06 (the register-staged
+//    tiled kernel); 32 x 64 x 128 TN 4.65 / 3.62. It loses with few tiles, where the small
+//    kernel's k division shortens each wavefront's MFMA chain (64 x 64 x 64 2.18 / 2.78;
+//    256 x 64 x 512 2.86 / 3.03), and on large outputs, where the tiled kernels reuse operands
+//    from LDS (2048 x 32 x 2048 9.83 / 10.59; 1024 x 64 x 2048 8.02 / 9.11) -- except at
+//    K = 16 (4096 x 16 x 4096 24.5 / 20.5).
+//  * K = 96..320, two or four wavefronts per tile (96 shapes, 60 won): 512-2048 tiles, e.g.
+//    32 x 128 x 128 @ 128 x 64 (config 2b) 3.79 / 3.59, 32 x 128 x 96 @ 96 x 128 6.31 / 4.19
+//    and 32 x 128 x 192 TN 8.25 / 6.30 (the register-staged tiled kernel), 4 x 64 x 320 @
+//    320 x 512 5.30 / 3.98. It loses with 256 tiles (256 x 128 x 256 2.63 / 2.90), at 4096
+//    tiles (1024 x 128 x 1024 7.21 / 8.03), with B transposed above K = 192 (32 x 128 x 256
+//    NT 8.51 / 9.30) and where the panel kernel applies (64 x 256 x 4096 4.19 / 4.85), which
+//    is therefore asked first.
 bool tiny_preferred(const GemmDesc &d) {
     if (!tiny_supported(d) || d.M < 16 || d.N < 16) return false;
     const int64_t t = tiles16(d);
-    if (t < (d.K <= 48 ? 512 : 1024)) return false;
-    if (d.K <= 16) return true;
-    return t <= (d.K <= 48 ? 8192 : 4096);
+    if (tiny_parts(d) == 1) {
+        if (t < (d.K <= 48 ? 512 : 1024)) return false;
+        if (d.K <= 16) return true;
+        return t <= (d.K <= 48 ? 8192 : 4096);
+    }
+    if (t < 512 || t > 2048) return false;
+    if (d.transB && d.K > 192) return false;
+    return !panel_preferred(d);
 }
 
 int launch_gemm_tiny(hipStream_t stream, const GemmDesc &d) {
     if (!tiny_supported(d))
-        return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm_tiny: K=%d > %d", d.K, TG_MAX * TT);
+        return set_error(MIGEMM_ERR_UNSUPPORTED,
+                         "gemm_tiny: K=%d (needs K <= 80, or K = 96, 128, 160, 192, 256, 320)",
+                         d.K);
     TinyArgs a;
     a.A = d.A;
     a.B = d.B;
@@ -211,15 +253,30 @@ int launch_gemm_tiny(hipStream_t stream, const GemmDesc &d) {
     const bool akc = !d.transA;
     const bool bkc = d.transB;
     int rc;
-    switch (d.K / TT) {
-        case 0: rc = launch_g<0>(stream, a, akc, bkc); break;
-        case 1: rc = launch_g<1>(stream, a, akc, bkc); break;
-        case 2: rc = launch_g<2>(stream, a, akc, bkc); break;
-        case 3: rc = launch_g<3>(stream, a, akc, bkc); break;
-        case 4: rc = launch_g<4>(stream, a, akc, bkc); break;
-        default: rc = launch_g<5>(stream, a, akc, bkc); break;
+    const int ks = tiny_parts(d);
+    if (ks == 1) {
+        switch (d.K / TT) {
+            case 0: rc = launch_g<0, 1>(stream, a, akc, bkc); break;
+            case 1: rc = launch_g<1, 1>(stream, a, akc, bkc); break;
+            case 2: rc = launch_g<2, 1>(stream, a, akc, bkc); break;
+            case 3: rc = launch_g<3, 1>(stream, a, akc, bkc); break;
+            case 4: rc = launch_g<4, 1>(stream, a, akc, bkc); break;
+            default: rc = launch_g<5, 1>(stream, a, akc, bkc); break;
+        }
+    } else if (ks == 2) {  // K = 96, 128, 160
+        switch (d.K / (2 * TT)) {
+            case 3: rc = launch_g<3, 2>(stream, a, akc, bkc); break;
+            case 4: rc = launch_g<4, 2>(stream, a, akc, bkc); break;
+            default: rc = launch_g<5, 2>(stream, a, akc, bkc); break;
+        }
+    } else {  // K = 192, 256, 320
+        switch (d.K / (4 * TT)) {
+            case 3: rc = launch_g<3, 4>(stream, a, akc, bkc); break;
+            case 4: rc = launch_g<4, 4>(stream, a, akc, bkc); break;
+            default: rc = launch_g<5, 4>(stream, a, akc, bkc); break;
+        }
     }
-    record_plan("tiny", d, TT, TT, 1, 0);
+    record_plan("tiny", d, TT, TT, ks, 0);
     return rc;
 }
 

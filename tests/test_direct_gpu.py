@@ -251,12 +251,16 @@ def test_panel_kernel_falls_back_outside_its_shapes():
 
 
 # (M, K, N, batch, bias, accumulate) for the short-K kernel: K = 1, 15, 16, 17 (no full
-# k-group, one, one plus a partial), 33, 64 (config 2a), 79 and 80 (the longest), with ragged
-# M and N around the 16-wide tiles, a batch of 32 and both epilogues.
+# k-group, one, one plus a partial), 33, 64 (config 2a), 79 and 80 (the longest for one
+# wavefront per tile); K = 96, 128 (config 2b), 160 (two wavefronts per tile) and 192, 256,
+# 320 (four), with ragged M and N around the 16-wide tiles, batches and both epilogues.
 TINY_SHAPES = [(1, 1, 1, 1, False, False), (17, 15, 33, 2, True, False),
                (16, 16, 16, 1, False, True), (33, 17, 47, 3, True, True),
                (128, 64, 128, 32, False, False), (100, 33, 70, 8, True, False),
-               (255, 79, 129, 1, False, True), (64, 80, 1000, 2, True, True)]
+               (255, 79, 129, 1, False, True), (64, 80, 1000, 2, True, True),
+               (47, 96, 65, 3, True, False), (128, 128, 64, 32, False, False),
+               (33, 160, 100, 2, False, True), (1, 192, 17, 1, True, True),
+               (130, 256, 31, 2, True, False), (64, 320, 64, 5, False, False)]
 
 
 @pytest.mark.parametrize("M,K,N,batch,bias,acc", TINY_SHAPES)
@@ -274,16 +278,47 @@ def test_tiny_kernel_exact(M, K, N, batch, bias, acc, ta, tb):
         _native.set_gemm_policy(prev)
 
 
-def test_tiny_kernel_falls_back_above_k_80():
-    """K = 81: the TINY policy runs the dispatcher's own choice, with the same result."""
+def test_tiny_kernel_falls_back_outside_its_k():
+    """K = 81, 112 (not a multiple of 32), 288 (not of 64) and 384: the TINY policy runs the
+    dispatcher's own choice, with the same result."""
     from my_pytchon_opencl_lib_amd import _native
     prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_TINY)
     try:
-        got, expect = run_exact(64, 81, 64, 0, 0, seed=81)
-        assert not _native.last_plan().startswith("tiny"), _native.last_plan()
-        assert np.array_equal(got, expect)
+        for K in (81, 112, 288, 384):
+            got, expect = run_exact(64, K, 64, 0, 0, seed=K)
+            assert not _native.last_plan().startswith("tiny"), (K, _native.last_plan())
+            assert np.array_equal(got, expect)
     finally:
         _native.set_gemm_policy(prev)
+
+
+def test_tiny_split_reduction_is_the_single_wavefront_sum_in_k_order():
+    """K = 128 on two wavefronts per tile: the partial tiles are added in k order, so the
+    result is identical on every call (and for the same operands in any layout)."""
+    from my_pytchon_opencl_lib_amd import _native
+    rng = np.random.default_rng(128)
+    A = rng.standard_normal((4, 100, 128)).astype(np.float32)
+    B = rng.standard_normal((4, 128, 90)).astype(np.float32)
+    prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_TINY)
+    try:
+        outs = []
+        for rep in range(3):
+            c = torch.full((4, 100, 90), float("nan"), device="cuda")
+            gemm_ex(0, 0, 100, 90, 128, dev(A), 128, 100 * 128, dev(B), 90, 128 * 90, None, c,
+                    90, 100 * 90, 4)
+            assert "splits=2" in _native.last_plan(), _native.last_plan()
+            outs.append(host(c))
+        bt = np.ascontiguousarray(np.swapaxes(B, 1, 2))
+        c = torch.full((4, 100, 90), float("nan"), device="cuda")
+        gemm_ex(0, 1, 100, 90, 128, dev(A), 128, 100 * 128, dev(bt), 128, 90 * 128, None, c,
+                90, 100 * 90, 4)
+        outs.append(host(c))
+    finally:
+        _native.set_gemm_policy(prev)
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+    check_gemm(outs[0], A, B, 0, 0, M=100, N=90, K=128, lda=128, ldb=90, sA=100 * 128,
+               sB=128 * 90, batch=4)
 
 
 def test_tiny_is_the_config2a_choice():
