@@ -240,13 +240,16 @@ bool panel_supported(const GemmDesc &d) {
 // 7.2 / 8.5, 128 x 512 x 512 5.3 / 7.0; but 32 x 1024 x 512 7.0 / 6.4 and 64 x 4096 x 1024
 // 19.0 / 12.7 with K split over work-groups). It loses at K = 256 below 192 tiles (4.1-4.4
 // against 3.4-4.0: its fixed cost is higher), above 768 tiles (256 x 512 x 4096 16.1 / 13.7
-// in 64x64 tiles) and at M <= 16, where half of each 32-row tile is empty.
+// in 64x64 tiles) and at M <= 16, where half of each 32-row tile is empty. A later audit
+// (288 shapes, batch 1 / 8 / 32, M and N 64-512, K 384-1024) moved two bounds: K = 384 pays
+// from 128 tiles (batch-8 64 x 384 x 256 5.1 against 5.9 us on the small kernel) and with
+// 32-63 tiles K stops at 768 (256 x 1024 x 128 7.0 against 6.3 us).
 bool panel_preferred(const GemmDesc &d) {
     if (d.M <= 16 || !panel_supported(d)) return false;
     const int64_t tiles = (int64_t)((d.M + PT - 1) / PT) * ((d.N + PT - 1) / PT) * d.batch;
     if (tiles < 16 || tiles > 768) return false;
-    if (d.K < (tiles < 192 ? 512 : 256)) return false;
-    const int kmax = tiles < 32 ? 512 : tiles < 64 ? 1024 : tiles < 128 ? 1536
+    if (d.K < (tiles < 128 ? 512 : tiles < 192 ? 384 : 256)) return false;
+    const int kmax = tiles < 32 ? 512 : tiles < 64 ? 768 : tiles < 128 ? 1536
                      : tiles < 192 ? 2048 : 1 << 30;
     return d.K <= kmax;
 }

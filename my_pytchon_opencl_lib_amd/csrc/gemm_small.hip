@@ -420,6 +420,9 @@ bool small_preferred(const GemmDesc &d) {
             if (d.K <= 1024) return tiles64 < 24 || (whole && tiles64 < 128);
             return tiles64 < 12 || (whole && tiles64 < 80);
         }
+        // (A transposed) up to K = 512 also with a k split at <= 32 tiles: 256 x 512 x 512 TN
+        // 8.0 against 10.3 us tiled, batch-8 128 x 512 x 128 TN 8.1 / 10.3
+        if (d.K <= 512 && tiles64 <= 32) return true;
         if (d.K <= 1024) return tiles64 < 24 || (whole && tiles64 < 80);
         return tiles64 < 12 || (whole && tiles64 < (d.K <= 1536 ? 80 : 48));
     }
