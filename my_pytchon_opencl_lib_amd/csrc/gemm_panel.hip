@@ -246,12 +246,15 @@ bool panel_supported(const GemmDesc &d) {
 // 32-63 tiles K stops at 768 (256 x 1024 x 128 7.0 against 6.3 us).
 bool panel_preferred(const GemmDesc &d) {
     if (d.M <= 16 || !panel_supported(d)) return false;
-    // every 32-row tile streams its columns of B over the whole K: with many rows and a long
-    // K the tiled kernel's 64x64 tiles (split over k) re-read B half as often (768 x 4096 x
-    // 768: 54.6 against 45.8 us; 1024 x 4096 x 768 63.7 / 54.9)
-    if (d.M > 256 && d.K > 1024) return false;
     const int64_t tiles = (int64_t)((d.M + PT - 1) / PT) * ((d.N + PT - 1) / PT) * d.batch;
     if (tiles < 16 || tiles > 768) return false;
+    // Long K with many tiles: every XCD streams the A panels of all its tiles' rows, and the
+    // tiled kernel's 64x64 tiles (split over k) re-read half as much (768 x 4096 x 768: 54.6
+    // against 45.8 us; 1024 x 4096 x 768 63.7 / 54.9; batch-8 256 x 8192 x 256 77.1 / 71.1),
+    // while up to 512 tiles the panel kernel stays ahead with 512 rows (512 x 2048 x 512 11.8
+    // against 15.5; batch-8 512 x 1536 x 128 17.1 / 23.7) and with few rows at 768 tiles
+    // (96 x 4096 x 8192 59.5 / 76.4).
+    if ((d.M > 256 && tiles > 512 && d.K > 1024) || (d.K >= 8192 && tiles >= 512)) return false;
     if (d.K < (tiles < 128 ? 512 : tiles < 192 ? 384 : 256)) return false;
     const int kmax = tiles < 32 ? 512 : tiles < 64 ? 768 : tiles < 128 ? 1536
                      : tiles < 192 ? 2048 : 1 << 30;

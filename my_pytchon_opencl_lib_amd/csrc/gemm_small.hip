@@ -414,7 +414,8 @@ bool small_preferred(const GemmDesc &d) {
         const bool whole = pl.splits == 1;
         if (pl.nb == 2) {  // 32x32 tiles
             if (d.K <= 1024) return tiles64 < 24 || (whole && (tiles64 < 128 || d.K >= 768));
-            return tiles64 < 12 || (whole && (tiles64 < 80 || d.M <= 128));
+            // up to 16 tiles also with a k split (256 x 2048 x 256 9.2 against 10.2 us tiled)
+            return tiles64 <= 16 || (whole && (tiles64 < 80 || d.M <= 128));
         }
         if (!d.transA) {  // 64x16 tiles, A K-contiguous
             if (d.K <= 1024) return tiles64 < 24 || (whole && tiles64 < 128);
@@ -426,7 +427,9 @@ bool small_preferred(const GemmDesc &d) {
         if (d.K <= 1024) return tiles64 < 24 || (whole && tiles64 < 80);
         return tiles64 < 12 || (whole && tiles64 < (d.K <= 1536 ? 80 : 48));
     }
-    return tiles64 <= 8;
+    // longer K: up to 8 tiles, or 16 with A K-contiguous (256 x 8192 x 256 17.7 against
+    // 18.8 us tiled, 512 x 8192 x 128 17.6 / 18.9)
+    return tiles64 <= (d.transA ? 8 : 16);
 }
 
 int launch_gemm_small(hipStream_t stream, const GemmDesc &d) {
