@@ -8,7 +8,8 @@
 //  * A work-group owns a 32x32 tile of C and has NW wavefronts (8, two per SIMD, when K has
 //    8 or more k-groups of 32); wavefront w multiplies the w-th contiguous share of the
 //    k-groups and the NW partial tiles are added in LDS in the order w = 0..NW-1
-//    (deterministic).
+//    (deterministic), each partial written into its own wavefront's ring, so the epilogue
+//    has one barrier.
 //  * The product is computed as C^T = B^T A^T with v_mfma_f32_32x32x2_f32: the MFMA's first
 //    operand is B (lane l supplies column n0 + l%32), its second A (lane l supplies row
 //    m0 + l%32). In step s of each 8-wide sub-group, lanes 0-31 supply k = s and lanes 32-63
@@ -20,9 +21,11 @@
 //    by 4 instructions and the loads ran at ~23 bytes per clock per CU.
 //  * Each wavefront keeps its own LDS ring of D k-groups (shipped D = 1: one k-group in
 //    flight while the previous one is multiplied) and waits for its own loads
-//    (s_waitcnt vmcnt), so the k loop has no barrier. The fragments of k-group i+1 are read
-//    into a second register set during k-group i's last MFMAs. Past the end the loads
-//    re-read the last k-group (never multiplied), so the wait count is constant.
+//    (s_waitcnt vmcnt), so the k loop has no barrier. k-group i's fragments are in
+//    registers before its first MFMA; its slot is refilled after the first 4 of its 16
+//    MFMAs, and k-group i+1's fragments are read into a second register set before the
+//    last 4. Past the end the loads re-read the last k-group (never multiplied), so the
+//    wait count is constant.
 //  * A rows are stored with chunk c of row r in slot c ^ ((r / 2) % 8), which makes the
 //    128-bit fragment reads conflict-free.
 //  * Work-groups are dealt to the 8 XCDs in contiguous chunks, both row tiles of a column
@@ -36,6 +39,9 @@
 
 namespace migemm {
 namespace {
+
+// A 16-byte vector at 4-byte alignment (bias and C rows may start at any float).
+typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
 
 struct PanelArgs {
     const float *A;
@@ -54,7 +60,7 @@ struct PanelArgs {
 constexpr int PT = 32;         // output tile edge
 constexpr int PKG = 32;        // k per k-group: 4 KB of each operand, whole 128-byte lines
 constexpr int PSTAGE = 2048;   // floats per ring stage: B 32 k-rows x 32, then A 32 rows x 32
-constexpr int PRED = PT * 33;  // floats per wavefront's partial tile in the reduction
+constexpr int PRS = 36;        // floats between the rows of a partial tile in the reduction
 
 // A rows in LDS: 32 floats (8 chunks of 16 bytes) per row; chunk c of row r is stored in
 // slot c ^ ((r / 2) % 8), so the 16 rows a 128-bit fragment read phase covers fall on 16
@@ -63,7 +69,7 @@ __device__ __forceinline__ int pa_swz(int r) { return (r >> 1) & 7; }
 
 template <int NW, int D>
 __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
-    static_assert(NW * D * PSTAGE >= NW * PRED, "the reduction reuses the rings");
+    static_assert(D * PSTAGE >= PT * PRS, "a partial tile fits in its wavefront's ring");
     static_assert(8 * (D - 1) < 64, "vmcnt range");
     __shared__ float ring[NW * D * PSTAGE];
 
@@ -88,11 +94,14 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
     const int g0 = min(G, w * per);
     const int ng = min(G, g0 + per) - g0;
 
-    // The bias of this thread's output column (every element a thread stores below is in
-    // column n0 + tid % 32), loaded now: in the epilogue its memory latency was ~0.5 us of
-    // the 64 x 1536 x 4096 gate GEMM's ~8.7 us.
-    const int ncol = n0 + (threadIdx.x & 31);
-    const float bias_v = p.bias != nullptr && ncol < p.N ? p.bias[ncol] : 0.f;
+    // The bias of this thread's 4 output columns (every group a thread stores below starts
+    // at column n0 + 4 (tid % 8)), loaded now: in the epilogue its memory latency was ~0.5 us
+    // of the 64 x 1536 x 4096 gate GEMM's ~8.7 us.
+    f4 bias4 = f4{0.f, 0.f, 0.f, 0.f};
+    {
+        const int nb = n0 + (threadIdx.x & 7) * 4;
+        if (p.bias != nullptr && nb < p.N) bias4 = *reinterpret_cast<const f4u *>(p.bias + nb);
+    }
 
     float *my = ring + w * D * PSTAGE;
     f16 acc;
@@ -172,12 +181,15 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
         read(0, cur);
         for (int i = 0; i < ng; ++i) {
             mma(cur, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            // cur's fragments are all in registers: refill slot i%D after the first 4 MFMAs,
+            // so k-group i+D's loads have 8 MFMAs (and the other wavefront's work) to land
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            issue(i + D, i % D);
+            __builtin_amdgcn_sched_barrier(0);
             mma(cur, 1);
             mma(cur, 2);
             __builtin_amdgcn_sched_barrier(0);
-            // cur's reads of slot i%D are complete (its MFMAs consumed them): refill it
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-            issue(i + D, i % D);
             wait_vmcnt<8 * (D - 1)>();  // k-group i+1 has landed
             read((i + 1) % D, nxt);
             __builtin_amdgcn_sched_barrier(0);
@@ -188,31 +200,35 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
     }
 
     // ---- combine the NW wavefronts in order, add the bias, store ----
-    // acc register r of lane l: C^T row (= column of C) 8(r/4) + 4(l/32) + r%4, C^T
-    // column (= row of C) l%32.
-    __syncthreads();  // every ring is drained and read
-    float *red = ring + w * PRED;
+    // Each wavefront writes its partial tile into its own ring (all of its loads have landed
+    // and its own reads are done), so a single barrier precedes the sum. acc register 4g + j
+    // of lane l is C(row l % 32, column 8g + 4(l / 32) + j); partial rows are 36 floats apart
+    // (16-byte aligned), so a thread adds 4 columns per LDS read.
     {
+        float *red = ring + w * D * PSTAGE;
         const int lo = lane & 31;
         const int hi = lane >> 5;
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-            red[lo * 33 + 8 * (r >> 2) + 4 * hi + (r & 3)] = acc[r];
+        for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<f4 *>(red + lo * PRS + 8 * g + 4 * hi) =
+                f4{acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
     }
     __syncthreads();
     float *Cb = p.C + (int64_t)bb * p.sC;
-    for (int e = threadIdx.x; e < PT * PT; e += NW * 64) {
-        const int mi = e >> 5;
-        const int ni = e & 31;
-        float v = ring[mi * 33 + ni];
+    for (int e = threadIdx.x; e < PT * PT / 4; e += NW * 64) {
+        const int mi = e >> 3;
+        const int nq = (e & 7) * 4;  // = the bias group loaded above: NW * 64 % 8 == 0
+        f4 v = *reinterpret_cast<const f4 *>(ring + mi * PRS + nq);
 #pragma unroll
-        for (int q = 1; q < NW; ++q) v += ring[q * PRED + mi * 33 + ni];
+        for (int q = 1; q < NW; ++q)
+            v += *reinterpret_cast<const f4 *>(ring + q * D * PSTAGE + mi * PRS + nq);
         const int m = m0 + mi;
-        const int n = n0 + ni;  // = ncol: NW * 64 is a multiple of 32
-        if (m < p.M && n < p.N) {
-            if (p.bias != nullptr) v = v + bias_v;
-            float *c = Cb + (int64_t)m * p.ldc + n;
-            *c = p.accumulate ? *c + v : v;
+        const int n = n0 + nq;
+        if (m < p.M && n < p.N) {  // N % 4 == 0: the whole group is inside
+            if (p.bias != nullptr) v = v + bias4;
+            f4u *c = reinterpret_cast<f4u *>(Cb + (int64_t)m * p.ldc + n);
+            if (p.accumulate) v = *c + v;
+            *c = v;
         }
     }
 }
@@ -290,9 +306,13 @@ int launch_gemm_panel(hipStream_t stream, const GemmDesc &d) {
     // with one k-group (8 KB) in flight while it multiplies the previous one: 64 KB of LDS.
     // Measured at 64 x 1536 x 4096 (100 rotating inputs, graph replay, us): 8 wavefronts
     // with 1 / 2 k-groups in flight 9.65 / 10.24, 4 with 2 / 3 / 4 10.86 / 11.01 / 11.86, 16
-    // with 1 10.8; loads issued before instead of after the first 12 MFMAs of each
-    // k-group 10.02 against 10.13. Deeper queues do not pay: the k loop alone (no loads)
-    // runs at ~91 % of the MFMA rate, and more loads in flight only slowed the loads.
+    // with 1 10.8. Deeper queues do not pay: the k loop alone (no loads) runs at ~91 % of
+    // the MFMA rate, and more loads in flight only slowed the loads. Where the refill is
+    // issued (min of 7 graph replays of 100 calls, two processes each, us, after 12 MFMAs
+    // / at the k-group's start / after 4): 64 x 1536 x 4096 9.41 / 9.42 / 9.06, 256 x 512 x
+    // 2048 9.11 / 8.86 / 8.54, 96 x 4096 x 8192 58.6 / 56.8 / 55.3; after 2 or 14 MFMAs
+    // within 1 % of after 4. With the one-barrier epilogue (same harness, another box):
+    // 9.20 -> 9.03, 9.01 -> 8.17 and 57.6 -> 55.1.
     const int G = d.K / PKG;
     int nw = G >= 8 ? 8 : (G >= 4 ? 4 : (G >= 2 ? 2 : 1));
     switch (nw) {

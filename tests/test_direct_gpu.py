@@ -235,6 +235,46 @@ def test_panel_kernel_exact(M, K, N, batch, bias, acc):
         _native.set_gemm_policy(prev)
 
 
+@pytest.mark.parametrize("acc", [False, True])
+def test_panel_kernel_unaligned_output_and_bias(acc):
+    """The panel epilogue stores 4 columns at a time and reads the bias 4 at a time: C and
+    the bias may start at any float (here one float past a 16-byte boundary, with an odd
+    ldc and batch stride); the elements between the rows of C stay untouched."""
+    from my_pytchon_opencl_lib_amd import _native
+    M, K, N, batch = 65, 256, 260, 2
+    ldc, sC = N + 3, (N + 3) * M + 5
+    rng = np.random.default_rng(11 + acc)
+    A = rng.integers(-4, 5, size=(batch, M, K)).astype(np.float32)
+    B = rng.integers(-4, 5, size=(batch, K, N)).astype(np.float32)
+    bv = rng.integers(-20, 21, size=N + 1).astype(np.float32)
+    buf = np.full(1 + batch * sC, np.nan, dtype=np.float32)
+    C0 = rng.integers(-50, 51, size=(batch, M, N)).astype(np.float32)
+    for b in range(batch):
+        for m in range(M):
+            s = 1 + b * sC + m * ldc
+            buf[s:s + N] = C0[b, m] if acc else np.nan
+    c = dev(buf)
+    bias = dev(bv)
+    prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_PANEL)
+    try:
+        gemm_ex(0, 0, M, N, K, dev(A), K, M * K, dev(B), N, K * N, bias[1:], c[1:], ldc, sC,
+                batch, acc)
+        assert _native.last_plan().startswith("panel"), _native.last_plan()
+    finally:
+        _native.set_gemm_policy(prev)
+    got = host(c)
+    expect = A.astype(np.float64) @ B.astype(np.float64) + bv[1:]
+    if acc:
+        expect = expect + C0
+    written = np.zeros(buf.shape, dtype=bool)
+    for b in range(batch):
+        for m in range(M):
+            s = 1 + b * sC + m * ldc
+            written[s:s + N] = True
+            assert np.array_equal(got[s:s + N], expect[b, m].astype(np.float32)), (b, m)
+    assert np.isnan(got[~written]).all()
+
+
 def test_panel_kernel_falls_back_outside_its_shapes():
     """K % 32 != 0, N % 4 != 0, a transposed operand or unaligned rows: the PANEL policy
     runs the dispatcher's own choice instead, with the same result."""
