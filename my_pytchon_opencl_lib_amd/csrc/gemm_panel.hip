@@ -22,7 +22,8 @@
 //  * Each wavefront keeps its own LDS ring of D k-groups (shipped D = 1: one k-group in
 //    flight while the previous one is multiplied) and waits for its own loads
 //    (s_waitcnt vmcnt), so the k loop has no barrier. k-group i's fragments are in
-//    registers before its first MFMA; its slot is refilled after the first 4 of its 16
+//    registers before its first MFMA (k-group 0's first sub-group starts as soon as A and
+//    B's first 8 k-rows have landed); its slot is refilled after the first 4 of its 16
 //    MFMAs, and k-group i+1's fragments are read into a second register set before the
 //    last 4. Past the end the loads re-read the last k-group (never multiplied), so the
 //    wait count is constant.
@@ -142,10 +143,11 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
             const char *bg = bbase + (int64_t)g * bstep;
             const char *ag = abase + (int64_t)g * astep;
             float *st = my + slot * PSTAGE;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) dma16(bg, bvoff0 + q * bq, st + 256 * q);
+            // A first: the first sub-group of k-group 0 needs all of A's loads, B's first
 #pragma unroll
             for (int q = 0; q < 4; ++q) dma16(ag, avoff[q], st + 1024 + 256 * q);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) dma16(bg, bvoff0 + q * bq, st + 256 * q);
         };
         // Fragments of sub-group j (k = 8j .. 8j+7 of the k-group), step s: B lane l holds
         // k-row 8j + s + 4(l/32), column l%32; A lane l holds row l%32, k 8j + 4(l/32) .. +3.
@@ -177,9 +179,43 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
 #pragma unroll
         for (int j = 0; j < D; ++j) issue(j, j);
         Frags cur, nxt;
-        wait_vmcnt<8 * (D - 1)>();  // k-group 0 has landed
-        read(0, cur);
-        for (int i = 0; i < ng; ++i) {
+        int i0 = 0;
+        if constexpr (D == 1) {
+            // k-group 0 peeled: its first sub-group starts once A and B's first k-rows have
+            // landed (5 of the 8 loads), while B's other 24 k-rows are still arriving
+            wait_vmcnt<3>();
+#pragma unroll
+            for (int j = 0; j < 4; ++j) cur.a[j] = dl_load16(my + aoff(j));
+#pragma unroll
+            for (int s = 0; s < 4; ++s) cur.b[0][s] = my[boff + s * PT];
+            __builtin_amdgcn_sched_barrier(0);
+            mma(cur, 0);
+            // MFMA intrinsics do not touch memory, so without a use here the compiler moves
+            // them past the wait below
+            asm volatile("" ::"v"(acc[0]));
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmcnt<0>();
+#pragma unroll
+            for (int j = 1; j < 4; ++j)
+#pragma unroll
+                for (int s = 0; s < 4; ++s) cur.b[j][s] = my[boff + (8 * j + s) * PT];
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slot is read
+            issue(1, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(cur, 1);
+            mma(cur, 2);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmcnt<0>();  // k-group 1 has landed
+            read(0, nxt);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(cur, 3);
+            cur = nxt;
+            i0 = 1;
+        } else {
+            wait_vmcnt<8 * (D - 1)>();  // k-group 0 has landed
+            read(0, cur);
+        }
+        for (int i = i0; i < ng; ++i) {
             mma(cur, 0);
             __builtin_amdgcn_sched_barrier(0);
             // cur's fragments are all in registers: refill slot i%D after the first 4 MFMAs,
@@ -312,7 +348,8 @@ int launch_gemm_panel(hipStream_t stream, const GemmDesc &d) {
     // / at the k-group's start / after 4): 64 x 1536 x 4096 9.41 / 9.42 / 9.06, 256 x 512 x
     // 2048 9.11 / 8.86 / 8.54, 96 x 4096 x 8192 58.6 / 56.8 / 55.3; after 2 or 14 MFMAs
     // within 1 % of after 4. With the one-barrier epilogue (same harness, another box):
-    // 9.20 -> 9.03, 9.01 -> 8.17 and 57.6 -> 55.1.
+    // 9.20 -> 9.03, 9.01 -> 8.17 and 57.6 -> 55.1. Starting k-group 0 after 5 of its 8
+    // loads: 8.95 -> 8.90, 8.15 -> 7.91, 64 x 1024 x 4096 7.03 -> 6.75.
     const int G = d.K / PKG;
     int nw = G >= 8 ? 8 : (G >= 4 ? 4 : (G >= 2 ? 2 : 1));
     switch (nw) {
