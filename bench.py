@@ -9,8 +9,10 @@ each M = N = K = 4096, 2*4096^3 FLOP. `value` is the whole step's FLOP / wall ti
 
 Prints ONE JSON line on stdout. Besides the step it carries, by default:
   configs            every other BASELINE config timed on this GPU (HIP events around HIP-graph
-                     replays of back-to-back calls), with its roofline fraction and the launch
-                     floor (a one-element fill kernel replayed the same way);
+                     replays of back-to-back calls), with its roofline fraction, the launch
+                     floor (a one-element fill kernel replayed the same way), for the small
+                     configs a data-movement floor (a torch kernel that reads and writes the
+                     same bytes) and torch's own fp32 GEMM of the shape (torch_blas_us);
   roofline           the dominant 4096^3 kernel, from HIP events in this run (frac) and from
                      the committed rocprofv3 kernel trace of this bench (frac_profiled);
   cpu_baseline       the oracle's restatement of the reference matmul_tiled arithmetic
@@ -478,7 +480,9 @@ def measure_all_configs(torch, nncl, _native, calls=100):
     out["launch_floor"] = {"us": round(floor_us, 2),
                            "kernel": "torch fill of 1 element, graph-replayed back to back"}
 
-    def rec(name, ms, fns):
+    def rec(name, ms, fns, floor=None, vendor=None):
+        """floor = (torch op description, fns): a torch kernel that reads the config's input
+        bytes and writes its output bytes, timed the same way (the data-movement floor)."""
         flop, byts, bound = CONFIGS[name]
         tf = flop / (ms * 1e-3) / 1e12
         gbs = byts / (ms * 1e-3) / 1e9
@@ -491,31 +495,50 @@ def measure_all_configs(torch, nncl, _native, calls=100):
                                    else (gbs / PEAK_HBM_GBS), 4),
                      "x_launch_floor": round(ms * 1e3 / floor_us, 2),
                      "kernel": _native.last_plan()}
+        if floor is not None:
+            fl_ms = timed(floor[1])
+            out[name]["data_floor"] = {"us": round(fl_ms * 1e3, 2), "kernel": floor[0]}
+            out[name]["x_data_floor"] = round(ms / fl_ms, 2)
+        if vendor is not None:  # torch's own fp32 GEMM of the same shape, for comparison
+            vd_ms = timed(vendor)
+            out[name]["torch_blas_us"] = round(vd_ms * 1e3, 2)
 
     r = lambda *s: torch.rand(*s, device=dev, generator=g) * 2 - 1
     A, B, C = r(256, 256), r(256, 256), torch.empty(256, 256, device=dev)
     f1 = [lambda: nncl.gemm(A, B, out=C)]
-    rec("1_nn_256", timed(f1), f1)
+    # Data-movement floors of the small configs: one torch elementwise kernel that reads
+    # the config's operands and writes its output (the same bytes, no arithmetic to speak of).
+    rec("1_nn_256", timed(f1), f1,
+        ("torch.add(A, B, out=C): reads A and B, writes C", [lambda: torch.add(A, B, out=C)]),
+        [lambda: torch.mm(A, B, out=C)])
     Q, Kt, P, V = r(32, 128, 64), r(32, 64, 128), r(32, 128, 128), r(32, 128, 64)
     S, O = torch.empty(32, 128, 128, device=dev), torch.empty(32, 128, 64, device=dev)
     f2a = [lambda: nncl.gemm(Q, Kt, out=S)]
-    rec("2a_bmm_qk", timed(f2a), f2a)
+    rec("2a_bmm_qk", timed(f2a), f2a,
+        ("torch.cat([Q, K^T], out=S): reads Q and K^T, writes S (2 MB each way)",
+         [lambda: torch.cat([Q.view(-1), Kt.view(-1)], out=S.view(-1))]),
+        [lambda: torch.bmm(Q, Kt, out=S)])
     f2b = [lambda: nncl.gemm(P, V, out=O)]
-    rec("2b_bmm_pv", timed(f2b), f2b)
+    rec("2b_bmm_pv", timed(f2b), f2b,
+        ("torch.addcmul(V, P[..., :64], P[..., 64:], out=O): reads P and V, writes O",
+         [lambda: torch.addcmul(V, P[..., :64], P[..., 64:], out=O)]),
+        [lambda: torch.bmm(P, V, out=O)])
     X = torch.randn(100, 64, 1536, device=dev, generator=g)
     W = r(1536, 4096) / 32
     bias = r(4096) / 32
     Y = torch.empty(64, 4096, device=dev)
     f3 = [lambda i=i: nncl.gemm(X[i], W, bias=bias, out=Y) for i in range(100)]
-    rec("3_lstm_gate_step", timed(f3, per=1), f3)
+    rec("3_lstm_gate_step", timed(f3, per=1), f3,
+        vendor=[lambda i=i: torch.addmm(bias, X[i], W, out=Y) for i in range(100)])
     A5, B5, C5 = r(1000, 777), r(777, 3000), torch.empty(1000, 3000, device=dev)
     f5a = [lambda: nncl.gemm(A5, B5, out=C5)]
-    rec("5a_ragged", timed(f5a), f5a)
+    rec("5a_ragged", timed(f5a), f5a, vendor=[lambda: torch.mm(A5, B5, out=C5)])
     x = r(1, 4096)
     copies = [r(4096, 11008) for _ in range(3)]  # 541 MB > the 256 MB MALL
     y = torch.empty(1, 11008, device=dev)
     f5b = [lambda c=c: nncl.gemm(x, c, out=y) for c in copies]
-    rec("5b_gemv", timed(f5b), f5b)
+    # (no torch data floor here: torch's column sum may record a memset node into the graph)
+    rec("5b_gemv", timed(f5b), f5b, vendor=[lambda c=c: torch.mm(x, c, out=y) for c in copies])
     del copies
 
     def permute_into(src, dst, axes):
@@ -528,10 +551,12 @@ def measure_all_configs(torch, nncl, _native, calls=100):
 
     T, Tt = r(4096, 4096), torch.empty(4096, 4096, device=dev)
     fpt = [lambda: permute_into(T, Tt, [1, 0])]
-    rec("a5_permute_4096_t", timed(fpt), fpt)
+    rec("a5_permute_4096_t", timed(fpt), fpt,
+        ("torch Tt.copy_(T.t()): torch's own transpose copy", [lambda: Tt.copy_(T.t())]))
     H, Hp = r(32, 128, 16, 64), torch.empty(32, 16, 128, 64, device=dev)
     fph = [lambda: permute_into(H, Hp, [0, 2, 1, 3])]
-    rec("a5_permute_heads_0213", timed(fph), fph)
+    rec("a5_permute_heads_0213", timed(fph), fph,
+        ("torch Hp.copy_(H.permute(0, 2, 1, 3))", [lambda: Hp.copy_(H.permute(0, 2, 1, 3))]))
     # the floor of a kernel that must read its input before it writes: a torch device copy
     # of 256 KB (one 256^2 operand) replayed the same way
     c0, c1 = r(256, 256), torch.empty(256, 256, device=dev)
