@@ -6,7 +6,8 @@
 // chain of a few MFMAs per wavefront at the price of lane permutations, an LDS reduction and
 // a barrier, and its wavefronts spend most of their lifetime waiting (wave-level counters).
 // Here a 16x16 tile of C is computed by KS = 1, 2 or 4 wavefronts of one work-group, each over
-// a contiguous 1/KS of K (at most five 16-wide k-groups, K <= 80 per wavefront):
+// a contiguous 1/KS of K (at most five 16-wide k-groups, K <= 80 per wavefront; K = 128 on
+// four wavefronts of 32):
 //  * every operand value of a wavefront goes from global memory (L2) straight to registers,
 //    all its loads issued before its first MFMA (8 to 40 registers);
 //  * fragments in the MFMA's own order: in step j of k-group g, lane l supplies row / column
@@ -180,12 +181,17 @@ int64_t tiles16(const GemmDesc &d) {
     return (int64_t)((d.M + TT - 1) / TT) * ((d.N + TT - 1) / TT) * d.batch;
 }
 
-// Wavefronts per tile: 1 for K <= 80 (any K), 2 for K = 96, 128, 160, 4 for K = 192, 256,
-// 320 (whole 16-wide k-groups, at most five per wavefront); 0: not supported.
+// Wavefronts per tile: 1 for K <= 80 (any K), 2 for K = 96 and 160, 4 for K = 128, 192, 256,
+// 320 (whole 16-wide k-groups, at most five per wavefront); 0: not supported. K = 128 takes
+// four wavefronts of two k-groups rather than two of four: the shorter MFMA chains and the
+// extra wavefronts in flight outweigh the larger reduction (graph replay, 100 calls, us, two
+// / four: config 2b 32 x 128 x 128 @ 128 x 64 3.54 / 3.35, 16 x 128 x 128 @ 128 x 64 2.91 /
+// 2.68, 32 x 128 x 128 @ 128 x 128 4.83 / 4.68, 512 x 128 x 512 3.53 / 3.27, 4 x 256 x 128 @
+// 128 x 256 TN 3.37 / 3.30, NT 32 x 128 x 128 @ 128 x 64 3.82 / 3.84).
 int tiny_parts(const GemmDesc &d) {
     if (d.K <= TG_MAX * TT) return 1;
-    if (d.K % (2 * TT) == 0 && d.K <= 2 * TG_MAX * TT) return 2;
     if (d.K % (4 * TT) == 0 && d.K <= 4 * TG_MAX * TT) return 4;
+    if (d.K % (2 * TT) == 0 && d.K <= 2 * TG_MAX * TT) return 2;
     return 0;
 }
 
@@ -206,7 +212,8 @@ bool tiny_supported(const GemmDesc &d) {
 //    from LDS (2048 x 32 x 2048 9.83 / 10.59; 1024 x 64 x 2048 8.02 / 9.11) -- except at
 //    K = 16 (4096 x 16 x 4096 24.5 / 20.5).
 //  * K = 96..320, two or four wavefronts per tile (96 shapes, 60 won): 512-2048 tiles, e.g.
-//    32 x 128 x 128 @ 128 x 64 (config 2b) 3.79 / 3.59, 32 x 128 x 96 @ 96 x 128 6.31 / 4.19
+//    32 x 128 x 128 @ 128 x 64 (config 2b) 3.79 / 3.59 (two wavefronts per tile; four: 3.35),
+//    32 x 128 x 96 @ 96 x 128 6.31 / 4.19
 //    and 32 x 128 x 192 TN 8.25 / 6.30 (the register-staged tiled kernel), 4 x 64 x 320 @
 //    320 x 512 5.30 / 3.98. It loses with 256 tiles (256 x 128 x 256 2.63 / 2.90), at 4096
 //    tiles (1024 x 128 x 1024 7.21 / 8.03), with B transposed above K = 192 (32 x 128 x 256
@@ -266,14 +273,14 @@ int launch_gemm_tiny(hipStream_t stream, const GemmDesc &d) {
             case 4: rc = launch_g<4, 1>(stream, a, akc, bkc); break;
             default: rc = launch_g<5, 1>(stream, a, akc, bkc); break;
         }
-    } else if (ks == 2) {  // K = 96, 128, 160
+    } else if (ks == 2) {  // K = 96, 160
         switch (d.K / (2 * TT)) {
             case 3: rc = launch_g<3, 2>(stream, a, akc, bkc); break;
-            case 4: rc = launch_g<4, 2>(stream, a, akc, bkc); break;
             default: rc = launch_g<5, 2>(stream, a, akc, bkc); break;
         }
-    } else {  // K = 192, 256, 320
+    } else {  // K = 128, 192, 256, 320
         switch (d.K / (4 * TT)) {
+            case 2: rc = launch_g<2, 4>(stream, a, akc, bkc); break;
             case 3: rc = launch_g<3, 4>(stream, a, akc, bkc); break;
             case 4: rc = launch_g<4, 4>(stream, a, akc, bkc); break;
             default: rc = launch_g<5, 4>(stream, a, akc, bkc); break;

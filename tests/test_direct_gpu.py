@@ -292,7 +292,7 @@ def test_panel_kernel_falls_back_outside_its_shapes():
 
 # (M, K, N, batch, bias, accumulate) for the short-K kernel: K = 1, 15, 16, 17 (no full
 # k-group, one, one plus a partial), 33, 64 (config 2a), 79 and 80 (the longest for one
-# wavefront per tile); K = 96, 128 (config 2b), 160 (two wavefronts per tile) and 192, 256,
+# wavefront per tile); K = 96, 160 (two wavefronts per tile) and 128 (config 2b), 192, 256,
 # 320 (four), with ragged M and N around the 16-wide tiles, batches and both epilogues.
 TINY_SHAPES = [(1, 1, 1, 1, False, False), (17, 15, 33, 2, True, False),
                (16, 16, 16, 1, False, True), (33, 17, 47, 3, True, True),
@@ -332,33 +332,35 @@ def test_tiny_kernel_falls_back_outside_its_k():
         _native.set_gemm_policy(prev)
 
 
-def test_tiny_split_reduction_is_the_single_wavefront_sum_in_k_order():
-    """K = 128 on two wavefronts per tile: the partial tiles are added in k order, so the
-    result is identical on every call (and for the same operands in any layout)."""
+@pytest.mark.parametrize("K,parts", [(96, 2), (128, 4)])
+def test_tiny_split_reduction_is_the_single_wavefront_sum_in_k_order(K, parts):
+    """K = 96 on two wavefronts per tile and K = 128 on four: the partial tiles are added in
+    k order, so the result is identical on every call (and for the same operands in any
+    layout)."""
     from my_pytchon_opencl_lib_amd import _native
-    rng = np.random.default_rng(128)
-    A = rng.standard_normal((4, 100, 128)).astype(np.float32)
-    B = rng.standard_normal((4, 128, 90)).astype(np.float32)
+    rng = np.random.default_rng(K)
+    A = rng.standard_normal((4, 100, K)).astype(np.float32)
+    B = rng.standard_normal((4, K, 90)).astype(np.float32)
     prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_TINY)
     try:
         outs = []
         for rep in range(3):
             c = torch.full((4, 100, 90), float("nan"), device="cuda")
-            gemm_ex(0, 0, 100, 90, 128, dev(A), 128, 100 * 128, dev(B), 90, 128 * 90, None, c,
+            gemm_ex(0, 0, 100, 90, K, dev(A), K, 100 * K, dev(B), 90, K * 90, None, c,
                     90, 100 * 90, 4)
-            assert "splits=2" in _native.last_plan(), _native.last_plan()
+            assert f"splits={parts}" in _native.last_plan(), _native.last_plan()
             outs.append(host(c))
         bt = np.ascontiguousarray(np.swapaxes(B, 1, 2))
         c = torch.full((4, 100, 90), float("nan"), device="cuda")
-        gemm_ex(0, 1, 100, 90, 128, dev(A), 128, 100 * 128, dev(bt), 128, 90 * 128, None, c,
+        gemm_ex(0, 1, 100, 90, K, dev(A), K, 100 * K, dev(bt), K, 90 * K, None, c,
                 90, 100 * 90, 4)
         outs.append(host(c))
     finally:
         _native.set_gemm_policy(prev)
     for o in outs[1:]:
         assert np.array_equal(o, outs[0])
-    check_gemm(outs[0], A, B, 0, 0, M=100, N=90, K=128, lda=128, ldb=90, sA=100 * 128,
-               sB=128 * 90, batch=4)
+    check_gemm(outs[0], A, B, 0, 0, M=100, N=90, K=K, lda=K, ldb=90, sA=100 * K,
+               sB=K * 90, batch=4)
 
 
 def test_tiny_is_the_config2a_choice():
