@@ -320,10 +320,10 @@ int migemm_tensor_buffer(const char *tensor_id, size_t bytes, void **ptr);
 #define MIGEMM_POLICY_SMALL 2  /* k-split 16x16x4 MFMA small-output kernel for every shape */
 #define MIGEMM_POLICY_SKINNY 3 /* fp32-FMA kernel wherever it applies (M <= 4, B not
                                   transposed), otherwise the AUTO choice */
-#define MIGEMM_POLICY_PANEL 4  /* 32x32-tile panel kernel wherever it applies (A not
-                                  transposed, B not transposed, K % 32 == 0, N % 4 == 0,
-                                  16-byte aligned rows, lda and ldb <= 2^25), otherwise
-                                  the AUTO choice */
+#define MIGEMM_POLICY_PANEL 4  /* 32x32-tile panel kernel wherever it applies (any layout,
+                                  K % 32 == 0, N % 4 == 0, M % 4 == 0 when A is
+                                  transposed, 16-byte aligned rows, lda and ldb <= 2^25),
+                                  otherwise the AUTO choice */
 #define MIGEMM_POLICY_TINY 5   /* 16x16 tiles of 1, 2 or 4 wavefronts with all operands in
                                   registers wherever it applies (K <= 80, or K = 96, 128,
                                   160, 192, 256, 320), otherwise the AUTO choice */

@@ -1,7 +1,9 @@
-// Panel fp32 GEMM for gfx950: C = A * B (+ bias) for outputs with few rows, A K-contiguous
-// (an activation panel such as the 64 x 1536 input of the LSTM gate GEMM, lstm_gemm_xw,
-// cs/cl_kernels/lstm.cl:273, or the h_{t-1} rows of its recurrent product, lstm.cl:80-101)
-// and B N-contiguous (a weight matrix [K, N]); "cs/" = csharp/cstorchcl/cstorchcl/.
+// Panel fp32 GEMM for gfx950: C = op(A) * op(B) (+ bias) for outputs with few rows, in every
+// operand layout: an activation panel such as the 64 x 1536 input of the LSTM gate GEMM
+// (lstm_gemm_xw, cs/cl_kernels/lstm.cl:273) or the h_{t-1} rows of its recurrent product
+// (lstm.cl:80-101) times a weight matrix stored [K, N], or [N, K] as the Python reference's
+// Linear keeps it (core/layers.py:21-33), and the transposed forms of bmm_permute_tiled
+// (cs/cl_kernels/bmm_permute_tiled.cl:7-122); "cs/" = csharp/cstorchcl/cstorchcl/.
 //
 // Such a GEMM has too few output tiles for the tiled kernel, and every 32x32 tile of C needs
 // its 32-row slice of A and 32-column slice of B over the whole K (393 KB at K = 1536).
@@ -13,8 +15,11 @@
 //  * The product is computed as C^T = B^T A^T with v_mfma_f32_32x32x2_f32: the MFMA's first
 //    operand is B (lane l supplies column n0 + l%32), its second A (lane l supplies row
 //    m0 + l%32). In step s of each 8-wide sub-group, lanes 0-31 supply k = s and lanes 32-63
-//    k = 4 + s, for both operands, so a lane's four A values of a sub-group are one 16-byte
-//    read and B's are four 4-byte reads of consecutive k-rows.
+//    k = 4 + s, for both operands. A K-contiguous operand (A not transposed, B transposed)
+//    is staged as 32 rows of 32 k, and a lane's four values of a sub-group are one 16-byte
+//    read; a k-row operand (B not transposed, A transposed) as 32 k-rows of 32 columns, and
+//    they are four 4-byte reads of consecutive k-rows. Every layout sums each output over k
+//    in the same order.
 //  * Every operand byte moves with global_load_lds_dwordx4 (16 bytes per lane, straight
 //    into LDS). A k-group of 32 is 4 KB of each operand, 8 load instructions per wavefront,
 //    each covering 8 whole 128-byte lines: with 8-wide k-groups every line of A was fetched
@@ -22,18 +27,19 @@
 //  * Each wavefront keeps its own LDS ring of D k-groups (shipped D = 1: one k-group in
 //    flight while the previous one is multiplied) and waits for its own loads
 //    (s_waitcnt vmcnt), so the k loop has no barrier. k-group i's fragments are in
-//    registers before its first MFMA (k-group 0's first sub-group starts as soon as A and
-//    B's first 8 k-rows have landed); its slot is refilled after the first 4 of its 16
+//    registers before its first MFMA (k-group 0's first sub-group starts as soon as both
+//    operands' first 8 k have landed); its slot is refilled after the first 4 of its 16
 //    MFMAs, and k-group i+1's fragments are read into a second register set before the
 //    last 4. Past the end the loads re-read the last k-group (never multiplied), so the
 //    wait count is constant.
-//  * A rows are stored with chunk c of row r in slot c ^ ((r / 2) % 8), which makes the
-//    128-bit fragment reads conflict-free.
+//  * K-contiguous rows are stored with chunk c of row r in slot c ^ ((r / 2) % 8), which
+//    makes the 128-bit fragment reads conflict-free.
 //  * Work-groups are dealt to the 8 XCDs in contiguous chunks, both row tiles of a column
 //    block on one XCD, so each XCD's L2 holds a contiguous 1/8 of B (3.1 MB for the gate
 //    GEMM) and B is fetched into L2 once.
 //  * Edges: rows beyond M and columns beyond N are clamped on load and not stored. The
-//    kernel needs K % 32 == 0, N % 4 == 0 and 16-byte aligned rows (the dispatcher checks).
+//    kernel needs K % 32 == 0, N % 4 == 0, M % 4 == 0 when A is transposed, and 16-byte
+//    aligned rows (the dispatcher checks).
 //  * Epilogue as the other kernels: bias after the k sum (linear.cl:119-122), then C is
 //    written or added to.
 #include "gemm_direct.h"
@@ -68,7 +74,7 @@ constexpr int PRS = 36;        // floats between the rows of a partial tile in t
 // distinct bank groups.
 __device__ __forceinline__ int pa_swz(int r) { return (r >> 1) & 7; }
 
-template <int NW, int D>
+template <int NW, int D, bool AKC, bool BKC>
 __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
     static_assert(D * PSTAGE >= PT * PRS, "a partial tile fits in its wavefront's ring");
     static_assert(8 * (D - 1) < 64, "vmcnt range");
@@ -110,63 +116,103 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
 
     if (ng > 0) {
-        // Load instruction q (0..3) of an operand fills 1 KB: lane L the 16 bytes at LDS
-        // float 256 q + 4 L.
-        // B (k-rows of 32 columns): lane L loads k-row 8q + L/8, columns n0 + 4 (L % 8) .. +3
-        // (clamped to the last whole chunk).
-        int bcol = n0 + 4 * (lane & 7);
-        bcol = bcol < p.N - 4 ? bcol : p.N - 4;
-        const uint32_t bvoff0 =
-            (uint32_t)((((uint32_t)(lane >> 3)) * (uint32_t)p.ldb + (uint32_t)bcol) * 4u);
-        const uint32_t bq = (uint32_t)(8 * p.ldb * 4);  // bytes between instructions
-        const char *bbase = reinterpret_cast<const char *>(
-            p.B + (int64_t)bb * p.sB + (int64_t)g0 * PKG * p.ldb);
-        const int64_t bstep = (int64_t)PKG * p.ldb * 4;  // bytes per k-group
-        // A (rows of 32 k): lane L loads row 8q + L/8 (clamped) into slot L % 8, the row's k
-        // chunk (L % 8) ^ pa_swz(row).
-        const int arl = lane >> 3;  // row within the instruction
-        uint32_t avoff[4];
+        // Each operand's 32 x 32 slice of a k-group is 4 load instructions of 1 KB per
+        // wavefront (lane L: 16 bytes at LDS float 256 q + 4 L of the operand's half of the
+        // stage), in one of two layouts:
+        //  * K-contiguous (A not transposed, B transposed): rows of 32 k. Lane L of
+        //    instruction q loads row 8q + L/8 (clamped) into slot L % 8, the row's k chunk
+        //    (L % 8) ^ pa_swz(row); a fragment of 4 consecutive k is one 16-byte read.
+        //  * k-rows (A transposed, B not): 32 k-rows of 32 columns. Lane L of instruction q
+        //    loads k-row 8q + L/8, columns i0 + 4 (L % 8) .. +3 (clamped to the last whole
+        //    chunk); a fragment is 4 reads of one column in consecutive k-rows.
+        // Offsets are bytes from the operand's element (i0, k-group 0) of this wavefront.
+        auto offsets = [&](auto kc, int i0, int extent, int64_t ld, uint32_t(&off)[4]) {
+            if constexpr (decltype(kc)::value) {
+                const int rl = lane >> 3;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int r = 8 * q + arl;
-            int arow = m0 + r;
-            arow = arow < p.M - 1 ? arow : p.M - 1;
-            const int chunk = (lane & 7) ^ pa_swz(r);
-            avoff[q] = (uint32_t)((((uint32_t)(arow - m0)) * (uint32_t)p.lda + 4u * chunk) * 4u);
-        }
+                for (int q = 0; q < 4; ++q) {
+                    const int r = 8 * q + rl;
+                    int row = i0 + r;
+                    row = row < extent - 1 ? row : extent - 1;
+                    const int chunk = (lane & 7) ^ pa_swz(r);
+                    off[q] = (uint32_t)((((uint32_t)(row - i0)) * (uint32_t)ld + 4u * chunk) * 4u);
+                }
+            } else {
+                int col = i0 + 4 * (lane & 7);
+                col = col < extent - 4 ? col : extent - 4;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    off[q] = (uint32_t)((((uint32_t)(8 * q + (lane >> 3))) * (uint32_t)ld +
+                                         (uint32_t)(col - i0)) * 4u);
+            }
+        };
+        uint32_t aoffs[4], boffs[4];
+        offsets(std::integral_constant<bool, AKC>{}, m0, p.M, p.lda, aoffs);
+        offsets(std::integral_constant<bool, BKC>{}, n0, p.N, p.ldb, boffs);
         const char *abase = reinterpret_cast<const char *>(
-            p.A + (int64_t)bb * p.sA + (int64_t)m0 * p.lda + (int64_t)g0 * PKG);
-        constexpr int64_t astep = PKG * 4;
+            p.A + (int64_t)bb * p.sA +
+            (AKC ? (int64_t)m0 * p.lda + (int64_t)g0 * PKG : (int64_t)g0 * PKG * p.lda + m0));
+        const char *bbase = reinterpret_cast<const char *>(
+            p.B + (int64_t)bb * p.sB +
+            (BKC ? (int64_t)n0 * p.ldb + (int64_t)g0 * PKG : (int64_t)g0 * PKG * p.ldb + n0));
+        // bytes per k-group
+        const int64_t astep = AKC ? (int64_t)PKG * 4 : (int64_t)PKG * p.lda * 4;
+        const int64_t bstep = BKC ? (int64_t)PKG * 4 : (int64_t)PKG * p.ldb * 4;
 
+        // The first MFMA sub-group of a k-group needs k 0..7 of both operands: all four
+        // instructions of a K-contiguous operand, the first of a k-row one. K-contiguous
+        // operands are issued first and k-row operands interleaved by instruction, so those
+        // loads are the oldest PEEL of the 8.
+        constexpr int PEEL = 4 * ((int)AKC + (int)BKC) + ((int)!AKC + (int)!BKC);
         auto issue = [&](int j, int slot) {
             const int g = j < ng ? j : ng - 1;
-            const char *bg = bbase + (int64_t)g * bstep;
             const char *ag = abase + (int64_t)g * astep;
+            const char *bg = bbase + (int64_t)g * bstep;
             float *st = my + slot * PSTAGE;
-            // A first: the first sub-group of k-group 0 needs all of A's loads, B's first
+            if constexpr (AKC) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) dma16(ag, avoff[q], st + 1024 + 256 * q);
+                for (int q = 0; q < 4; ++q) dma16(ag, aoffs[q], st + 1024 + 256 * q);
+            }
+            if constexpr (BKC) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) dma16(bg, bvoff0 + q * bq, st + 256 * q);
+                for (int q = 0; q < 4; ++q) dma16(bg, boffs[q], st + 256 * q);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if constexpr (!AKC) dma16(ag, aoffs[q], st + 1024 + 256 * q);
+                if constexpr (!BKC) dma16(bg, boffs[q], st + 256 * q);
+            }
         };
         // Fragments of sub-group j (k = 8j .. 8j+7 of the k-group), step s: B lane l holds
-        // k-row 8j + s + 4(l/32), column l%32; A lane l holds row l%32, k 8j + 4(l/32) .. +3.
+        // column l%32 at k-row 8j + 4(l/32) + s; A lane l holds row l%32 at the same k.
         const int lo = lane & 31;
         const int hi = lane >> 5;
-        const int boff = 4 * hi * PT + lo;
-        auto aoff = [&](int j) { return 1024 + lo * PT + 4 * ((2 * j + hi) ^ pa_swz(lo)); };
+        auto frag = [&](auto kc, const float *half, int j) {
+            f4 v;
+            if constexpr (decltype(kc)::value) {
+                v = dl_load16(half + lo * PT + 4 * ((2 * j + hi) ^ pa_swz(lo)));
+            } else {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) v[s] = half[(8 * j + 4 * hi + s) * PT + lo];
+            }
+            return v;
+        };
+        auto frag_a = [&](int slot, int j) {
+            return frag(std::integral_constant<bool, AKC>{}, my + slot * PSTAGE + 1024, j);
+        };
+        auto frag_b = [&](int slot, int j) {
+            return frag(std::integral_constant<bool, BKC>{}, my + slot * PSTAGE, j);
+        };
 
         struct Frags {
-            float b[4][4];
+            f4 b[4];
             f4 a[4];
         };
         auto read = [&](int slot, Frags &f) {
-            const float *st = my + slot * PSTAGE;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-#pragma unroll
-                for (int s = 0; s < 4; ++s) f.b[j][s] = st[boff + (8 * j + s) * PT];
-                f.a[j] = dl_load16(st + aoff(j));
+                f.b[j] = frag_b(slot, j);
+                f.a[j] = frag_a(slot, j);
             }
         };
         auto mma = [&](const Frags &f, int j) {
@@ -181,13 +227,14 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
         Frags cur, nxt;
         int i0 = 0;
         if constexpr (D == 1) {
-            // k-group 0 peeled: its first sub-group starts once A and B's first k-rows have
-            // landed (5 of the 8 loads), while B's other 24 k-rows are still arriving
-            wait_vmcnt<3>();
+            // k-group 0 peeled: its first sub-group starts once the loads it needs have
+            // landed (PEEL of the 8), while the rest of the k-group is still arriving
+            wait_vmcnt<8 - PEEL>();
 #pragma unroll
-            for (int j = 0; j < 4; ++j) cur.a[j] = dl_load16(my + aoff(j));
-#pragma unroll
-            for (int s = 0; s < 4; ++s) cur.b[0][s] = my[boff + s * PT];
+            for (int j = 0; j < 4; ++j) {
+                if (AKC || j == 0) cur.a[j] = frag_a(0, j);
+                if (BKC || j == 0) cur.b[j] = frag_b(0, j);
+            }
             __builtin_amdgcn_sched_barrier(0);
             mma(cur, 0);
             // MFMA intrinsics do not touch memory, so without a use here the compiler moves
@@ -196,9 +243,10 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
             __builtin_amdgcn_sched_barrier(0);
             wait_vmcnt<0>();
 #pragma unroll
-            for (int j = 1; j < 4; ++j)
-#pragma unroll
-                for (int s = 0; s < 4; ++s) cur.b[j][s] = my[boff + (8 * j + s) * PT];
+            for (int j = 1; j < 4; ++j) {
+                if constexpr (!AKC) cur.a[j] = frag_a(0, j);
+                if constexpr (!BKC) cur.b[j] = frag_b(0, j);
+            }
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slot is read
             issue(1, 0);
             __builtin_amdgcn_sched_barrier(0);
@@ -269,6 +317,19 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
     }
 }
 
+// One k-group ring slot per wavefront (D = 1), NW wavefronts along K; operand layouts AKC
+// (A K-contiguous, i.e. not transposed) and BKC (B K-contiguous, i.e. transposed).
+template <bool AKC, bool BKC>
+int launch_nw(hipStream_t stream, const PanelArgs &a, int nw) {
+    switch (nw) {
+        case 8: hipLaunchKernelGGL((gemm_panel_kernel<8, 1, AKC, BKC>), dim3(a.total), dim3(8 * 64), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL((gemm_panel_kernel<4, 1, AKC, BKC>), dim3(a.total), dim3(4 * 64), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((gemm_panel_kernel<2, 1, AKC, BKC>), dim3(a.total), dim3(2 * 64), 0, stream, a); break;
+        default: hipLaunchKernelGGL((gemm_panel_kernel<1, 1, AKC, BKC>), dim3(a.total), dim3(64), 0, stream, a); break;
+    }
+    return hip_check(hipGetLastError(), "gemm_panel_kernel launch");
+}
+
 bool aligned16(const float *p, int64_t ld, int64_t stride) {
     return ((uintptr_t)p & 15) == 0 && ld % 4 == 0 && stride % 4 == 0;
 }
@@ -276,10 +337,12 @@ bool aligned16(const float *p, int64_t ld, int64_t stride) {
 }  // namespace
 
 bool panel_supported(const GemmDesc &d) {
-    // A K-contiguous and B N-contiguous; whole 32-wide k-groups and 16-byte chunks of B;
-    // every row 16-byte aligned; each lane's load offset within a k-group fits 32 bits:
-    // A's is below 32 lda * 4 bytes, B's below (31 ldb + N) * 4 <= 128 ldb bytes.
-    return !d.transA && !d.transB && d.K % PKG == 0 && d.N % 4 == 0 && d.N >= 4 &&
+    // Whole 32-wide k-groups; 16-byte chunks of C's rows (the epilogue) and of a k-row
+    // operand's rows (B not transposed: N % 4 == 0; A transposed: M % 4 == 0); every
+    // operand row 16-byte aligned; each lane's load offset within a k-group fits 32 bits:
+    // below 32 ld * 4 bytes for a K-contiguous operand, (31 ld + extent) * 4 <= 128 ld bytes
+    // for a k-row one.
+    return d.K % PKG == 0 && d.N % 4 == 0 && d.N >= 4 && (!d.transA || d.M % 4 == 0) &&
            aligned16(d.A, d.lda, d.sA) && aligned16(d.B, d.ldb, d.sB) &&
            d.lda <= ((int64_t)1 << 25) && d.ldb <= ((int64_t)1 << 25);
 }
@@ -352,14 +415,17 @@ int launch_gemm_panel(hipStream_t stream, const GemmDesc &d) {
     // loads: 8.95 -> 8.90, 8.15 -> 7.91, 64 x 1024 x 4096 7.03 -> 6.75.
     const int G = d.K / PKG;
     int nw = G >= 8 ? 8 : (G >= 4 ? 4 : (G >= 2 ? 2 : 1));
-    switch (nw) {
-        case 8: hipLaunchKernelGGL((gemm_panel_kernel<8, 1>), dim3(a.total), dim3(8 * 64), 0, stream, a); break;
-        case 4: hipLaunchKernelGGL((gemm_panel_kernel<4, 1>), dim3(a.total), dim3(4 * 64), 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((gemm_panel_kernel<2, 1>), dim3(a.total), dim3(2 * 64), 0, stream, a); break;
-        default: hipLaunchKernelGGL((gemm_panel_kernel<1, 1>), dim3(a.total), dim3(64), 0, stream, a); break;
-    }
+    int rc;
+    if (!d.transA && !d.transB)
+        rc = launch_nw<true, false>(stream, a, nw);
+    else if (!d.transA)
+        rc = launch_nw<true, true>(stream, a, nw);
+    else if (!d.transB)
+        rc = launch_nw<false, false>(stream, a, nw);
+    else
+        rc = launch_nw<false, true>(stream, a, nw);
     record_plan("panel", d, PT, PT, 1, 16);
-    return hip_check(hipGetLastError(), "gemm_panel_kernel launch");
+    return rc;
 }
 
 }  // namespace migemm

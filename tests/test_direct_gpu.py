@@ -212,9 +212,11 @@ def test_small_kernel_32x32_tiles_exact(ta, tb):
         _native.set_gemm_policy(prev)
 
 
-# The panel kernel (gemm_panel_kernel: 32x32 tiles, NN, K % 32 == 0, N % 4 == 0): ragged M
-# (1, 17, 33, 63, 65) and N (4, 36, 260), K with 1, 2, 4, 8 and more k-groups (so 1, 2, 4
-# and 8 wavefronts, uneven shares), batches with bias and the accumulating epilogue.
+# The panel kernel (gemm_panel_kernel: 32x32 tiles, K % 32 == 0, N % 4 == 0, M % 4 == 0 when
+# A is transposed), in every operand layout: ragged M (1, 17, 33, 63, 65; rounded up to a
+# multiple of 4 for a transposed A) and N (4, 36, 260), K with 1, 2, 4, 8 and more k-groups
+# (so 1, 2, 4 and 8 wavefronts, uneven shares), batches with bias and the accumulating
+# epilogue.
 PANEL_SHAPES = [(1, 32, 4, 1, False, False), (17, 64, 36, 2, True, False),
                 (33, 128, 260, 3, False, True), (63, 256, 100, 1, True, True),
                 (65, 1536, 4096, 1, True, False), (64, 800, 516, 2, False, False),
@@ -222,17 +224,51 @@ PANEL_SHAPES = [(1, 32, 4, 1, False, False), (17, 64, 36, 2, True, False),
 
 
 @pytest.mark.parametrize("M,K,N,batch,bias,acc", PANEL_SHAPES)
-def test_panel_kernel_exact(M, K, N, batch, bias, acc):
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_panel_kernel_exact(M, K, N, batch, bias, acc, ta, tb):
     from my_pytchon_opencl_lib_amd import _native
+    if ta:
+        M = (M + 3) // 4 * 4
     prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_PANEL)
     try:
-        say("panel exact", M, K, N, batch, bias, acc)
-        got, expect = run_exact(M, K, N, 0, 0, batch=batch, bias=bias, acc=acc,
-                                seed=M + 3 * K + 7 * N)
+        say("panel exact", M, K, N, batch, bias, acc, ta, tb)
+        got, expect = run_exact(M, K, N, ta, tb, batch=batch, bias=bias, acc=acc,
+                                seed=M + 3 * K + 7 * N + ta + 2 * tb)
         assert _native.last_plan().startswith("panel"), _native.last_plan()
         assert np.array_equal(got, expect)
     finally:
         _native.set_gemm_policy(prev)
+
+
+def test_panel_layouts_give_identical_bits():
+    """The panel kernel sums each output over k in the same order whatever the operand
+    layout: NN, NT, TN and TT of the same random operands give the same bits, within
+    1e-5 sqrt(K) of fp64."""
+    from my_pytchon_opencl_lib_amd import _native
+    M, K, N, batch = 96, 1536, 520, 2
+    rng = np.random.default_rng(1536)
+    A = rng.standard_normal((batch, M, K)).astype(np.float32)
+    B = rng.standard_normal((batch, K, N)).astype(np.float32)
+    At = np.ascontiguousarray(np.swapaxes(A, 1, 2))
+    Bt = np.ascontiguousarray(np.swapaxes(B, 1, 2))
+    outs = []
+    prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_PANEL)
+    try:
+        for ta, tb in LAYOUTS:
+            say("panel layouts", ta, tb)
+            a, lda = (At, M) if ta else (A, K)
+            b, ldb = (Bt, K) if tb else (B, N)
+            c = torch.full((batch, M, N), float("nan"), device="cuda")
+            gemm_ex(ta, tb, M, N, K, dev(a), lda, M * K, dev(b), ldb, K * N, None, c, N,
+                    M * N, batch)
+            assert _native.last_plan().startswith("panel"), _native.last_plan()
+            outs.append(host(c))
+    finally:
+        _native.set_gemm_policy(prev)
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+    check_gemm(outs[0], A, B, 0, 0, M=M, N=N, K=K, lda=K, ldb=N, sA=M * K, sB=K * N,
+               batch=batch)
 
 
 @pytest.mark.parametrize("acc", [False, True])
@@ -276,13 +312,14 @@ def test_panel_kernel_unaligned_output_and_bias(acc):
 
 
 def test_panel_kernel_falls_back_outside_its_shapes():
-    """K % 32 != 0, N % 4 != 0, a transposed operand or unaligned rows: the PANEL policy
-    runs the dispatcher's own choice instead, with the same result."""
+    """K % 32 != 0, N % 4 != 0 or, with A transposed, M % 4 != 0 (whose rows are then not
+    16-byte aligned either): the PANEL policy runs the dispatcher's own choice instead, with
+    the same result."""
     from my_pytchon_opencl_lib_amd import _native
     prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_PANEL)
     try:
-        for M, K, N, ta, tb in [(64, 100, 256, 0, 0), (64, 128, 258, 0, 0), (64, 128, 256, 1, 0),
-                                (64, 128, 256, 0, 1)]:
+        for M, K, N, ta, tb in [(64, 100, 256, 0, 0), (64, 128, 258, 0, 0), (66, 128, 256, 1, 0),
+                                (64, 100, 256, 0, 1), (65, 128, 256, 1, 1)]:
             got, expect = run_exact(M, K, N, ta, tb, seed=K + N + ta)
             assert not _native.last_plan().startswith("panel"), (M, K, N, ta, tb)
             assert np.array_equal(got, expect)
