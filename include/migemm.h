@@ -318,8 +318,9 @@ int migemm_tensor_buffer(const char *tensor_id, size_t bytes, void **ptr);
 #define MIGEMM_POLICY_AUTO 0   /* choice by shape (default) */
 #define MIGEMM_POLICY_TILED 1  /* LDS-tiled 32x32x2 MFMA kernel (+ split-K) for every shape */
 #define MIGEMM_POLICY_SMALL 2  /* k-split 16x16x4 MFMA small-output kernel for every shape */
-#define MIGEMM_POLICY_SKINNY 3 /* fp32-FMA kernel wherever it applies (M <= 4, B not
-                                  transposed), otherwise the AUTO choice */
+#define MIGEMM_POLICY_SKINNY 3 /* fp32-FMA streaming kernels wherever they apply (M <= 4;
+                                  B transposed: whole rows of B per wavefront), otherwise
+                                  the AUTO choice */
 #define MIGEMM_POLICY_PANEL 4  /* 32x32-tile panel kernel wherever it applies (any layout,
                                   K % 32 == 0, N % 4 == 0, M % 4 == 0 when A is
                                   transposed, 16-byte aligned rows, lda and ldb <= 2^25),

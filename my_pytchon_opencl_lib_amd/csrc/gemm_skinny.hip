@@ -1,6 +1,8 @@
-// Skinny fp32 GEMM (M <= 4 rows of C, B not transposed): the decode-like GEMV of the
-// matmul path, C[M,N] = A[M,K] * B[K,N] (+ bias), which reads each element of B once and
-// is therefore bound by HBM bandwidth (0.5 FLOP/byte at M = 1), not by the matrix cores.
+// Skinny fp32 GEMM (M <= 4 rows of C): the decode-like GEMV of the matmul path,
+// C[M,N] = A[M,K] * op(B) (+ bias), which reads each element of B once and is therefore
+// bound by HBM bandwidth (0.5 FLOP/byte at M = 1), not by the matrix cores. B stored [N, K]
+// (transposed, the weight layout of the Python reference's Linear, core/layers.py:21-33)
+// runs gemv_rows_kernel below: a wavefront streams whole rows of B. B stored [K, N]:
 //
 // Work split: a work-group of 4 wavefronts owns 256 consecutive columns (one float4 of
 // B per lane) and a slice of KC rows of K; the slice of A is staged in LDS, wavefront w
@@ -178,6 +180,139 @@ __global__ void __launch_bounds__(SK_THREADS) gemm_skinny_kernel(SkinnyArgs p) {
     }
 }
 
+// B transposed (stored [N, K]): output column n is the dot product of A's rows with row n
+// of the stored B, whose K floats are contiguous. A wavefront owns RW consecutive rows of B
+// and streams each over the whole K, 16 bytes per lane, U 1 KB loads per row in flight;
+// lane L covers k = 256 i + 4 L .. +3. The lanes' partial sums are added by a butterfly
+// over the wavefront (a fixed order), so nothing leaves the wavefront but the result and
+// the call is one launch. A's rows (MR <= 4) are read through the caches with each chunk of
+// B; every wavefront shares them, and RW rows per wavefront reuse each chunk of A RW times.
+// Measured (graph replay, rotating copies of B, us; RW x U = 1 x 4 / 1 x 8 / 2 x 4 / 4 x 4):
+// 1 x 11008 x 4096 29.2 / 28.9 / 30.6 / 35.7; 2 x 11008 x 4096 37.5 / 36.4 / 34.6 / 37.7;
+// 4 x 11008 x 4096 50.8 / 50.6 / 42.8 / 38.0; 1 x 8192 x 8192 43.9 / 43.8 / 48.2 / 55.5.
+template <int MR>
+struct RowsPlan {
+    static constexpr int RW = MR == 1 ? 1 : (MR == 2 ? 2 : 4);  // rows of B per wavefront
+    static constexpr int U = MR <= 2 ? 8 : 4;                    // 1 KB chunks per row in flight
+};
+constexpr int RW_WAVES = 4;  // wavefronts per work-group
+
+template <int MR, bool AVEC>
+__global__ void __launch_bounds__(RW_WAVES * 64) gemv_rows_kernel(SkinnyArgs p) {
+    constexpr int RW = RowsPlan<MR>::RW;
+    constexpr int U = RowsPlan<MR>::U;
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int n0 = (blockIdx.x * RW_WAVES + w) * RW;
+    const int b = blockIdx.y;
+    if (n0 >= p.N) return;  // no barrier below: whole wavefronts may leave
+    const float *Ab = p.A + (int64_t)b * p.sA;
+    const float *Bb = p.B + (int64_t)b * p.sB;
+    const float *brow[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) brow[r] = Bb + (int64_t)min(n0 + r, p.N - 1) * p.ldb;
+
+    f4 acc[MR][RW];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int r = 0; r < RW; ++r) acc[m][r] = f4{0.f, 0.f, 0.f, 0.f};
+
+    auto load_a = [&](int m, int k) {
+        const float *q = Ab + (int64_t)m * p.a_rs;
+        f4 v;
+        if constexpr (AVEC)
+            v = *reinterpret_cast<const f4u *>(q + k);
+        else
+            v = f4{q[(int64_t)k * p.a_ks], q[(int64_t)(k + 1) * p.a_ks],
+                   q[(int64_t)(k + 2) * p.a_ks], q[(int64_t)(k + 3) * p.a_ks]};
+        return v;
+    };
+    auto fma4 = [&](f4 &c, const f4 &x, const f4 &y) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) c[e] = __builtin_fmaf(x[e], y[e], c[e]);
+    };
+    // whole batches of U chunks of 256 k: no bounds checks
+    constexpr int STEP = 256 * U;
+    const int kfull = p.K / STEP * STEP;
+    for (int kb = 0; kb < kfull; kb += STEP) {
+        f4 bv[U][RW], av[U][MR];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+                bv[u][r] = __builtin_nontemporal_load(
+                    reinterpret_cast<const f4u *>(brow[r] + kb + 256 * u + 4 * lane));
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) av[u][m] = load_a(m, kb + 256 * u + 4 * lane);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int r = 0; r < RW; ++r) fma4(acc[m][r], av[u][m], bv[u][r]);
+    }
+    // the rest of K, one chunk of 256 at a time; k >= K contributes nothing
+    for (int kb = kfull; kb < p.K; kb += 256) {
+        const int k = kb + 4 * lane;
+        if (k + 4 <= p.K) {
+            f4 av[MR];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) av[m] = load_a(m, k);
+#pragma unroll
+            for (int r = 0; r < RW; ++r) {
+                const f4 bv = *reinterpret_cast<const f4u *>(brow[r] + k);
+#pragma unroll
+                for (int m = 0; m < MR; ++m) fma4(acc[m][r], av[m], bv);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (k + e < p.K) {
+#pragma unroll
+                    for (int r = 0; r < RW; ++r) {
+                        const float bv = brow[r][k + e];
+#pragma unroll
+                        for (int m = 0; m < MR; ++m)
+                            acc[m][r][e] = __builtin_fmaf(
+                                Ab[(int64_t)m * p.a_rs + (int64_t)(k + e) * p.a_ks], bv,
+                                acc[m][r][e]);
+                    }
+                }
+            }
+        }
+    }
+    // lane sums, then the wavefront butterfly: every lane ends with the same total
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            float v = (acc[m][r][0] + acc[m][r][1]) + (acc[m][r][2] + acc[m][r][3]);
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+            const int n = n0 + r;
+            if (lane == 0 && n < p.N) {
+                if (p.bias != nullptr) v = v + p.bias[n];
+                float *c = p.C + (int64_t)b * p.sC + (int64_t)m * p.ldc + n;
+                *c = p.accumulate ? *c + v : v;
+            }
+        }
+    }
+}
+
+template <int MR>
+int launch_rows(hipStream_t st, const SkinnyArgs &a, bool avec, int batch) {
+    constexpr int per_wg = RW_WAVES * RowsPlan<MR>::RW;
+    dim3 grid((a.N + per_wg - 1) / per_wg, batch);
+    if (avec)
+        hipLaunchKernelGGL((gemv_rows_kernel<MR, true>), grid, dim3(RW_WAVES * 64), 0, st, a);
+    else
+        hipLaunchKernelGGL((gemv_rows_kernel<MR, false>), grid, dim3(RW_WAVES * 64), 0, st, a);
+    return hip_check(hipGetLastError(), "gemv_rows_kernel launch");
+}
+
 template <int MR>
 int launch_mr(hipStream_t st, const SkinnyArgs &a, bool vec, int batch) {
     dim3 grid(a.cblocks, a.slices, batch);
@@ -193,8 +328,22 @@ int launch_mr(hipStream_t st, const SkinnyArgs &a, bool vec, int batch) {
 }  // namespace
 
 bool skinny_supported(const GemmDesc &d) {
-    return d.M <= SK_MAXM && !d.transB && d.N >= 4 && d.batch <= 65535 &&
-           (int64_t)d.K <= (int64_t)65535 * 256;
+    if (d.M > SK_MAXM || d.batch > 65535) return false;
+    if (d.transB) return true;  // gemv_rows_kernel
+    return d.N >= 4 && (int64_t)d.K <= (int64_t)65535 * 256;
+}
+
+// B transposed: where the rows kernel beats the other families (graph replay, rotating
+// copies of B, M 1-4 x N 1024-11008 x K 512-8192, us, rows / small kernel). At M = 1 (a
+// wavefront per row) at every shape: 1 x 1024 x 512 2.58 / 4.87, 1 x 4096 x 1024 5.04 /
+// 5.49, 1 x 11008 x 4096 30.0 / 39.5. With 2-4 rows per wavefront it needs many rows: at
+// N = 11008 from K = 1024 (M = 2: 12.46 / 13.62) or K = 2048 (M = 3-4: 21.3 / 24.5), but at
+// N = 4096 the small kernel wins (4 x 4096 x 4096 22.4 / 15.3, 2 x 4096 x 4096 15.2 / 14.8).
+static bool rows_preferred(const GemmDesc &d) {
+    const int64_t rows = (int64_t)d.N * d.batch;
+    if (d.M == 1) return rows >= 1024;
+    if (d.M == 2) return rows >= 8192 && d.K >= 1024;
+    return rows >= 8192 && d.K >= 2048;
 }
 
 // Streaming B pays once B is too large to sit in the caches: from 64 MB of B the kernel
@@ -204,7 +353,9 @@ bool skinny_supported(const GemmDesc &d) {
 // 12.1; 4 x 4096 x 2048 14.9 / 12.3) and below that the small kernel wins (3 x 6565 x 500
 // 20.1 / 7.7).
 bool skinny_preferred(const GemmDesc &d) {
-    return skinny_supported(d) && (int64_t)d.K * d.N * d.batch >= ((int64_t)16 << 20);
+    if (!skinny_supported(d)) return false;
+    if (d.transB) return rows_preferred(d);
+    return (int64_t)d.K * d.N * d.batch >= ((int64_t)16 << 20);
 }
 
 int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {
@@ -224,6 +375,24 @@ int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {
     a.N = d.N;
     a.K = d.K;
     a.cblocks = (d.N + SK_COLS - 1) / SK_COLS;
+    a.batch = d.batch;
+    a.accumulate = d.accumulate;
+    a.partial = nullptr;
+
+    if (d.transB) {  // rows of the stored B streamed whole: one launch, no partial sums
+        a.kc = d.K;
+        a.slices = 1;
+        const bool avec = !d.transA;
+        int rc;
+        switch (d.M) {
+            case 1: rc = launch_rows<1>(stream, a, avec, d.batch); break;
+            case 2: rc = launch_rows<2>(stream, a, avec, d.batch); break;
+            case 3: rc = launch_rows<3>(stream, a, avec, d.batch); break;
+            default: rc = launch_rows<4>(stream, a, avec, d.batch); break;
+        }
+        record_plan("skinny-rows", d, 0, 0, 1, 16);
+        return rc;
+    }
 
     // Slices of KC = 4 wavefronts x 64 rows (four batches of 16 per wavefront) give the
     // 5b shape (11008 x 4096) 43 x 16 = 688 work-groups, all resident at once, each
@@ -237,9 +406,6 @@ int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {
     if (a.slices > 65535)  // K <= 65535 * SK_KC_MAX is part of skinny_supported
         return set_error(MIGEMM_ERR_UNSUPPORTED, "gemm_skinny: K=%d needs %d slices", d.K,
                          a.slices);
-    a.partial = nullptr;
-    a.batch = d.batch;
-    a.accumulate = d.accumulate;
     if (a.slices > 1) {
         const size_t part_bytes = (size_t)a.slices * d.batch * d.M * d.N * sizeof(float);
         int st = MIGEMM_OK;

@@ -92,9 +92,10 @@ void record_plan(const char *kernel, const GemmDesc &d, int bm, int bn, int spli
 // Launchers. They assume a validated descriptor and only enqueue work.
 int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d);
 int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d);
-// M <= 4 and B not transposed (the shapes gemm_skinny_kernel handles).
+// M <= 4 (gemm_skinny_kernel for B not transposed, gemv_rows_kernel for B transposed).
 bool skinny_supported(const GemmDesc &d);
-// Supported and B large enough (>= 64 MB) for the streaming kernel to beat the others.
+// Supported, and a shape where the streaming kernel beats the others (B not transposed:
+// >= 64 MB of B; transposed: enough rows of B, gemm_skinny.hip).
 bool skinny_preferred(const GemmDesc &d);
 int launch_gemm_small(hipStream_t stream, const GemmDesc &d);
 // A K-contiguous, B N-contiguous, K % 8 == 0, N % 4 == 0, 16-byte aligned rows

@@ -413,3 +413,51 @@ def test_tiny_is_the_config2a_choice():
     assert _native.last_plan().startswith("tiny"), _native.last_plan()
     check_gemm(host(c), Q, Kt, 0, 0, M=128, N=128, K=64, lda=64, ldb=128, sA=128 * 64,
                sB=64 * 128, batch=32)
+
+
+# The rows kernel of the skinny family (gemv_rows_kernel: M <= 4, B stored [N, K], each
+# wavefront streaming 1, 2 or 4 whole rows of B): K with no whole batch of loads (3, 200),
+# one batch and a vector tail (2304 = 2048 + 256), batches with a partial last chunk
+# (2051, 4099: k beyond K in the last 16 bytes), N not a multiple of the rows per wavefront,
+# A in both layouts, batches with bias and the accumulating epilogue.
+ROWS_SHAPES = [(1, 3, 5, 1, False, False), (2, 200, 37, 2, True, False),
+               (3, 2304, 1030, 1, False, True), (4, 2051, 1026, 2, True, True),
+               (1, 4099, 2050, 1, True, False), (2, 1027, 3, 3, False, False)]
+
+
+@pytest.mark.parametrize("M,K,N,batch,bias,acc", ROWS_SHAPES)
+@pytest.mark.parametrize("ta", [0, 1])
+def test_rows_kernel_exact(M, K, N, batch, bias, acc, ta):
+    from my_pytchon_opencl_lib_amd import _native
+    prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_SKINNY)
+    try:
+        say("rows exact", M, K, N, batch, bias, acc, ta)
+        got, expect = run_exact(M, K, N, ta, 1, batch=batch, bias=bias, acc=acc,
+                                seed=M + 3 * K + 7 * N + ta)
+        assert _native.last_plan().startswith("skinny-rows"), _native.last_plan()
+        assert np.array_equal(got, expect)
+    finally:
+        _native.set_gemm_policy(prev)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_rows_kernel_random_and_dispatch(M):
+    """Random operands within 1e-5 sqrt(K) of fp64, the same bits for either layout of A, and
+    the GEMV the dispatcher sends to the rows kernel under AUTO (M = 1, any width; M = 2-4
+    with many rows of long K)."""
+    from my_pytchon_opencl_lib_amd import _native
+    K, N = 4099, 11008
+    rng = np.random.default_rng(4099 + M)
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    Bt = rng.uniform(-1, 1, (N, K)).astype(np.float32)
+    bias = rng.uniform(-1, 1, N).astype(np.float32)
+    say("rows random", M, K, N)
+    outs = []
+    for ta in (0, 1):
+        a = np.ascontiguousarray(A.T) if ta else A
+        c = torch.full((M, N), float("nan"), device="cuda")
+        gemm_ex(ta, 1, M, N, K, dev(a), M if ta else K, 0, dev(Bt), K, 0, dev(bias), c, N, 0, 1)
+        assert _native.last_plan().startswith("skinny-rows"), (ta, _native.last_plan())
+        outs.append(host(c))
+    assert np.array_equal(outs[0], outs[1])
+    check_gemm(outs[0], A, Bt, 0, 1, bias=bias, M=M, N=N, K=K, lda=K, ldb=K)
