@@ -700,10 +700,22 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
                 // per-shape best falls from 0.32 % to 0.18 %, and 3000 x 256 x 8000 takes
                 // 64x64 tiles (115.1 us) instead of 128x256 (136.7 us).
                 const double s = d.K <= 512 ? 1.5 : 1.0;
+                // C rows that do not start on 128-byte lines are stored as partial lines, and
+                // a 256x256 work-group (one per CU) cannot hide that store burst behind other
+                // work-groups' k loops; up to K = 1024 its overhead counts twice then (graph
+                // replay, us, 64x64 / 128x128 / 128x256 / 256x256): 12000 x 500 x 6565 NT
+                // (the Python Linear(500 -> 6565) forward) 683-755 / 645 / 656 / 742, TT
+                // 674-710 / 634 / 641 / 734, 8192 x 512 x 8191 NT 527 / 517 / 535 / 608,
+                // 4096 x 300 x 4095 NT 101 / 115 / 116 / 126, 8192 x 1024 x 8190 TT 980 / 1011
+                // / 954 / 1033; with N = 6560 all four 616-690 and 256x256 among the best. On
+                // the dispatcher grid (M, N 1000-8000, K 256-4096, NN / NT / TN) the 256x256
+                // picks with such C rows ran 0.76-0.96x as long at K <= 1024 (5000 x 256 x
+                // 3000 NT 93.9 -> 71.7 us in 64x64 tiles), but 1.01x at K = 4096.
+                const bool cmis = (d.ldc % 32 != 0 || ((uintptr_t)d.C & 127) != 0) && d.K <= 1024;
                 c64 = cost(64, 64, 135.2, 95);
                 c0 = cost(128, 128, 147.6, 90 * s);
                 c1 = cost(128, 256, 152.1, 98 * s);
-                c2 = cost(256, 256, 152.6, 75 * s);
+                c2 = cost(256, 256, 152.6, 75 * s * (cmis ? 2.0 : 1.0));
             } else {
                 c64 = cost(64, 64, 134.2, 75);
                 c0 = cost(128, 128, 138.9, 78);
