@@ -329,7 +329,8 @@ int launch_mr(hipStream_t st, const SkinnyArgs &a, bool vec, int batch) {
 
 bool skinny_supported(const GemmDesc &d) {
     if (d.M > SK_MAXM || d.batch > 65535) return false;
-    if (d.transB) return true;  // gemv_rows_kernel
+    // gemv_rows_kernel: its k loops step in int, 256 x 8 floats at a time
+    if (d.transB) return d.K <= (1 << 30);
     return d.N >= 4 && (int64_t)d.K <= (int64_t)65535 * 256;
 }
 
