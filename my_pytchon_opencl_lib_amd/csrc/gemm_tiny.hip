@@ -12,8 +12,9 @@
 //    all its loads issued before its first MFMA (8 to 40 registers);
 //  * fragments in the MFMA's own order: in step j of k-group g, lane l supplies row / column
 //    l % 16 at k = 16 g + 4 (l / 16) + j. A K-contiguous operand is one 16-byte load per
-//    k-group (4 rows x 64 contiguous bytes per 16 lanes); an M- or N-contiguous one is four
-//    4-byte loads, 16 lanes covering 64 contiguous bytes of one k-row;
+//    k-group, 16 lanes reading 4 rows x 64 contiguous bytes, put in fragment order by a lane
+//    permutation; an M- or N-contiguous one is four 4-byte loads, 16 lanes covering 64
+//    contiguous bytes of one k-row;
 //  * one accumulator per wavefront, MFMAs in ascending k; with KS > 1 the wavefronts' partial
 //    tiles are added through LDS in k order after one barrier: a fixed association order;
 //  * 4 / KS tiles per work-group (consecutive along N, so the wavefronts read the same rows of
@@ -82,10 +83,25 @@ __global__ void __launch_bounds__(TWG * 64) gemm_tiny_kernel(TinyArgs p) {
     // A(i, k) = Ab[i*lda + k] (AKC) or Ab[k*lda + i]; B(k, n) = Bb[n*ldb + k] (BKC) or
     // Bb[k*ldb + n]. pa / pb: this lane's row / column at k = k0 + 4 * lq.
     const int k0 = kp * G * TT;
-    const float *pa = AKC ? Ab + (int64_t)row * p.lda + k0 + 4 * lq
+    // A K-contiguous operand read in fragment order would give each 16-lane group 16
+    // different rows; it is read coalesced instead: lane (lq, li = 4a + c) loads the 16
+    // bytes of row 4 lq + a at k = 4c .. 4c+3 (a 16-lane group reads 4 rows x 64 contiguous
+    // bytes), and a lane permutation (ds_bpermute, no LDS storage) gives lane (lq, li) row
+    // li at k = 4 lq + j, the same values as the fragment-order load.
+    const int crow = 4 * lq + (li >> 2);
+    const int ck = 4 * (li & 3);
+    const int perm_src = (16 * (li >> 2) + 4 * (li & 3) + lq) * 4;  // byte index of the source
+    const float *pa = AKC ? Ab + (int64_t)min(m0 + crow, p.M - 1) * p.lda + k0 + ck
                           : Ab + (int64_t)(k0 + 4 * lq) * p.lda + row;
-    const float *pb = BKC ? Bb + (int64_t)col * p.ldb + k0 + 4 * lq
+    const float *pb = BKC ? Bb + (int64_t)min(n0 + crow, p.N - 1) * p.ldb + k0 + ck
                           : Bb + (int64_t)(k0 + 4 * lq) * p.ldb + col;
+    auto permute = [&](f4 v) {
+        f4 r;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            r[j] = __int_as_float(__builtin_amdgcn_ds_bpermute(perm_src, __float_as_int(v[j])));
+        return r;
+    };
     const int64_t a_g = AKC ? TT : (int64_t)TT * p.lda;  // per k-group
     const int64_t b_g = BKC ? TT : (int64_t)TT * p.ldb;
 
@@ -115,6 +131,11 @@ __global__ void __launch_bounds__(TWG * 64) gemm_tiny_kernel(TinyArgs p) {
                 xb[j] = Bb[BKC ? (int64_t)col * p.ldb + k : (int64_t)k * p.ldb + col];
             }
         }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        if constexpr (AKC) fa[g] = permute(fa[g]);
+        if constexpr (BKC) fb[g] = permute(fb[g]);
     }
     f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -216,22 +237,21 @@ bool tiny_supported(const GemmDesc &d) {
 //    32 x 128 x 96 @ 96 x 128 6.31 / 4.19
 //    and 32 x 128 x 192 TN 8.25 / 6.30 (the register-staged tiled kernel), 4 x 64 x 320 @
 //    320 x 512 5.30 / 3.98. It loses with 256 tiles (256 x 128 x 256 2.63 / 2.90), at 4096
-//    tiles (1024 x 128 x 1024 7.21 / 8.03), with B transposed above K = 192 (32 x 128 x 256
-//    NT 8.51 / 9.30) and where the panel kernel applies (64 x 256 x 4096 4.19 / 4.85), which
-//    is therefore asked first.
+//    tiles (1024 x 128 x 1024 7.21 / 8.03) and where the panel kernel applies (64 x 256 x
+//    4096 4.19 / 4.85; batch-32 128 x 256 x 128 NT 5.40 / 5.94), which is therefore asked
+//    first.
 bool tiny_preferred(const GemmDesc &d) {
     if (!tiny_supported(d) || d.M < 16 || d.N < 16) return false;
     const int64_t t = tiles16(d);
     if (tiny_parts(d) == 1) {
-        // B transposed: its 16-byte fragment loads read 16 rows per 16 lanes; above K = 48
-        // the small kernel's coalesced loads win (1024 x 64 x 1024 NT 6.1 against 5.6 us)
-        if (d.transB && d.K > 48) return false;
+        // (B transposed took the small kernel above K = 48 while the K-contiguous loads
+        // read 16 rows per 16 lanes; read coalesced it runs as NN does: batch-32 128 x 64 x
+        // 128 NT 3.11 us against 4.01 on the small kernel, 512 x 64 x 512 2.63 / 3.31)
         if (t < (d.K <= 48 ? 512 : 1024)) return false;
         if (d.K <= 16) return true;
         return t <= (d.K <= 48 ? 8192 : 4096);
     }
     if (t < 512 || t > 2048) return false;
-    if (d.transB && d.K > 192) return false;
     return !panel_preferred(d);
 }
 
