@@ -251,7 +251,11 @@ bool tiny_preferred(const GemmDesc &d) {
         if (d.K <= 16) return true;
         return t <= (d.K <= 48 ? 8192 : 4096);
     }
-    if (t < 512 || t > 2048) return false;
+    // From 64 tiles when A is K-contiguous (coalesced loads; graph replay, us, small kernel
+    // / this one: 256 x 256 x 256 NN 2.94 / 2.50, NT 2.83 / 2.63, 128 x 256 x 128 NN 2.81 /
+    // 2.32, 256 x 320 x 256 NN 3.41 / 2.81); a transposed A (four 4-byte loads per
+    // fragment) keeps the small kernel below 512 tiles (256 x 256 x 256 TN 2.83 / 2.95).
+    if (t < (d.transA ? 512 : 64) || t > 2048) return false;
     return !panel_preferred(d);
 }
 
