@@ -597,7 +597,17 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     };
     int cfg, splits = 1;
     int big = 0;  // 128x128 tiles; 1: 128x256, 2: 256x256 (see below)
-    if (tiles(128, 128) >= 512) {
+    if (narrow_rows_streaming(d)) {
+        // few rows over a large B (gemm_small.hip, small_preferred): 32x32 tiles, the k loop
+        // split until there are ~1536 work-groups (ranges of >= 8 k-tiles of 32): batch-16
+        // 8 x 6000 x 1024 (512 tiles) 89.0 us in 3 ranges, 178.5 whole
+        cfg = 32;
+        const int64_t t32 = tiles(32, 32);
+        const int64_t want = (1536 + t32 - 1) / t32;
+        int64_t cap = nk32 / 8 < 8 ? nk32 / 8 : 8;
+        if (cap < 1) cap = 1;
+        splits = (int)(want < cap ? want : cap);
+    } else if (tiles(128, 128) >= 512) {
         cfg = 128;
     } else if (d.K >= 4096 && d.M >= 128 && d.N >= 128 && tiles(128, 128) >= 128) {
         // Long K over few tiles. Weighed by time ~ rounds of 256 work-groups x 2 area
@@ -725,10 +735,27 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
             const double best = std::min(std::min(c64, c0), std::min(c1, c2));
             cfg = best == c64 ? 64 : 128;
             big = best == c2 ? 2 : (best == c1 ? 1 : 0);
+        } else if (d.K <= 320 && fits) {
+            // Element-wise loads and a short k loop: 64x64 tiles, several work-groups per CU
+            // overlapping one another's prologue and C store (graph replay, us, 64x64 /
+            // 128x128: 4001 x 101 x 4003 48.1 / 72.0, 3001 x 203 x 5001 67.6 / 85.1, 6000 x
+            // 250 x 6001 NT 183.2 / 214.0, 2047 x 61 x 8191 TT 36.8 / 62.8, 3001 x 301 x 3001
+            // TN 55.8 / 70.0; from K = 400 the larger tiles win: 8000 x 400 x 4001 238.5 /
+            // 222.7).
+            cfg = 64;
+            big = 0;
         } else {
+            // 64x64 tiles weigh in at 0.88 of the 256x256 rate, fitted to five shapes (graph
+            // replay, us, 64x64 / 128x128: 1231 x 4246 x 7348 NT 598 / 745, batch-8 701 x 1107
+            // x 1602 TT 166 / 209, 12000 x 500 x 6565 702 / 633, 6000 x 1000 x 6001 595 /
+            // 542, 4096 x 4095 x 4095 980 / 951 with 256x256 at 941); the estimate picks the
+            // faster of the two in all five.
+            const double c64 = fits ? cost(64, 64, 0.88, 0) : 1e300;
             const double c0 = cost(128, 128, 0.966, 0), c1 = cost(128, 256, 0.981, 16);
             const double c2 = cost(256, 256, 1.0, 32);
-            big = c2 <= c1 && c2 <= c0 ? 2 : (c1 <= c0 ? 1 : 0);
+            const double best = std::min(std::min(c64, c0), std::min(c1, c2));
+            cfg = best == c64 ? 64 : 128;
+            big = best == c2 ? 2 : (best == c1 ? 1 : 0);
         }
     }
     // tuning overrides (migemm_set_tuning), validated when they were set

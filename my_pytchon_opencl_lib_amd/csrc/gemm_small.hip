@@ -403,10 +403,28 @@ SmallPlan plan_small(const GemmDesc &d) {
 //      200 x 2048 x 300 14.7 / 11.6 and 6000 x 2048 x 64 28.7 / 26.8 split;
 //    - longer K with at most 8 tiles (64 x 4096 x 512 10.5 / 11.8; 128 x 8192 x 128 11.7 /
 //      13.4; 256 x 4096 x 256 takes the tiled split, 14.2 / 13.6).
+bool narrow_rows_streaming(const GemmDesc &d) {
+    return d.M > 4 && d.M <= 16 && !d.transB &&
+           (int64_t)d.K * d.N * d.batch * 4 >= ((int64_t)256 << 20);
+}
+
 bool small_preferred(const GemmDesc &d) {
-    if (d.M <= 4 || d.N <= 4) return true;
+    // Outputs 16 or fewer rows (or columns) wide: the tiled kernels' 64-256 wide tiles would
+    // be mostly empty (graph replay, us, small / tiled: batch-32 8 x 195 x 3480 20.9 / 53.9,
+    // batch-32 3000 x 200 x 12 21.0 / 33.0, batch-16 2048 x 512 x 16 TN 16.8 / 22.6,
+    // batch-16 16 x 1024 x 4096 58.9 / 68.0).
+    // Except few rows over a B of 256 MB or more (B not transposed): the tiled kernel's 32x32
+    // tiles stream B in longer row segments (batch-16 16 x 2048 x 4096 100.8 / 157.4 us on
+    // this kernel, batch-16 8 x 6000 x 1024 89.0 / 115.8, batch-16 16 x 1024 x 4096 46.1 /
+    // 57.6; batch-16 8 x 2048 x 1024, 134 MB, 32.8 / 28.9).
+    if (narrow_rows_streaming(d)) return false;
+    if (d.M <= 16 || d.N <= 16) return true;
     const int64_t tiles64 = cdiv(d.M, 64) * cdiv(d.N, 64) * d.batch;
     if (tiles64 >= 256) return false;
+    // Short K below one round of 64x64 tiles: the tiled kernel's 32x32 tiles lose to these
+    // (1000 x 100 x 700 6.95 / 9.15, 3567 x 164 x 199 TN 11.1 / 15.5, batch-2 187 x 129 x
+    // 1259 TN 7.8 / 12.3, batch-8 300 x 84 x 200 6.4 / 7.9).
+    if (d.K < 256) return true;
     const int mn = d.M < d.N ? d.M : d.N;
     if (mn <= 32 || d.K <= 64) return true;
     if (d.K <= 2048) {

@@ -241,7 +241,11 @@ bool tiny_supported(const GemmDesc &d) {
 //    4096 4.19 / 4.85; batch-32 128 x 256 x 128 NT 5.40 / 5.94), which is therefore asked
 //    first.
 bool tiny_preferred(const GemmDesc &d) {
-    if (!tiny_supported(d) || d.M < 16 || d.N < 16) return false;
+    // Outputs under 16 rows or columns only with one wavefront per tile (batch-32 15 x 77 x 1550
+    // 6.1 us against 6.8 on the small kernel, batch-8 5 x 62 x 4700 TT 5.0 / 5.7; but 8 x 256
+    // x 4096 on four wavefronts per tile 5.0 / 4.2).
+    if (!tiny_supported(d)) return false;
+    if ((d.M < 16 || d.N < 16) && tiny_parts(d) != 1) return false;
     const int64_t t = tiles16(d);
     if (tiny_parts(d) == 1) {
         // (B transposed took the small kernel above K = 48 while the K-contiguous loads

@@ -109,8 +109,11 @@ bool tiny_supported(const GemmDesc &d);
 bool tiny_preferred(const GemmDesc &d);
 int launch_gemm_tiny(hipStream_t stream, const GemmDesc &d);
 int launch_gemm_panel(hipStream_t stream, const GemmDesc &d);
-// True when C has too few 64x64 tiles to occupy the 256 CUs (gemm_small_kernel).
+// True when C has too few 64x64 tiles to occupy the 256 CUs, or is 16 or fewer rows or
+// columns wide (gemm_small_kernel).
 bool small_preferred(const GemmDesc &d);
+// 5-16 rows of C over a B (not transposed) of 256 MB or more: the tiled kernel's 32x32 tiles.
+bool narrow_rows_streaming(const GemmDesc &d);
 
 // Device workspace owned by the library: one growing buffer per device, stream and slot.
 // Slot 0 holds split-K partial sums (GEMM, column sums); slot 1 holds operands staged by
