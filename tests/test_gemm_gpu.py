@@ -702,3 +702,38 @@ def test_nonfinite_inputs_propagate(nncl, policy, M, K, N, ta, tb):
     assert np.array_equal(np.isneginf(got), neg)
     ok = ~(nan | pos | neg)
     assert np.array_equal(got[ok], fin[ok].astype(np.float32))
+
+
+# Shapes the dispatcher sends to particular kernels under AUTO (the regimes a random-shape audit
+# of the dispatcher found): each is checked against fp64 with the kernel it must run.
+AUTO_REGIMES = [
+    # 5-16 rows over >= 256 MB of B: 32x32 tiles, k split to ~1536 work-groups
+    (dict(batch=16, M=8, K=6000, N=1024, ta=0, tb=0), "tiled-staged tile=32x32 splits=3"),
+    # operands not loadable 16 bytes per lane, short K, large output: 64x64 tiles
+    (dict(batch=1, M=2047, K=61, N=2051, ta=1, tb=1), "tiled-direct tile=64x64"),
+    # 16 or fewer rows: the small kernel, or the short-K kernel for K <= 80
+    (dict(batch=32, M=8, K=195, N=1000, ta=0, tb=0), "small"),
+    (dict(batch=8, M=10, K=75, N=2166, ta=0, tb=0), "tiny"),
+    # few 64x64 tiles and K < 256: the small kernel
+    (dict(batch=1, M=1000, K=100, N=700, ta=0, tb=0), "small"),
+    # a weight stored [N, K] at M = 1: rows streamed whole
+    (dict(batch=1, M=1, K=4096, N=2048, ta=0, tb=1), "skinny-rows"),
+]
+
+
+@pytest.mark.parametrize("spec,plan", AUTO_REGIMES)
+def test_auto_regimes(nncl, spec, plan):
+    from my_pytchon_opencl_lib_amd import _native
+    b, M, K, N, ta, tb = (spec[k] for k in ("batch", "M", "K", "N", "ta", "tb"))
+    say("auto regime", spec, plan)
+    rng = np.random.default_rng(M * 7 + K + N)
+    A = rng.uniform(-1, 1, (b, K, M) if ta else (b, M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (b, N, K) if tb else (b, K, N)).astype(np.float32)
+    prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_AUTO)
+    try:
+        C = host(nncl.gemm(dev(A), dev(B), transA=bool(ta), transB=bool(tb)))
+        assert _native.last_plan().startswith(plan), _native.last_plan()
+    finally:
+        _native.set_gemm_policy(prev)
+    check_gemm(C.reshape(b, M, N), A, B, ta, tb, M=M, N=N, K=K, lda=M if ta else K,
+               ldb=K if tb else N, sA=M * K, sB=K * N, batch=b, rows=sample_rows(M, 32))
