@@ -708,8 +708,14 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
                 // 1.5x their fitted overhead: on a grid of 200 shapes (M, N in 1000..8000, K
                 // in 256..4096, NN and TN, every tile timed) the picks' total time above the
                 // per-shape best falls from 0.32 % to 0.18 %, and 3000 x 256 x 8000 takes
-                // 64x64 tiles (115.1 us) instead of 128x256 (136.7 us).
-                const double s = d.K <= 512 ? 1.5 : 1.0;
+                // 64x64 tiles (115.1 us) instead of 128x256 (136.7 us). Outputs of 4096 or
+                // more 128x128 tiles (8 or more rounds of 128x256) are exempt: over that many
+                // rounds the work-groups drift apart and overlap one another's prologue and
+                // store. On 84 outputs of 2000-16000 x 2048-8192 at K = 256-768 the picks'
+                // total time above the per-shape best falls from 1.1 % to 0.25 %; the
+                // Python Linear(500 -> 6565) forward, 12000 x 500 x 6565 NT, takes 128x256
+                // tiles (670 us) instead of 64x64 (740-754).
+                const double s = d.K <= 512 && tiles(128, 128) < 4096 ? 1.5 : 1.0;
                 // C rows that do not start on 128-byte lines are stored as partial lines, and
                 // a 256x256 work-group (one per CU) cannot hide that store burst behind other
                 // work-groups' k loops; up to K = 1024 its overhead counts twice then (graph
