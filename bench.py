@@ -13,6 +13,8 @@ Prints ONE JSON line on stdout. Besides the step it carries, by default:
                      floor (a one-element fill kernel replayed the same way), for the small
                      configs a data-movement floor (a torch kernel that reads and writes the
                      same bytes) and torch's own fp32 GEMM of the shape (torch_blas_us);
+  callers            the path's callers at the reference's sizes (the Linear(500 -> 6565)
+                     layer forward and backward, the LSTM GEMM stages and recurrent step);
   roofline           the dominant 4096^3 kernel, from HIP events in this run (frac) and from
                      the committed rocprofv3 kernel trace of this bench (frac_profiled);
   cpu_baseline       the oracle's restatement of the reference matmul_tiled arithmetic
@@ -263,6 +265,7 @@ def main():
     value = 3 * FLOP_4096 / (ms_per_step * 1e-3) / 1e12
 
     configs = measure_all_configs(torch, nncl, _native) if args.configs == "all" else None
+    callers = measure_callers(torch, nncl, _native) if args.configs == "all" else None
     ref = None if args.no_reference else reference_same_gpu(per_form["NN"]["ms"])
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
 
@@ -304,6 +307,7 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": roofline,
         "configs": configs,
+        "callers": callers,
         "reference_same_gpu": ref,
         "cpu_baseline": cpu,
     }
@@ -443,6 +447,27 @@ def summarize_trace(directory, steps, warmup):
     print("\n".join(lines))
 
 
+def graph_timed(torch, cap, fns, per):
+    """Device ms per call: HIP events around 5 replays of a HIP graph that runs the calls
+    `fns` `per` times back to back, captured on stream `cap` (its own library workspace, sized
+    by one eager round on it first)."""
+    with torch.cuda.stream(cap):
+        for f in fns:
+            f()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        for _ in range(per):
+            for f in fns:
+                f()
+    graph.replay()
+    torch.cuda.synchronize()
+    t = Timer(torch)
+    for _ in range(5):
+        t.around(graph.replay)
+    return t.mean_ms() / (per * len(fns))
+
+
 def measure_all_configs(torch, nncl, _native, calls=100):
     """Per-config device time per call, from HIP events around a HIP graph that replays
     `calls` back-to-back calls (so host launch overhead is not measured, and the graph's own
@@ -458,22 +483,7 @@ def measure_all_configs(torch, nncl, _native, calls=100):
     cap = torch.cuda.Stream()  # the capturing stream: its own library workspace
 
     def timed(fns, per=None):
-        per = per or max(1, calls // len(fns))
-        with torch.cuda.stream(cap):  # sizes cap's workspace before the capture
-            for f in fns:
-                f()
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=cap):
-            for _ in range(per):
-                for f in fns:
-                    f()
-        graph.replay()
-        torch.cuda.synchronize()
-        t = Timer(torch)
-        for _ in range(5):
-            t.around(graph.replay)
-        return t.mean_ms() / (per * len(fns))
+        return graph_timed(torch, cap, fns, per or max(1, calls // len(fns)))
 
     z = torch.empty(1, device=dev)
     floor_us = timed([lambda: z.fill_(1.0)]) * 1e3
@@ -562,6 +572,66 @@ def measure_all_configs(torch, nncl, _native, calls=100):
     c0, c1 = r(256, 256), torch.empty(256, 256, device=dev)
     out["copy_floor"] = {"us": round(timed([lambda: c1.copy_(c0)]) * 1e3, 2),
                          "kernel": "torch copy of 256 KB, graph-replayed back to back"}
+    return out
+
+
+def measure_callers(torch, nncl, _native):
+    """The path's callers at the sizes the reference runs them, through the host interface
+    (graph replay as for the configs, device us per call):
+      Linear(500 -> 6565) on [8, 1500, 500] (TestLSTMRealTrain/EncoderDecoder.cs:29,75): the
+        C# forward NnClGlob.LinearForward (W [1, 500, 6565], linear.cl), the Python
+        Linear.forward (W [6565, 500], core/layers.py:21-33) as one NT GEMM, LinearOp.Backward
+        dX (NT), dW (one TN GEMM over 12000 rows) and db (column sum);
+      the LSTM of BASELINE config 3 (batch 64 x 100 steps, input 512, hidden 1024): the three
+        GEMM stages of NnClGlob.Lstm / LstmBackward and the recurrent product of one step
+        (lstm.cl:80-101), rotating over the 99 steps that have one."""
+    from my_pytchon_opencl_lib_amd import layers
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    cap = torch.cuda.Stream()
+    r = lambda *s: torch.randn(*s, device=dev, generator=g)
+    out = {}
+
+    def rec(name, fns, per, flop=0, byts=0):
+        ms = graph_timed(torch, cap, fns, per)
+        fns[0]()
+        e = {"us": round(ms * 1e3, 1), "kernel": _native.last_plan()}
+        if flop:
+            tf = flop / (ms * 1e-3) / 1e12
+            e.update(tflops=round(tf, 1), frac_mfma=round(tf / PEAK_FP32_MFMA_TFLOPS, 3))
+        if byts:
+            gbs = byts / (ms * 1e-3) / 1e9
+            e.update(GBps=round(gbs, 1), frac_hbm=round(gbs / PEAK_HBM_GBS, 3))
+        out[name] = e
+
+    B, M, K, N = 8, 1500, 500, 6565
+    fl = 2 * B * M * K * N
+    X, W, bias, G = r(B, M, K), r(1, K, N) / 22, r(N) / 22, r(B, M, N) / 64
+    rec("linear_forward_cs 12000x500->6565 +bias", [lambda: nncl.LinearForward(X, W, bias)], 5, fl)
+    lin = layers.Linear(K, N, nncl, weight=r(N, K) / 22)
+    rec("linear_forward_py 12000x500->6565 (NT)", [lambda: lin(X)], 5, fl)
+    rec("linear_dX 12000x6565->500 (NT)", [lambda: nncl.BmmPermute(G, W, transB=True)], 5, fl)
+    rec("linear_dW 500x6565 over 12000 rows (TN)", [lambda: nncl.linear_weight_grad(X, G)], 5, fl)
+    rec("linear_db column sum 12000x6565", [lambda: nncl.LinearBiasBackward(G, [N])], 20,
+        byts=4 * (B * M * N + N))
+    del X, G, lin
+    bs, seq, F, H = 64, 100, 512, 1024
+    T, Gs = bs * seq, 4 * H
+    Xl, Wl, bl, Gr = r(bs, seq, F), r(F, Gs) / 32, r(Gs) / 32, r(T, Gs) / 64
+    Hout, U = r(bs, seq, H), r(H, Gs) / 32
+    gW, gU, gB = (torch.zeros(F, Gs, device=dev), torch.zeros(H, Gs, device=dev),
+                  torch.zeros(Gs, device=dev))
+    rec("lstm_gemm_xw 6400x512->4096 +bias", [lambda: nncl.LstmGemmXW(Xl, Wl, bl)], 10,
+        2 * T * F * Gs)
+    rec("lstm_gemm_grad_x 6400x4096->512", [lambda: nncl.LstmGemmGradX(Gr, Wl, (bs, seq, F))],
+        10, 2 * T * F * Gs)
+    rec("lstm_gemm_grad_weights (W, U, bias)",
+        [lambda: nncl.LstmGemmGradWeights(Xl, Hout, Gr, gW, gU, gB)], 5, 2 * T * (F + H) * Gs)
+    XW = r(bs, seq, Gs)
+    rec("lstm_recurrent_step 64x1024->4096 (+= XW_t)",
+        [lambda t=t: nncl.LstmRecurrentGates(XW, Hout, U, t) for t in range(1, seq)], 1,
+        2 * bs * H * Gs)
     return out
 
 
