@@ -751,12 +751,15 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
             cfg = 64;
             big = 0;
         } else {
-            // 64x64 tiles weigh in at 0.88 of the 256x256 rate, fitted to five shapes (graph
-            // replay, us, 64x64 / 128x128: 1231 x 4246 x 7348 NT 598 / 745, batch-8 701 x 1107
-            // x 1602 TT 166 / 209, 12000 x 500 x 6565 702 / 633, 6000 x 1000 x 6001 595 /
-            // 542, 4096 x 4095 x 4095 980 / 951 with 256x256 at 941); the estimate picks the
-            // faster of the two in all five.
-            const double c64 = fits ? cost(64, 64, 0.88, 0) : 1e300;
+            // 64x64 tiles weigh in at 0.91 of the 256x256 rate. Fitted first to five shapes
+            // (graph replay, us, 64x64 / 128x128: 1231 x 4246 x 7348 NT 598 / 745, batch-8
+            // 701 x 1107 x 1602 TT 166 / 209, 12000 x 500 x 6565 702 / 633, 6000 x 1000 x
+            // 6001 595 / 542, 4096 x 4095 x 4095 980 / 951 with 256x256 at 941; the estimate
+            // picks the faster in all five), then raised from 0.88 on 49 audited outputs of
+            // 256-16384 per side (picks' time above the per-shape best 1.13 -> 0.72 %) and
+            // checked on 40 others: 5 picks changed, each 2-12 % faster (8948 x 1088 x 3283
+            // 558.0 -> 489.6), 0.5 % less in total.
+            const double c64 = fits ? cost(64, 64, 0.91, 0) : 1e300;
             const double c0 = cost(128, 128, 0.966, 0), c1 = cost(128, 256, 0.981, 16);
             const double c2 = cost(256, 256, 1.0, 32);
             const double best = std::min(std::min(c64, c0), std::min(c1, c2));
