@@ -756,7 +756,7 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
             // 701 x 1107 x 1602 TT 166 / 209, 12000 x 500 x 6565 702 / 633, 6000 x 1000 x
             // 6001 595 / 542, 4096 x 4095 x 4095 980 / 951 with 256x256 at 941; the estimate
             // picks the faster in all five), then raised from 0.88 on 49 audited outputs of
-            // 256-16384 per side (picks' time above the per-shape best 1.13 -> 0.72 %) and
+            // 256-16384 per side (picks' time above the per-shape best 1.13 -> 0.84 %) and
             // checked on 40 others: 5 picks changed, each 2-12 % faster (8948 x 1088 x 3283
             // 558.0 -> 489.6), 0.5 % less in total.
             const double c64 = fits ? cost(64, 64, 0.91, 0) : 1e300;
