@@ -718,6 +718,9 @@ AUTO_REGIMES = [
     (dict(batch=1, M=1000, K=100, N=700, ta=0, tb=0), "small"),
     # a weight stored [N, K] at M = 1: rows streamed whole
     (dict(batch=1, M=1, K=4096, N=2048, ta=0, tb=1), "skinny-rows"),
+    # a tiny output over a huge K (dot products): the small kernel in 256 k ranges
+    (dict(batch=1, M=1, K=1000000, N=1, ta=0, tb=0), "small tile=16x16 splits=256"),
+    (dict(batch=1, M=7, K=300000, N=9, ta=0, tb=1), "small tile=16x16 splits=254"),
 ]
 
 
