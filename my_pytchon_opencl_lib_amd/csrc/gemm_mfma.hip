@@ -696,7 +696,13 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     // 256x256 work-groups fill a CU alone, their prologue and C store not overlapped (about
     // 32 k-steps per tile, 16 for 128x256), which decides short K: 12000 x 6565 x 500 runs
     // 729 us at 128x128, 747 at 256x256.
-    if (cfg == 128 && splits == 1 && tiles(128, 128) >= 512) {
+    if (cfg == 128 && splits == 1 && tiles(128, 128) >= 512 && d.K <= 16) {
+        // K <= 16: writing C is the work; 128x128 tiles, whole 128-byte lines per row and
+        // four work-groups per CU (us, 64x64 / 128x128 / 256x256: 65536 x 3 x 4096 297.4 /
+        // 217.5 / 241.0; 16384 x 8 x 16384 271.8 / 275.0 / 284.8; 20000 x 16 x 20000 446.0 /
+        // 336.1 / 376.6)
+        big = 0;
+    } else if (cfg == 128 && splits == 1 && tiles(128, 128) >= 512) {
         const double k = d.K;
         auto cost = [&](int bm, int bn, double rate, double over) {
             return (double)((tiles(bm, bn) + 255) / 256) * bm * bn * (k + over) / rate;

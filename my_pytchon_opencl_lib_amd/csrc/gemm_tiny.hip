@@ -252,6 +252,17 @@ bool tiny_preferred(const GemmDesc &d) {
         // read 16 rows per 16 lanes; read coalesced it runs as NN does: batch-32 128 x 64 x
         // 128 NT 3.11 us against 4.01 on the small kernel, 512 x 64 x 512 2.63 / 3.31)
         if (t < (d.K <= 48 ? 512 : 1024)) return false;
+        // Outputs of 64 MB or more over K <= 16 are bound by writing C: where C's rows start
+        // on 128-byte lines the tiled kernel's 128x128 tiles store whole lines, these 16x16
+        // tiles half lines (graph replay, us, this kernel / 128x128: 65536 x 3 x 4096 395.3
+        // / 220.3, 16384 x 8 x 16384 429.2 / 268.6, 9868 x 8 x 6208 NT 136.9 / 61.0, batch-16
+        // 1024 x 8 x 1024 31.7 / 21.5; a torch fill of the same C: 157.3 for the first).
+        // Rows off the lines make each of the larger tiles' row stores straddle two lines,
+        // and this kernel stays (7008 x 6 x 6220 54.0 / 128.7, 4556 x 1 x 14292 65.5 /
+        // 204.5).
+        if (d.K <= 16 && t >= 65536 && d.ldc % 32 == 0 && (d.batch == 1 || d.sC % 32 == 0) &&
+            ((uintptr_t)d.C & 127) == 0)
+            return false;
         if (d.K <= 16) return true;
         return t <= (d.K <= 48 ? 8192 : 4096);
     }

@@ -721,6 +721,10 @@ AUTO_REGIMES = [
     # a tiny output over a huge K (dot products): the small kernel in 256 k ranges
     (dict(batch=1, M=1, K=1000000, N=1, ta=0, tb=0), "small tile=16x16 splits=256"),
     (dict(batch=1, M=7, K=300000, N=9, ta=0, tb=1), "small tile=16x16 splits=254"),
+    # outputs of >= 64 MB over K <= 16 with C rows on 128-byte lines: 128x128 tiles
+    (dict(batch=1, M=8192, K=4, N=8192, ta=0, tb=0), "tiled-direct tile=128x128"),
+    # the same with rows off the lines: the short-K kernel
+    (dict(batch=1, M=7008, K=6, N=6220, ta=0, tb=0), "tiny"),
 ]
 
 
