@@ -696,6 +696,9 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     // 256x256 work-groups fill a CU alone, their prologue and C store not overlapped (about
     // 32 k-steps per tile, 16 for 128x256), which decides short K: 12000 x 6565 x 500 runs
     // 729 us at 128x128, 747 at 256x256.
+    // C's rows start on 64-byte boundaries (every batch entry's too)
+    const bool rows64 = d.ldc % 16 == 0 && ((uintptr_t)d.C & 63) == 0 &&
+                        (d.batch == 1 || d.sC % 16 == 0);
     if (cfg == 128 && splits == 1 && tiles(128, 128) >= 512 && d.K <= 16) {
         // K <= 16: writing C is the work; 128x128 tiles, whole 128-byte lines per row and
         // four work-groups per CU (us, 64x64 / 128x128 / 256x256: 65536 x 3 x 4096 297.4 /
@@ -734,10 +737,17 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
                 // picks with such C rows ran 0.76-0.96x as long at K <= 1024 (5000 x 256 x
                 // 3000 NT 93.9 -> 71.7 us in 64x64 tiles), but 1.01x at K = 4096.
                 const bool cmis = (d.ldc % 32 != 0 || ((uintptr_t)d.C & 127) != 0) && d.K <= 1024;
+                // Rows off 64-byte boundaries as well cost every tile wider than 64 about 110
+                // k-steps more per tile at K <= 256 (the C store; 8192 x 64 x 8180 against
+                // 8192 x 64 x 8192, us: 128x128 215.8 / 114.8, 256x256 220.4 / 120.8, 64x64
+                // 124.0 / 121.1), which then replaces the 256x256 term above. By K = 500 the
+                // other work-groups' k loops hide it (12000 x 500 x 6565 NT 728 in 128x256
+                // tiles, 787 in 64x64).
+                const double om = !rows64 && d.K <= 256 ? 110.0 : 0.0;
                 c64 = cost(64, 64, 135.2, 95);
-                c0 = cost(128, 128, 147.6, 90 * s);
-                c1 = cost(128, 256, 152.1, 98 * s);
-                c2 = cost(256, 256, 152.6, 75 * s * (cmis ? 2.0 : 1.0));
+                c0 = cost(128, 128, 147.6, 90 * s + om);
+                c1 = cost(128, 256, 152.1, 98 * s + om);
+                c2 = cost(256, 256, 152.6, 75 * s + (om > 0 ? om : cmis ? 75 * s : 0.0));
             } else {
                 c64 = cost(64, 64, 134.2, 75);
                 c0 = cost(128, 128, 138.9, 78);
@@ -748,13 +758,16 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
             cfg = best == c64 ? 64 : 128;
             big = best == c2 ? 2 : (best == c1 ? 1 : 0);
         } else if (d.K <= 320 && fits) {
-            // Element-wise loads and a short k loop: 64x64 tiles, several work-groups per CU
-            // overlapping one another's prologue and C store (graph replay, us, 64x64 /
-            // 128x128: 4001 x 101 x 4003 48.1 / 72.0, 3001 x 203 x 5001 67.6 / 85.1, 6000 x
-            // 250 x 6001 NT 183.2 / 214.0, 2047 x 61 x 8191 TT 36.8 / 62.8, 3001 x 301 x 3001
-            // TN 55.8 / 70.0; from K = 400 the larger tiles win: 8000 x 400 x 4001 238.5 /
-            // 222.7).
-            cfg = 64;
+            // Element-wise loads and a short k loop, where the C store weighs: 64x64 tiles
+            // when C's rows are off 64-byte boundaries (graph replay, us, 64x64 / 128x128:
+            // 4001 x 101 x 4003 48.1 / 72.0, 3001 x 203 x 5001 67.6 / 85.1, 6000 x 250 x 6001
+            // NT 183.2 / 214.0, 2047 x 61 x 8191 TT 36.8 / 62.8, 3001 x 301 x 3001 TN 55.8 /
+            // 70.0; from K = 400 the larger tiles win: 8000 x 400 x 4001 238.5 / 222.7),
+            // 128x128 when they are on them and there are >= 6 rounds of tiles (11079 x 94 x
+            // 11104 TN 314.5 / 265.2, 15658 x 73 x 10496 TN 363.7 / 306.8, 12110 x 41 x 11152
+            // TT 232.4 / 196.0; with fewer 64x64 still wins: 2501 x 96 x 5008 TT 36.3 / 42.0,
+            // 3343 x 85 x 6128 NT 53.1 / 60.8).
+            cfg = rows64 && tiles(128, 128) >= 1536 ? 128 : 64;
             big = 0;
         } else {
             // 64x64 tiles weigh in at 0.91 of the 256x256 rate. Fitted first to five shapes

@@ -725,6 +725,10 @@ AUTO_REGIMES = [
     (dict(batch=1, M=8192, K=4, N=8192, ta=0, tb=0), "tiled-direct tile=128x128"),
     # the same with rows off the lines: the short-K kernel
     (dict(batch=1, M=7008, K=6, N=6220, ta=0, tb=0), "tiny"),
+    # short K, C rows off 64-byte boundaries: 64x64 tiles; on them (operands loaded 4 bytes
+    # per lane, >= 6 rounds of tiles): 128x128
+    (dict(batch=1, M=8192, K=64, N=8180, ta=0, tb=0), "tiled-direct tile=64x64"),
+    (dict(batch=1, M=12592, K=47, N=2304, ta=0, tb=0), "tiled-direct tile=128x128"),
 ]
 
 
