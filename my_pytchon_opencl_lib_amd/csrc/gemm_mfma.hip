@@ -813,6 +813,9 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         fits && cfg != 32 && (splits == 1 || big != 1 || direct_mode == 2);
 
     a.splits = splits;
+    // C stored through L2 by tiles 128 or more wide whose rows are off 64-byte boundaries
+    // (tiled_common.h, store_tile)
+    a.write_back = cfg == 128 && !rows64;
     a.partial = nullptr;
     if (splits > 1) {
         int st = MIGEMM_OK;

@@ -28,6 +28,7 @@ struct TiledArgs {
     int kt_per_split;      // k-tiles per range
     float *partial;        // [splits][batch][M][N] partial sums when splits > 1
     int accumulate;        // C += result instead of C = result
+    int write_back;        // C stored through L2 (write-back) instead of non-temporally
     // launch-invariant divisors of tile_coord (multiply-high divisions), set by
     // set_tile_divisors once tiles_m, tiles_n, batch are final
     FastDiv per_split;     // tiles_m * tiles_n * batch
@@ -106,13 +107,19 @@ __device__ __forceinline__ void store_tile(const TiledArgs &p, const TileCoord &
         return;
     }
     float *Cb = p.C + (int64_t)tc.b * p.sC;
-    // Two copies of the store loop behind a uniform branch, so the plain store never
-    // carries a (speculated) load of C. The plain store is non-temporal: every work-group of
-    // a large GEMM writes its tile at about the same time, at the end, and dirty C lines held
-    // in L2 are written back when the kernel ends, before the next kernel on the stream can
-    // start (4096^3 forms back to back: 2.758-2.768 -> 2.750-2.756 ms per step of three).
-    // Split-K partials keep ordinary stores: the reduction reads them right away.
-    auto store = [&](auto accumulate) {
+    // Copies of the store loop behind a uniform branch, so a plain store never carries a
+    // (speculated) load of C. The plain store is non-temporal: every work-group of a large
+    // GEMM writes its tile at about the same time, at the end, and dirty C lines held in L2
+    // are written back when the kernel ends, before the next kernel on the stream can start
+    // (4096^3 forms back to back: 2.758-2.768 -> 2.750-2.756 ms per step of three).
+    // p.write_back (tiles 128 or more wide whose C rows do not start on 64-byte boundaries)
+    // stores through L2 instead: each row of such a tile begins and ends in a line it shares
+    // with a neighbouring tile, and L2 merges the two parts before the line goes to HBM
+    // (graph replay, us, non-temporal / write-back: 8192 x 64 x 8180 in 128x128 tiles
+    // 213.3 / 129.4, 12000 x 500 x 6565 NT in 128x256 686.7 / 647.8, 4096 x 4096 x 4095 TN
+    // in 256x256 942.9 / 924.2; 64x64 tiles lose with it, 12000 x 80 x 6565 NT 172.7 /
+    // 189.0). Split-K partials keep ordinary stores: the reduction reads them right away.
+    auto store = [&](auto mode) {  // 0: non-temporal, 1: write-back, 2: C += result
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const int col = c0 + j * 32 + lo;
@@ -128,8 +135,10 @@ __device__ __forceinline__ void store_tile(const TiledArgs &p, const TileCoord &
                         float v = acc[i][j][r];
                         if (p.bias != nullptr) v = v + bv;
                         float *c = Cb + (int64_t)row * p.ldc + col;
-                        if constexpr (decltype(accumulate)::value)
+                        if constexpr (decltype(mode)::value == 2)
                             *c = *c + v;
+                        else if constexpr (decltype(mode)::value == 1)
+                            *c = v;
                         else
                             __builtin_nontemporal_store(v, c);
                     }
@@ -138,9 +147,11 @@ __device__ __forceinline__ void store_tile(const TiledArgs &p, const TileCoord &
         }
     };
     if (p.accumulate)
-        store(std::true_type{});
+        store(std::integral_constant<int, 2>{});
+    else if (p.write_back)
+        store(std::integral_constant<int, 1>{});
     else
-        store(std::false_type{});
+        store(std::integral_constant<int, 0>{});
 }
 
 // Tiles of bm x bn (256x256, 128x256, 128x128 or 64x64) with operands loaded straight into
