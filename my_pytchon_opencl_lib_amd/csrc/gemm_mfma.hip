@@ -622,12 +622,20 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         // 512 x 6400 x 4096 TN 256-split 207.9, 64x64 203.2 (chosen); 1000 x 4096 x 3000
         // 128-split 249.7, 64x64 198.4 (chosen); 500 x 12000 x 6565 TN 128-split 685.0
         // (chosen), 64x64 722.4; 12000 x 6565 x 500 NT 128-split 669.8, 64x64 633.1 (chosen).
+        // 64x64 tiles are also weighed in 2-4 ranges, and operands loaded 4 bytes per lane
+        // (not `direct`) lower the rates of 64x64 and 128x128 tiles to 0.85 and 0.95: on 30
+        // shapes of this regime (K 4096-16384, every tile and range count timed) the picks'
+        // time above the per-shape best fell from 7.1 % to 2.7 % (800 x 5000 x 2500 NT 213.4
+        // -> 184.0 us in four 64x64 ranges, 160 x 10116 x 11952 490.6 -> 418.7, the LSTM
+        // gate gradient 6400 x 4096 x 512 NT 230.9 -> 220.3 in three).
+        const double e64 = direct ? 1.0 : 0.85, e128 = direct ? 1.0 : 0.95;
         auto traffic = [&](int s) { return (2.0 * s + 1) * d.M * d.N * 4.0 * d.batch / 6e6; };
         const int64_t t128 = tiles(128, 128), t256 = tiles(256, 256), t64 = tiles(64, 64);
         int64_t want = (1024 + t128 - 1) / t128;
         want += want & 1;
         const int s128 = (int)(want < 8 ? want : 8);
-        double best = est(t128 * s128, 16384, (double)d.K / s128, 78, 138.9) + traffic(s128);
+        double best =
+            est(t128 * s128, 16384, (double)d.K / s128, 78, 138.9 * e128) + traffic(s128);
         cfg = 128;
         splits = s128;
         if (av && bv && (t256 == 32 || t256 == 64)) {
@@ -640,11 +648,15 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
                 splits = s256;
             }
         }
-        if (fits && est(t64, 4096, d.K, 95, 135.2) < best) {
-            best = est(t64, 4096, d.K, 95, 135.2);
-            cfg = 64;
-            big = 0;
-            splits = 1;
+        for (int s = 1; s <= 4 && fits; ++s) {
+            const double c = est(t64 * s, 4096, (double)d.K / s, 95, 135.2 * e64) +
+                             (s > 1 ? traffic(s) : 0.0);
+            if (c < best) {
+                best = c;
+                cfg = 64;
+                big = 0;
+                splits = s;
+            }
         }
         if (direct) {
             int c = cfg, b = big;
