@@ -264,7 +264,11 @@ bool tiny_preferred(const GemmDesc &d) {
             ((uintptr_t)d.C & 127) == 0)
             return false;
         if (d.K <= 16) return true;
-        return t <= (d.K <= 48 ? 8192 : 4096);
+        // Above these tile counts larger outputs go to the tiled kernel; outputs under 16 rows
+        // or columns stay here (graph replay, us, small kernel / this one: batch-32 11 x 33 x
+        // 18406 38.0 / 20.8, batch-32 2 x 35 x 7626 TN 18.9 / 12.0, 8 x 40 x 200000 16.0 /
+        // 11.0, batch-4 100000 x 50 x 7 26.4 / 19.8; 29 of 30 such shapes faster here).
+        return t <= (d.K <= 48 ? 8192 : 4096) || d.M < 16 || d.N < 16;
     }
     // From 64 tiles when A is K-contiguous (coalesced loads; graph replay, us, small kernel
     // / this one: 256 x 256 x 256 NN 2.94 / 2.50, NT 2.83 / 2.63, 128 x 256 x 128 NN 2.81 /

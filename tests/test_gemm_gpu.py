@@ -714,6 +714,7 @@ AUTO_REGIMES = [
     # 16 or fewer rows: the small kernel, or the short-K kernel for K <= 80
     (dict(batch=32, M=8, K=195, N=1000, ta=0, tb=0), "small"),
     (dict(batch=8, M=10, K=75, N=2166, ta=0, tb=0), "tiny"),
+    (dict(batch=32, M=2, K=35, N=7626, ta=1, tb=0), "tiny"),
     # few 64x64 tiles and K < 256: the small kernel
     (dict(batch=1, M=1000, K=100, N=700, ta=0, tb=0), "small"),
     # a weight stored [N, K] at M = 1: rows streamed whole
