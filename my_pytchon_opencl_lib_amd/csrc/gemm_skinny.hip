@@ -342,7 +342,15 @@ bool skinny_supported(const GemmDesc &d) {
 // N = 4096 the small kernel wins (4 x 4096 x 4096 22.4 / 15.3, 2 x 4096 x 4096 15.2 / 14.8).
 static bool rows_preferred(const GemmDesc &d) {
     const int64_t rows = (int64_t)d.N * d.batch;
-    if (d.M == 1) return rows >= 1024;
+    // M = 1: every row count, except many short rows, whose per-row reduction outweighs
+    // the stream (graph replay, us, rows kernel / small kernel: 1 x 1301 x 440 3.58 / 5.55,
+    // batch-8 1 x 1755 x 40 3.89 / 5.51, 1 x 173 x 17 2.72 / 3.06; batch-32 1 x 302 x 5262
+    // 56.1 / 45.2, 1 x 134 x 29895 9.33 / 6.45). A wavefront streams a whole row at ~8 GB/s,
+    // so rows longer than 10000 take this kernel only if there are >= 768 of them; fewer,
+    // longer rows go to the small kernel's k ranges (batch-8 1 x 137946 x 25 78.9 / 24.6,
+    // 1 x 32279 x 52 16.9 / 9.2; a dot product, 1 x 10^7 x 1, 91 there; 1 x 31706 x 877 27.2 /
+    // 34.1)
+    if (d.M == 1) return !(d.K < 320 && rows >= 16384) && (d.K <= 10000 || rows >= 768);
     if (d.M == 2) return rows >= 8192 && d.K >= 1024;
     return rows >= 8192 && d.K >= 2048;
 }
