@@ -364,6 +364,10 @@ static bool rows_preferred(const GemmDesc &d) {
 bool skinny_preferred(const GemmDesc &d) {
     if (!skinny_supported(d)) return false;
     if (d.transB) return rows_preferred(d);
+    // 3-4 rows of C over a batch: each entry's B must reach the bound itself (graph replay,
+    // us, this kernel / small kernel: batch-4 4 x 824 x 5425 36.2 / 18.9, batch-8 4 x 1028 x
+    // 2151 36.3 / 19.9; batch-2 4 x 7959 x 4144, 132 MB per entry, 57.2 / 87.3)
+    if (d.M >= 3) return (int64_t)d.K * d.N >= ((int64_t)16 << 20);
     return (int64_t)d.K * d.N * d.batch >= ((int64_t)16 << 20);
 }
 

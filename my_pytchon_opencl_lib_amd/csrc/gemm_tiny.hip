@@ -264,11 +264,13 @@ bool tiny_preferred(const GemmDesc &d) {
             ((uintptr_t)d.C & 127) == 0)
             return false;
         if (d.K <= 16) return true;
-        // Above these tile counts larger outputs go to the tiled kernel; outputs under 16 rows
-        // or columns stay here (graph replay, us, small kernel / this one: batch-32 11 x 33 x
-        // 18406 38.0 / 20.8, batch-32 2 x 35 x 7626 TN 18.9 / 12.0, 8 x 40 x 200000 16.0 /
-        // 11.0, batch-4 100000 x 50 x 7 26.4 / 19.8; 29 of 30 such shapes faster here).
-        return t <= (d.K <= 48 ? 8192 : 4096) || d.M < 16 || d.N < 16;
+        // Above these tile counts larger outputs go to the tiled kernel (graph replay, us, this
+        // kernel / 64x64 tiles: 1 x 4296 x 33 x 618 10.0 / 11.3, batch-8 615 x 17 x 711 10.5 /
+        // 11.7, 269 x 68 x 5623 8.8 / 10.3; batch-8 512 x 79 x 681 TN 17.2 / 12.1, 2195 x 26 x
+        // 6327 NT 30.2 / 25.8); outputs under 16 rows or columns stay here (small kernel /
+        // this one: batch-32 11 x 33 x 18406 38.0 / 20.8, batch-32 2 x 35 x 7626 TN 18.9 /
+        // 12.0, 8 x 40 x 200000 16.0 / 11.0; 29 of 30 such shapes faster here).
+        return t <= (d.K <= 48 ? 16384 : 8192) || d.M < 16 || d.N < 16;
     }
     // From 64 tiles when A is K-contiguous (coalesced loads; graph replay, us, small kernel
     // / this one: 256 x 256 x 256 NN 2.94 / 2.50, NT 2.83 / 2.63, 128 x 256 x 128 NN 2.81 /
