@@ -730,6 +730,12 @@ AUTO_REGIMES = [
     # per lane, >= 6 rounds of tiles): 128x128
     (dict(batch=1, M=8192, K=64, N=8180, ta=0, tb=0), "tiled-direct tile=64x64"),
     (dict(batch=1, M=12592, K=47, N=2304, ta=0, tb=0), "tiled-direct tile=128x128"),
+    # long K over few tiles: 64x64 tiles in k ranges (the LSTM gate gradient)
+    (dict(batch=1, M=6400, K=4096, N=512, ta=0, tb=1), "tiled-direct tile=64x64 splits=3"),
+    # one row of C, B stored [N, K], few rows: the rows GEMV; 3 rows over a batch whose
+    # entries hold small B: the small kernel
+    (dict(batch=1, M=1, K=1301, N=440, ta=0, tb=1), "skinny-rows"),
+    (dict(batch=8, M=3, K=6278, N=362, ta=0, tb=0), "small"),
 ]
 
 
