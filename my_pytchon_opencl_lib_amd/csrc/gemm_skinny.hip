@@ -87,11 +87,15 @@ __global__ void __launch_bounds__(SK_THREADS) gemm_skinny_kernel(SkinnyArgs p) {
     }
     __syncthreads();
 
+    // Column of accumulator e: four adjacent columns per lane with 16-byte loads; otherwise
+    // (N % 4 != 0) lane + 64 e, so each 4-byte load instruction reads 256 contiguous bytes
+    // of the row instead of touching 1 KB at a 16-byte stride.
+    auto col = [&](int e) { return VEC ? n + e : cb * SK_COLS + e * 64 + lane; };
     // Columns beyond N read a clamped, in-bounds column; their sums are never stored.
     const float *colp = Bb + (VEC ? (n < p.N ? n : p.N - 4) : 0);
     int nc[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) nc[e] = min(n + e, p.N - 1);
+    for (int e = 0; e < 4; ++e) nc[e] = min(col(e), p.N - 1);
 
     f4 acc[MR];
 #pragma unroll
@@ -108,6 +112,9 @@ __global__ void __launch_bounds__(SK_THREADS) gemm_skinny_kernel(SkinnyArgs p) {
             v = __builtin_nontemporal_load(reinterpret_cast<const f4u *>(rowp));
         else if constexpr (VEC)
             __builtin_memcpy(&v, rowp, sizeof(f4));
+        else if constexpr (NTL)
+            v = f4{__builtin_nontemporal_load(rowp + nc[0]), __builtin_nontemporal_load(rowp + nc[1]),
+                   __builtin_nontemporal_load(rowp + nc[2]), __builtin_nontemporal_load(rowp + nc[3])};
         else
             v = f4{rowp[nc[0]], rowp[nc[1]], rowp[nc[2]], rowp[nc[3]]};
         return v;
@@ -162,10 +169,11 @@ __global__ void __launch_bounds__(SK_THREADS) gemm_skinny_kernel(SkinnyArgs p) {
                 float *crow = p.C + (int64_t)b * p.sC + (int64_t)m * p.ldc;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    if (n + e < p.N) {
+                    const int c = col(e);
+                    if (c < p.N) {
                         float v = tot[m][e];
-                        if (p.bias != nullptr) v = v + p.bias[n + e];
-                        crow[n + e] = p.accumulate ? crow[n + e] + v : v;
+                        if (p.bias != nullptr) v = v + p.bias[c];
+                        crow[c] = p.accumulate ? crow[c] + v : v;
                     }
                 }
             }
@@ -175,7 +183,7 @@ __global__ void __launch_bounds__(SK_THREADS) gemm_skinny_kernel(SkinnyArgs p) {
             for (int m = 0; m < MR; ++m)
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    if (n + e < p.N) part[(int64_t)m * p.N + n + e] = tot[m][e];
+                    if (col(e) < p.N) part[(int64_t)m * p.N + col(e)] = tot[m][e];
         }
     }
 }
@@ -321,7 +329,7 @@ int launch_mr(hipStream_t st, const SkinnyArgs &a, bool vec, int batch) {
     if (vec)
         hipLaunchKernelGGL((gemm_skinny_kernel<MR, true, true>), grid, dim3(SK_THREADS), 0, st, a);
     else
-        hipLaunchKernelGGL((gemm_skinny_kernel<MR, false, false>), grid, dim3(SK_THREADS), 0, st, a);
+        hipLaunchKernelGGL((gemm_skinny_kernel<MR, false, true>), grid, dim3(SK_THREADS), 0, st, a);
     return hip_check(hipGetLastError(), "gemm_skinny_kernel launch");
 }
 
@@ -366,8 +374,14 @@ bool skinny_preferred(const GemmDesc &d) {
     if (d.transB) return rows_preferred(d);
     // 3-4 rows of C over a batch: each entry's B must reach the bound itself (graph replay,
     // us, this kernel / small kernel: batch-4 4 x 824 x 5425 36.2 / 18.9, batch-8 4 x 1028 x
-    // 2151 36.3 / 19.9; batch-2 4 x 7959 x 4144, 132 MB per entry, 57.2 / 87.3)
-    if (d.M >= 3) return (int64_t)d.K * d.N >= ((int64_t)16 << 20);
+    // 2151 36.3 / 19.9; batch-2 4 x 7959 x 4144, 132 MB per entry, 57.2 / 87.3). With
+    // N % 4 != 0, 96 MB of B over the whole batch is enough (rotating copies of B: batch-16
+    // 3 x 9907 x 526 76.4 / 120.1, batch-8 4 x 11128 x 1349 106.6 / 148.2, batch-4 4 x 11887
+    // x 529 34.8 / 44.7; 48 of 48 such shapes of two seeds 0.57-0.99x; below it batch-8 3 x
+    // 3350 x 866, 93 MB, 26.5 / 22.6, batch-4 3 x 995 x 4479 23.6 / 17.9).
+    if (d.M >= 3)
+        return (int64_t)d.K * d.N >= ((int64_t)16 << 20) ||
+               (d.N % 4 != 0 && (int64_t)d.K * d.N * d.batch >= ((int64_t)23 << 20));
     return (int64_t)d.K * d.N * d.batch >= ((int64_t)16 << 20);
 }
 

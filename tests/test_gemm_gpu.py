@@ -736,6 +736,10 @@ AUTO_REGIMES = [
     # entries hold small B: the small kernel
     (dict(batch=1, M=1, K=1301, N=440, ta=0, tb=1), "skinny-rows"),
     (dict(batch=8, M=3, K=6278, N=362, ta=0, tb=0), "small"),
+    # 3-4 rows over a batch with N % 4 != 0: from 96 MB of B over the batch, the skinny
+    # kernel (below it, the small kernel)
+    (dict(batch=4, M=4, K=11887, N=529, ta=0, tb=0), "skinny tile=0x256"),
+    (dict(batch=8, M=3, K=3350, N=866, ta=0, tb=0), "small"),
 ]
 
 
