@@ -409,7 +409,10 @@ int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {
     if (d.transB) {  // rows of the stored B streamed whole: one launch, no partial sums
         a.kc = d.K;
         a.slices = 1;
-        const bool avec = !d.transA;
+        // A's row is contiguous also when A is stored transposed with one row and lda = 1
+        // (a [K, 1] column); the 4-byte loads would otherwise touch 1 KB per instruction at
+        // a 16-byte stride for every 1 KB of B.
+        const bool avec = !d.transA || (d.M == 1 && d.lda == 1);
         int rc;
         switch (d.M) {
             case 1: rc = launch_rows<1>(stream, a, avec, d.batch); break;
