@@ -760,6 +760,8 @@ AUTO_REGIMES = [
     # kernel (below it, the small kernel)
     (dict(batch=4, M=4, K=11887, N=529, ta=0, tb=0), "skinny tile=0x256"),
     (dict(batch=8, M=3, K=3350, N=866, ta=0, tb=0), "small"),
+    # a narrow output over long K with 16 MB or more of operands: 1.5x the k ranges
+    (dict(batch=1, M=1846, K=4713, N=17, ta=0, tb=0), "small tile=32x32 splits=8"),
 ]
 
 
