@@ -205,7 +205,10 @@ struct RowsPlan {
 };
 constexpr int RW_WAVES = 4;  // wavefronts per work-group
 
-template <int MR, bool AVEC>
+// AM: how A is read. 0 = A's rows are contiguous; 1 = strided, one element at a time;
+// 2 = A stored transposed and dense ([K, MR], lda = MR): the MR values of 4 consecutive k
+// are 4 MR contiguous floats, fetched as MR 16-byte loads.
+template <int MR, int AM>
 __global__ void __launch_bounds__(RW_WAVES * 64) gemv_rows_kernel(SkinnyArgs p) {
     constexpr int RW = RowsPlan<MR>::RW;
     constexpr int U = RowsPlan<MR>::U;
@@ -229,12 +232,28 @@ __global__ void __launch_bounds__(RW_WAVES * 64) gemv_rows_kernel(SkinnyArgs p) 
     auto load_a = [&](int m, int k) {
         const float *q = Ab + (int64_t)m * p.a_rs;
         f4 v;
-        if constexpr (AVEC)
+        if constexpr (AM == 0)
             v = *reinterpret_cast<const f4u *>(q + k);
         else
             v = f4{q[(int64_t)k * p.a_ks], q[(int64_t)(k + 1) * p.a_ks],
                    q[(int64_t)(k + 2) * p.a_ks], q[(int64_t)(k + 3) * p.a_ks]};
         return v;
+    };
+    // A's values at k .. k+3 for every row m (k + 4 <= K)
+    auto load_a_all = [&](f4 (&av)[MR], int k) {
+        if constexpr (AM == 2) {
+            f4 t[MR];
+#pragma unroll
+            for (int j = 0; j < MR; ++j)
+                t[j] = *reinterpret_cast<const f4u *>(Ab + (int64_t)k * MR + 4 * j);
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) av[m][e] = t[(e * MR + m) / 4][(e * MR + m) % 4];
+        } else {
+#pragma unroll
+            for (int m = 0; m < MR; ++m) av[m] = load_a(m, k);
+        }
     };
     auto fma4 = [&](f4 &c, const f4 &x, const f4 &y) {
 #pragma unroll
@@ -252,9 +271,7 @@ __global__ void __launch_bounds__(RW_WAVES * 64) gemv_rows_kernel(SkinnyArgs p) 
                 bv[u][r] = __builtin_nontemporal_load(
                     reinterpret_cast<const f4u *>(brow[r] + kb + 256 * u + 4 * lane));
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int m = 0; m < MR; ++m) av[u][m] = load_a(m, kb + 256 * u + 4 * lane);
+        for (int u = 0; u < U; ++u) load_a_all(av[u], kb + 256 * u + 4 * lane);
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -267,8 +284,7 @@ __global__ void __launch_bounds__(RW_WAVES * 64) gemv_rows_kernel(SkinnyArgs p) 
         const int k = kb + 4 * lane;
         if (k + 4 <= p.K) {
             f4 av[MR];
-#pragma unroll
-            for (int m = 0; m < MR; ++m) av[m] = load_a(m, k);
+            load_a_all(av, k);
 #pragma unroll
             for (int r = 0; r < RW; ++r) {
                 const f4 bv = *reinterpret_cast<const f4u *>(brow[r] + k);
@@ -311,13 +327,15 @@ __global__ void __launch_bounds__(RW_WAVES * 64) gemv_rows_kernel(SkinnyArgs p) 
 }
 
 template <int MR>
-int launch_rows(hipStream_t st, const SkinnyArgs &a, bool avec, int batch) {
+int launch_rows(hipStream_t st, const SkinnyArgs &a, int am, int batch) {
     constexpr int per_wg = RW_WAVES * RowsPlan<MR>::RW;
     dim3 grid((a.N + per_wg - 1) / per_wg, batch);
-    if (avec)
-        hipLaunchKernelGGL((gemv_rows_kernel<MR, true>), grid, dim3(RW_WAVES * 64), 0, st, a);
+    if (am == 0)
+        hipLaunchKernelGGL((gemv_rows_kernel<MR, 0>), grid, dim3(RW_WAVES * 64), 0, st, a);
+    else if (am == 2)
+        hipLaunchKernelGGL((gemv_rows_kernel<MR, 2>), grid, dim3(RW_WAVES * 64), 0, st, a);
     else
-        hipLaunchKernelGGL((gemv_rows_kernel<MR, false>), grid, dim3(RW_WAVES * 64), 0, st, a);
+        hipLaunchKernelGGL((gemv_rows_kernel<MR, 1>), grid, dim3(RW_WAVES * 64), 0, st, a);
     return hip_check(hipGetLastError(), "gemv_rows_kernel launch");
 }
 
@@ -412,13 +430,13 @@ int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d) {
         // A's row is contiguous also when A is stored transposed with one row and lda = 1
         // (a [K, 1] column); the 4-byte loads would otherwise touch 1 KB per instruction at
         // a 16-byte stride for every 1 KB of B.
-        const bool avec = !d.transA || (d.M == 1 && d.lda == 1);
+        const int am = !d.transA || (d.M == 1 && d.lda == 1) ? 0 : d.lda == d.M ? 2 : 1;
         int rc;
         switch (d.M) {
-            case 1: rc = launch_rows<1>(stream, a, avec, d.batch); break;
-            case 2: rc = launch_rows<2>(stream, a, avec, d.batch); break;
-            case 3: rc = launch_rows<3>(stream, a, avec, d.batch); break;
-            default: rc = launch_rows<4>(stream, a, avec, d.batch); break;
+            case 1: rc = launch_rows<1>(stream, a, am, d.batch); break;
+            case 2: rc = launch_rows<2>(stream, a, am, d.batch); break;
+            case 3: rc = launch_rows<3>(stream, a, am, d.batch); break;
+            default: rc = launch_rows<4>(stream, a, am, d.batch); break;
         }
         record_plan("skinny-rows", d, 0, 0, 1, 16);
         return rc;

@@ -289,24 +289,25 @@ def test_skinny_rows_and_bias(nncl, policy, M):
     assert np.array_equal(C, C2)
 
 
-@pytest.mark.parametrize("K,N,batch", [(1001, 777, 1), (4096, 2048, 1), (206, 228, 8)])
-def test_rows_gemv_transposed_column(nncl, K, N, batch):
-    """One row of C with A stored transposed as a [K, 1] column (lda = 1) and B stored
-    [N, K]: the rows GEMV reads that column as a contiguous row. Small-integer operands make
-    the result exact in any summation order."""
+@pytest.mark.parametrize("M,K,N,batch", [(1, 1001, 777, 1), (1, 4096, 2048, 1), (1, 206, 228, 8),
+                                         (2, 1001, 777, 1), (3, 2050, 300, 2), (4, 1027, 513, 1)])
+def test_rows_gemv_transposed_a(nncl, M, K, N, batch):
+    """B stored [N, K] and A stored transposed and dense ([K, M], lda = M): one row is read
+    as a contiguous row, 2-4 rows as 4 M contiguous floats per 4 values of k. Small-integer
+    operands make the result exact in any summation order."""
     from my_pytchon_opencl_lib_amd import _native
-    say("rows gemv, A a column", K, N, batch)
-    A = small_ints((batch, K, 1), K + N)
+    say("rows gemv, A transposed", M, K, N, batch)
+    A = small_ints((batch, K, M), K + N + M)
     B = small_ints((batch, N, K), K * 3 + N)
     bias = small_ints((N,), N)
-    prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_AUTO)
+    prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_SKINNY)
     try:
         C = gemm_gpu(nncl, A, B, transA=True, transB=True, bias=bias)
         assert _native.last_plan().startswith("skinny-rows"), _native.last_plan()
     finally:
         _native.set_gemm_policy(prev)
     expect = np.einsum("bkm,bnk->bmn", A.astype(np.int64), B.astype(np.int64)) + bias
-    assert np.array_equal(C.reshape(batch, 1, N), expect.astype(np.float32))
+    assert np.array_equal(C.reshape(batch, M, N), expect.astype(np.float32))
 
 
 def test_graph_capture_replays_match_eager(nncl):
