@@ -60,6 +60,10 @@ CONFIGS = {
     "2b_bmm_pv": (2 * 32 * 128 * 128 * 64, 4 * 32 * (128 * 128 + 128 * 64 * 2), "hbm"),
     "3_lstm_gate_step": (2 * 64 * 1536 * 4096,
                          4 * (64 * 1536 + 1536 * 4096 + 64 * 4096 + 4096), "mfma"),
+    # config 3 in the reference's stateful form (lstm_hid_forward, lstm.cl:832-844): x_t, h_{t-1},
+    # W, U as four buffers, the same FLOP and bytes as the concatenated product
+    "3h_lstm_hid_step": (2 * 64 * 1536 * 4096,
+                         4 * (64 * 512 + 64 * 1024 + 1536 * 4096 + 64 * 4096 + 4096), "mfma"),
     "5a_ragged": (2 * 1000 * 3000 * 777, 4 * (1000 * 777 + 777 * 3000 + 1000 * 3000), "mfma"),
     "5b_gemv": (2 * 4096 * 11008, 4 * (4096 + 4096 * 11008 + 11008), "hbm"),
     # tensor_permute (cl_kernels/permute.cl:11-50): not a BASELINE config, but the path's
@@ -85,10 +89,12 @@ def parse():
     p.add_argument("--no-reference", action="store_true",
                    help="skip the reference bmm_tiled run on this GPU")
     p.add_argument("--pmc-target", nargs="?", const="4096",
-                   choices=["4096", "1", "2a", "2b", "3", "5a", "5b", "a5t", "a5h", "floor"],
+                   choices=["4096", "1", "2a", "2b", "3", "3h", "5a", "5b", "a5t", "a5h",
+                            "floor"],
                    help="run only one workload for rocprofv3 --pmc passes, each 3 times: '4096' "
                         "the three 4096^3 forms, '1' / '2a' / '2b' / '3' / '5a' / '5b' that "
-                        "BASELINE config, 'a5t' / 'a5h' the 4096^2 [1,0] and the [0,2,1,3] "
+                        "BASELINE config, '3h' config 3 in the stateful x_t W + h_{t-1} U "
+                        "form, 'a5t' / 'a5h' the 4096^2 [1,0] and the [0,2,1,3] "
                         "head-split permutes, 'floor' the one-element fill kernel; then a 256 MiB "
                         "device copy 3 times (the reference for scaling FETCH_SIZE / "
                         "WRITE_SIZE to bytes)")
@@ -335,6 +341,12 @@ def pmc_target(torch, nncl, which="4096"):
         bias = r(4096) / 32
         Y = torch.empty(64, 4096, device=dev)
         calls = [lambda i=i: nncl.gemm(X[i], W, bias=bias, out=Y) for i in range(3)]
+    elif which == "3h":
+        Xs = torch.randn(64, 3, 512, device=dev, generator=g)
+        Wx, Uh, bias = r(512, 4096) / 32, r(1024, 4096) / 32, r(4096) / 32
+        Hp, Ho = r(64, 1024), r(64, 3, 1024)
+        ws = torch.empty(3, 64, 4096, device=dev)
+        calls = [lambda t=t: nncl.LstmHidGates(Xs, Wx, Uh, bias, Hp, Ho, ws, t) for t in range(3)]
     elif which == "5a":
         A, B, C = r(1000, 777), r(777, 3000), torch.empty(1000, 3000, device=dev)
         calls = [lambda: nncl.gemm(A, B, out=C)] * 3
@@ -540,6 +552,15 @@ def measure_all_configs(torch, nncl, _native, calls=100):
     f3 = [lambda i=i: nncl.gemm(X[i], W, bias=bias, out=Y) for i in range(100)]
     rec("3_lstm_gate_step", timed(f3, per=1), f3,
         vendor=[lambda i=i: torch.addmm(bias, X[i], W, out=Y) for i in range(100)])
+    del X
+    # the stateful form: 100 steps of one sequence chunk, step 0 from the incoming state
+    Xs = torch.randn(64, 100, 512, device=dev, generator=g)
+    Wx, Uh = r(512, 4096) / 32, r(1024, 4096) / 32
+    Hp, Ho = r(64, 1024), r(64, 100, 1024)
+    ws = torch.empty(100, 64, 4096, device=dev)
+    f3h = [lambda t=t: nncl.LstmHidGates(Xs, Wx, Uh, bias, Hp, Ho, ws, t) for t in range(100)]
+    rec("3h_lstm_hid_step", timed(f3h, per=1), f3h)
+    del Xs, Ho, ws
     A5, B5, C5 = r(1000, 777), r(777, 3000), torch.empty(1000, 3000, device=dev)
     f5a = [lambda: nncl.gemm(A5, B5, out=C5)]
     rec("5a_ragged", timed(f5a), f5a, vendor=[lambda: torch.mm(A5, B5, out=C5)])

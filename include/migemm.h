@@ -185,6 +185,26 @@ int migemm_lstm_gemm_grad_weights(void *stream, const float *X, const float *H_o
 int migemm_lstm_recurrent_gates(void *stream, float *XW, const float *H_out, const float *U,
                                 int batch_size, int seq_len, int hidden_size, int t);
 
+/* The gate product of one timestep of kernel lstm_hid_forward, cs/cl_kernels/lstm.cl:788-870
+ * (gate loop :832-844), enqueued by NnClGlob.LstmWithWithState
+ * (cs/compiler/NnClGlob.cs:1067-1100) for layers/LSTMStateful.cs: with x, h, W and U as four
+ * separate buffers, in one launch where the panel kernel applies (no x||h concatenation):
+ *   workspace[t, b, g] = bias[g] + sum_i X[b, t, i] * W[i, g] + sum_h hp[b, h] * U[h, g]
+ * for b < batch_size, g < 4*hidden_size, with hp = H_prev [batch_size, hidden_size] at t == 0
+ * (the chunk's incoming state, lstm.cl:821) and hp[b] = H_out[b, t-1, :] after (the previous
+ * step's output, lstm.cl:861). X [batch_size, seq_len, in_features], W [in_features, 4H],
+ * U [hidden_size, 4H], bias [4H], H_out [batch_size, seq_len, hidden_size], workspace
+ * [seq_len, batch_size, 4H] (the reference's gate buffer); only workspace[t] is written.
+ * H_prev is read only at t == 0 and H_out only at t > 0: the other may be NULL. The
+ * reference adds the bias first and the products in one fp32 chain (lstm.cl:833-843); this
+ * sums the products by MFMA and adds the bias after them, within the tolerance above. The
+ * activations and the cell update that follow in the reference kernel are not part of
+ * this library (a caller applies them between steps). */
+int migemm_lstm_hid_gates(void *stream, const float *X, const float *W, const float *U,
+                          const float *bias, const float *H_prev, const float *H_out,
+                          float *workspace, int batch_size, int seq_len, int in_features,
+                          int hidden_size, int t);
+
 /* Replaces kernel tensor_permute, cl_kernels/permute.cl:11-18, enqueued by
  * NnClGlob.Permute (cs/compiler/NnClGlob.cs:382-424) and nncl_glob.py:148-174.
  * dst = src.permute(axes); src_dims and axes are HOST int arrays of length num_dims

@@ -95,6 +95,7 @@ SIGNATURES = {
     "migemm_lstm_gemm_grad_x": ([_vp, _vp, _vp, _vp, _i32, _i32, _i32], _i32),
     "migemm_lstm_gemm_grad_weights": ([_vp] * 7 + [_i32] * 4, _i32),
     "migemm_lstm_recurrent_gates": ([_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32], _i32),
+    "migemm_lstm_hid_gates": ([_vp] * 8 + [_i32] * 5, _i32),
     "migemm_tensor_permute": ([_vp, _vp, _vp, _ip, _ip, _i32], _i32),
     "migemm_linear_bias_backward": ([_vp, _vp, _vp, _i32, _i32], _i32),
     "migemm_reduce_sum_axis": ([_vp, _vp, _vp, _i32, _i32, _i32], _i32),

@@ -314,6 +314,33 @@ static int run_gemm(hipStream_t stream, const GemmDesc &desc) {
     return launch_gemm_tiled(stream, d);
 }
 
+// C = opA(A) opB(B) + opA(A2) opB(B2) (+ bias) for a descriptor with a second operand pair:
+// one panel launch over the k-groups of both pairs where the panel kernel applies and is
+// the AUTO choice for the concatenated product (or is forced), otherwise the first product
+// with the bias and then the second accumulated onto it, each dispatched as a GEMM of its
+// own.
+static int run_gemm_pair(hipStream_t stream, const GemmDesc &d) {
+    const int policy = g_policy.load(std::memory_order_relaxed);
+    if (panel_supported(d) && (policy == MIGEMM_POLICY_PANEL ||
+                               (policy == MIGEMM_POLICY_AUTO && panel_preferred(d))))
+        return launch_gemm_panel(stream, d);
+    GemmDesc first = d;
+    first.A2 = nullptr;
+    first.B2 = nullptr;
+    first.K2 = 0;
+    int rc = run_gemm(stream, first);
+    if (rc != MIGEMM_OK) return rc;
+    GemmDesc second = first;
+    second.A = d.A2;
+    second.B = d.B2;
+    second.lda = d.lda2;
+    second.ldb = d.ldb2;
+    second.K = d.K2;
+    second.bias = nullptr;
+    second.accumulate = true;
+    return run_gemm(stream, second);
+}
+
 }  // namespace migemm
 
 using namespace migemm;
@@ -513,6 +540,66 @@ int migemm_lstm_recurrent_gates(void *stream, float *XW, const float *H_out, con
         stream, 0, 0, batch_size, (int)gates, hidden_size, H_out + (int64_t)(t - 1) * hidden_size,
         (int64_t)seq_len * hidden_size, 0, U, gates, 0, nullptr, XW + (int64_t)t * gates,
         (int64_t)seq_len * gates, 0, 1, MIGEMM_GEMM_ACCUMULATE);
+}
+
+int migemm_lstm_hid_gates(void *stream, const float *X, const float *W, const float *U,
+                          const float *bias, const float *H_prev, const float *H_out,
+                          float *workspace, int batch_size, int seq_len, int in_features,
+                          int hidden_size, int t) {
+    clear_error();
+    if (X == nullptr || W == nullptr || U == nullptr || bias == nullptr || workspace == nullptr)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "lstm_hid_gates: null pointer argument");
+    if (batch_size < 1 || seq_len < 1 || in_features < 1 || hidden_size < 1)
+        return set_error(MIGEMM_ERR_INVALID_ARG,
+                         "lstm_hid_gates: sizes must be >= 1 (batch=%d seq=%d in=%d hidden=%d)",
+                         batch_size, seq_len, in_features, hidden_size);
+    if (t < 0 || t >= seq_len)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "lstm_hid_gates: step %d not in [0, %d)", t,
+                         seq_len);
+    // h_{t-1}: the chunk's incoming state at t = 0 (H_prev, lstm.cl:821), else the previous
+    // step's output row of the same sequence (H_out, written at lstm.cl:861)
+    const float *hsrc = t == 0 ? H_prev : H_out;
+    if (hsrc == nullptr)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "lstm_hid_gates: %s is null at step %d",
+                         t == 0 ? "H_prev" : "H_out", t);
+    const int64_t gates = (int64_t)4 * hidden_size;
+    if (gates > INT32_MAX)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "lstm_hid_gates: 4*hidden exceeds 2^31-1");
+    const int G = (int)gates;
+    int64_t n_x, n_w, n_u, n_h, n_ws, bs;
+    if (!mul_add_ok(batch_size, seq_len, 0, &bs) || !mul_add_ok(bs, in_features, 0, &n_x) ||
+        !mul_add_ok(in_features, gates, 0, &n_w) || !mul_add_ok(hidden_size, gates, 0, &n_u) ||
+        !mul_add_ok(t == 0 ? batch_size : bs, hidden_size, 0, &n_h) ||
+        !mul_add_ok(bs, gates, 0, &n_ws))
+        return set_error(MIGEMM_ERR_INVALID_ARG, "lstm_hid_gates: size overflows");
+    // the step's gates, workspace[t, 0..batch, 0..4H): one contiguous range
+    float *out = workspace + (int64_t)t * batch_size * gates;
+    const int64_t n_out = (int64_t)batch_size * gates;
+    if (ranges_overlap(out, n_out, X, n_x) || ranges_overlap(out, n_out, W, n_w) ||
+        ranges_overlap(out, n_out, U, n_u) || ranges_overlap(out, n_out, bias, gates) ||
+        ranges_overlap(out, n_out, hsrc, n_h))
+        return set_error(MIGEMM_ERR_ALIAS, "lstm_hid_gates: the step's gates overlap an input");
+    GemmDesc d;
+    d.A = X + (int64_t)t * in_features;  // x_t of sequence b: row b, seq_len*F apart
+    d.lda = (int64_t)seq_len * in_features;
+    d.B = W;
+    d.ldb = gates;
+    d.bias = bias;
+    d.C = out;
+    d.ldc = gates;
+    d.sA = d.sB = d.sC = 0;
+    d.M = batch_size;
+    d.N = G;
+    d.K = in_features;
+    d.batch = 1;
+    d.transA = d.transB = false;
+    d.accumulate = false;
+    d.A2 = t == 0 ? H_prev : H_out + (int64_t)(t - 1) * hidden_size;
+    d.lda2 = t == 0 ? (int64_t)hidden_size : (int64_t)seq_len * hidden_size;
+    d.B2 = U;
+    d.ldb2 = gates;
+    d.K2 = hidden_size;
+    return run_gemm_pair(static_cast<hipStream_t>(stream), d);
 }
 
 int migemm_linear_weight_grad(void *stream, const float *X, const float *dY, float *dW, int M,

@@ -62,6 +62,13 @@ struct PanelArgs {
     int accumulate;
     FastDiv per_batch;  // tiles_m * tiles_n (multiply-high division in the prologue)
     FastDiv tm_div;     // tiles_m
+    // Second operand pair (kernels with TWO, batch 1): C = op(A) op(B) + op(A2) op(B2)
+    // (+ bias), A2 / B2 in the orientations of A / B with K2 = K - 32 G1 k; k-groups G1..
+    // of the sum are theirs. The stateful LSTM gates x_t W + h_{t-1} U.
+    const float *A2;
+    const float *B2;
+    int64_t lda2, ldb2;
+    int G1;  // k-groups of the first pair
 };
 
 constexpr int PT = 32;         // output tile edge
@@ -74,7 +81,7 @@ constexpr int PRS = 36;        // floats between the rows of a partial tile in t
 // distinct bank groups.
 __device__ __forceinline__ int pa_swz(int r) { return (r >> 1) & 7; }
 
-template <int NW, int D, bool AKC, bool BKC>
+template <int NW, int D, bool AKC, bool BKC, bool TWO>
 __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
     static_assert(D * PSTAGE >= PT * PRS, "a partial tile fits in its wavefront's ring");
     static_assert(8 * (D - 1) < 64, "vmcnt range");
@@ -149,15 +156,28 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
         uint32_t aoffs[4], boffs[4];
         offsets(std::integral_constant<bool, AKC>{}, m0, p.M, p.lda, aoffs);
         offsets(std::integral_constant<bool, BKC>{}, n0, p.N, p.ldb, boffs);
+        // (TWO: the bases are the pairs' k-group 0 and issue() adds the absolute k-group)
+        const int gb = TWO ? 0 : g0;
         const char *abase = reinterpret_cast<const char *>(
             p.A + (int64_t)bb * p.sA +
-            (AKC ? (int64_t)m0 * p.lda + (int64_t)g0 * PKG : (int64_t)g0 * PKG * p.lda + m0));
+            (AKC ? (int64_t)m0 * p.lda + (int64_t)gb * PKG : (int64_t)gb * PKG * p.lda + m0));
         const char *bbase = reinterpret_cast<const char *>(
             p.B + (int64_t)bb * p.sB +
-            (BKC ? (int64_t)n0 * p.ldb + (int64_t)g0 * PKG : (int64_t)g0 * PKG * p.ldb + n0));
+            (BKC ? (int64_t)n0 * p.ldb + (int64_t)gb * PKG : (int64_t)gb * PKG * p.ldb + n0));
         // bytes per k-group
         const int64_t astep = AKC ? (int64_t)PKG * 4 : (int64_t)PKG * p.lda * 4;
         const int64_t bstep = BKC ? (int64_t)PKG * 4 : (int64_t)PKG * p.ldb * 4;
+        uint32_t aoffs2[4] = {0, 0, 0, 0}, boffs2[4] = {0, 0, 0, 0};
+        const char *abase2 = nullptr, *bbase2 = nullptr;
+        int64_t astep2 = 0, bstep2 = 0;
+        if constexpr (TWO) {
+            offsets(std::integral_constant<bool, AKC>{}, m0, p.M, p.lda2, aoffs2);
+            offsets(std::integral_constant<bool, BKC>{}, n0, p.N, p.ldb2, boffs2);
+            abase2 = reinterpret_cast<const char *>(p.A2 + (AKC ? (int64_t)m0 * p.lda2 : m0));
+            bbase2 = reinterpret_cast<const char *>(p.B2 + (BKC ? (int64_t)n0 * p.ldb2 : n0));
+            astep2 = AKC ? (int64_t)PKG * 4 : (int64_t)PKG * p.lda2 * 4;
+            bstep2 = BKC ? (int64_t)PKG * 4 : (int64_t)PKG * p.ldb2 * 4;
+        }
 
         // The first MFMA sub-group of a k-group needs k 0..7 of both operands: all four
         // instructions of a K-contiguous operand, the first of a k-row one. K-contiguous
@@ -166,21 +186,42 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
         constexpr int PEEL = 4 * ((int)AKC + (int)BKC) + ((int)!AKC + (int)!BKC);
         auto issue = [&](int j, int slot) {
             const int g = j < ng ? j : ng - 1;
-            const char *ag = abase + (int64_t)g * astep;
-            const char *bg = bbase + (int64_t)g * bstep;
+            const char *ag, *bg;
+            uint32_t ao[4], bo[4];
+            if constexpr (TWO) {
+                // wave-uniform choice of the pair that holds absolute k-group g0 + g
+                const int ga = g0 + g;
+                const bool second = ga >= p.G1;
+                const int gl = second ? ga - p.G1 : ga;
+                ag = second ? abase2 + (int64_t)gl * astep2 : abase + (int64_t)gl * astep;
+                bg = second ? bbase2 + (int64_t)gl * bstep2 : bbase + (int64_t)gl * bstep;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    ao[q] = second ? aoffs2[q] : aoffs[q];
+                    bo[q] = second ? boffs2[q] : boffs[q];
+                }
+            } else {
+                ag = abase + (int64_t)g * astep;
+                bg = bbase + (int64_t)g * bstep;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    ao[q] = aoffs[q];
+                    bo[q] = boffs[q];
+                }
+            }
             float *st = my + slot * PSTAGE;
             if constexpr (AKC) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) dma16(ag, aoffs[q], st + 1024 + 256 * q);
+                for (int q = 0; q < 4; ++q) dma16(ag, ao[q], st + 1024 + 256 * q);
             }
             if constexpr (BKC) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) dma16(bg, boffs[q], st + 256 * q);
+                for (int q = 0; q < 4; ++q) dma16(bg, bo[q], st + 256 * q);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                if constexpr (!AKC) dma16(ag, aoffs[q], st + 1024 + 256 * q);
-                if constexpr (!BKC) dma16(bg, boffs[q], st + 256 * q);
+                if constexpr (!AKC) dma16(ag, ao[q], st + 1024 + 256 * q);
+                if constexpr (!BKC) dma16(bg, bo[q], st + 256 * q);
             }
         };
         // Fragments of sub-group j (k = 8j .. 8j+7 of the k-group), step s: B lane l holds
@@ -318,16 +359,25 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
 }
 
 // One k-group ring slot per wavefront (D = 1), NW wavefronts along K; operand layouts AKC
-// (A K-contiguous, i.e. not transposed) and BKC (B K-contiguous, i.e. transposed).
-template <bool AKC, bool BKC>
+// (A K-contiguous, i.e. not transposed) and BKC (B K-contiguous, i.e. transposed); TWO: a
+// second operand pair.
+template <bool AKC, bool BKC, bool TWO>
 int launch_nw(hipStream_t stream, const PanelArgs &a, int nw) {
     switch (nw) {
-        case 8: hipLaunchKernelGGL((gemm_panel_kernel<8, 1, AKC, BKC>), dim3(a.total), dim3(8 * 64), 0, stream, a); break;
-        case 4: hipLaunchKernelGGL((gemm_panel_kernel<4, 1, AKC, BKC>), dim3(a.total), dim3(4 * 64), 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((gemm_panel_kernel<2, 1, AKC, BKC>), dim3(a.total), dim3(2 * 64), 0, stream, a); break;
-        default: hipLaunchKernelGGL((gemm_panel_kernel<1, 1, AKC, BKC>), dim3(a.total), dim3(64), 0, stream, a); break;
+        case 8: hipLaunchKernelGGL((gemm_panel_kernel<8, 1, AKC, BKC, TWO>), dim3(a.total), dim3(8 * 64), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL((gemm_panel_kernel<4, 1, AKC, BKC, TWO>), dim3(a.total), dim3(4 * 64), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((gemm_panel_kernel<2, 1, AKC, BKC, TWO>), dim3(a.total), dim3(2 * 64), 0, stream, a); break;
+        default: hipLaunchKernelGGL((gemm_panel_kernel<1, 1, AKC, BKC, TWO>), dim3(a.total), dim3(64), 0, stream, a); break;
     }
     return hip_check(hipGetLastError(), "gemm_panel_kernel launch");
+}
+
+template <bool TWO>
+int launch_layout(hipStream_t stream, const PanelArgs &a, const GemmDesc &d, int nw) {
+    if (!d.transA && !d.transB) return launch_nw<true, false, TWO>(stream, a, nw);
+    if (!d.transA) return launch_nw<true, true, TWO>(stream, a, nw);
+    if (!d.transB) return launch_nw<false, false, TWO>(stream, a, nw);
+    return launch_nw<false, true, TWO>(stream, a, nw);
 }
 
 bool aligned16(const float *p, int64_t ld, int64_t stride) {
@@ -341,10 +391,15 @@ bool panel_supported(const GemmDesc &d) {
     // operand's rows (B not transposed: N % 4 == 0; A transposed: M % 4 == 0); every
     // operand row 16-byte aligned; each lane's load offset within a k-group fits 32 bits:
     // below 32 ld * 4 bytes for a K-contiguous operand, (31 ld + extent) * 4 <= 128 ld bytes
-    // for a k-row one.
-    return d.K % PKG == 0 && d.N % 4 == 0 && d.N >= 4 && (!d.transA || d.M % 4 == 0) &&
-           aligned16(d.A, d.lda, d.sA) && aligned16(d.B, d.ldb, d.sB) &&
-           d.lda <= ((int64_t)1 << 25) && d.ldb <= ((int64_t)1 << 25);
+    // for a k-row one. A second operand pair (batch 1) meets the same conditions.
+    const bool pair1 = d.K % PKG == 0 && d.N % 4 == 0 && d.N >= 4 &&
+                       (!d.transA || d.M % 4 == 0) && aligned16(d.A, d.lda, d.sA) &&
+                       aligned16(d.B, d.ldb, d.sB) && d.lda <= ((int64_t)1 << 25) &&
+                       d.ldb <= ((int64_t)1 << 25);
+    if (d.A2 == nullptr) return pair1;
+    return pair1 && d.batch == 1 && d.K2 % PKG == 0 && aligned16(d.A2, d.lda2, 0) &&
+           aligned16(d.B2, d.ldb2, 0) && d.lda2 <= ((int64_t)1 << 25) &&
+           d.ldb2 <= ((int64_t)1 << 25);
 }
 
 // Where the panel kernel beats the other families (graph replay, NN, M in 16..256, N in
@@ -364,6 +419,13 @@ bool panel_preferred(const GemmDesc &d) {
     // x 8 TN 16.7 us here, 14.6 on the small kernel)
     if (d.M <= 16 || d.N <= 16 || !panel_supported(d)) return false;
     const int64_t tiles = (int64_t)((d.M + PT - 1) / PT) * ((d.N + PT - 1) / PT) * d.batch;
+    // a second operand pair runs as one GEMM over the concatenated k: K + K2
+    if (d.A2 != nullptr) {
+        GemmDesc one = d;
+        one.A2 = nullptr;
+        one.K = d.K + d.K2;
+        return panel_preferred(one);
+    }
     if (tiles < 16 || tiles > 768) return false;
     // Long K with many tiles: every XCD streams the A panels of all its tiles' rows, and the
     // tiled kernel's 64x64 tiles (split over k) re-read half as much (768 x 4096 x 768: 54.6
@@ -403,6 +465,13 @@ int launch_gemm_panel(hipStream_t stream, const GemmDesc &d) {
     a.accumulate = d.accumulate;
     a.per_batch = make_fastdiv((uint32_t)(a.tiles_m * a.tiles_n));
     a.tm_div = make_fastdiv((uint32_t)a.tiles_m);
+    const bool two = d.A2 != nullptr;
+    a.A2 = d.A2;
+    a.B2 = d.B2;
+    a.lda2 = d.lda2;
+    a.ldb2 = d.ldb2;
+    a.G1 = d.K / PKG;
+    if (two) a.K = d.K + d.K2;  // the kernel walks the k-groups of both pairs
     // NW wavefronts split the k-groups (8, two per SIMD, unless K has fewer k-groups), each
     // with one k-group (8 KB) in flight while it multiplies the previous one: 64 KB of LDS.
     // Measured at 64 x 1536 x 4096 (100 rotating inputs, graph replay, us): 8 wavefronts
@@ -415,18 +484,13 @@ int launch_gemm_panel(hipStream_t stream, const GemmDesc &d) {
     // within 1 % of after 4. With the one-barrier epilogue (same harness, another box):
     // 9.20 -> 9.03, 9.01 -> 8.17 and 57.6 -> 55.1. Starting k-group 0 after 5 of its 8
     // loads: 8.95 -> 8.90, 8.15 -> 7.91, 64 x 1024 x 4096 7.03 -> 6.75.
-    const int G = d.K / PKG;
+    const int G = a.K / PKG;
     int nw = G >= 8 ? 8 : (G >= 4 ? 4 : (G >= 2 ? 2 : 1));
-    int rc;
-    if (!d.transA && !d.transB)
-        rc = launch_nw<true, false>(stream, a, nw);
-    else if (!d.transA)
-        rc = launch_nw<true, true>(stream, a, nw);
-    else if (!d.transB)
-        rc = launch_nw<false, false>(stream, a, nw);
-    else
-        rc = launch_nw<false, true>(stream, a, nw);
-    record_plan("panel", d, PT, PT, 1, 16);
+    const int rc = two ? launch_layout<true>(stream, a, d, nw)
+                       : launch_layout<false>(stream, a, d, nw);
+    GemmDesc shown = d;
+    shown.K = a.K;
+    record_plan(two ? "panel-pair" : "panel", shown, PT, PT, 1, 16);
     return rc;
 }
 

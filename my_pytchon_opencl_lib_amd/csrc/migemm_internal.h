@@ -65,6 +65,14 @@ struct GemmDesc {
     // device array); nullptr = the library workspace of the stream.
     float *scratch = nullptr;
     size_t scratch_bytes = 0;
+    // Optional second operand pair (batch 1): C = opA(A) opB(B) + opA(A2) opB(B2) (+ bias),
+    // A2 [M, K2] and B2 [K2, N] in the orientations of A and B (the stateful LSTM gates
+    // x_t W + h_{t-1} U). Only the panel kernel takes it; run_gemm_pair otherwise runs the
+    // two products as two GEMMs.
+    const float *A2 = nullptr;
+    const float *B2 = nullptr;
+    int64_t lda2 = 0, ldb2 = 0;
+    int K2 = 0;
 };
 
 // Device memory for `bytes` of fp32 partial sums of the GEMM `d`: d.scratch when the call
@@ -98,13 +106,16 @@ bool skinny_supported(const GemmDesc &d);
 // >= 64 MB of B; transposed: enough rows of B, gemm_skinny.hip).
 bool skinny_preferred(const GemmDesc &d);
 int launch_gemm_small(hipStream_t stream, const GemmDesc &d);
-// A K-contiguous, B N-contiguous, K % 8 == 0, N % 4 == 0, 16-byte aligned rows
+// Every operand layout with K % 32 == 0 (K2 % 32 == 0 for a second pair), N % 4 == 0,
+// M % 4 == 0 when A is transposed, 16-byte aligned operand rows and lda, ldb <= 2^25
 // (gemm_panel_kernel: 32x32 tiles, operands loaded straight into LDS).
 bool panel_supported(const GemmDesc &d);
 // Supported, and a shape where it beats the small and tiled families.
 bool panel_preferred(const GemmDesc &d);
 
-// Short-K kernel (gemm_tiny.hip): one wavefront per 16x16 tile over the whole K <= 80.
+// Short-K kernel (gemm_tiny.hip): 16x16 tiles with all operands in registers, one
+// wavefront per tile over K <= 80, two or four (each a share of K) for K = 96, 128, 160,
+// 192, 256 or 320.
 bool tiny_supported(const GemmDesc &d);
 bool tiny_preferred(const GemmDesc &d);
 int launch_gemm_tiny(hipStream_t stream, const GemmDesc &d);

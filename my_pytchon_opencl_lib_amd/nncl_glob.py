@@ -10,6 +10,8 @@ Reference interfaces mirrored (paths relative to the reference repository;
   Tensor LinearForward(x, w, bias)    :1493    NnClGlob.LinearForward(x, w, bias)
   Tensor LinearBiasBackward(g, shape) :1557    NnClGlob.LinearBiasBackward(g, shape)
   Tensor Sum(x, axis, keepDims)       :1595    NnClGlob.Sum(x, axis, keepDims)
+  LstmWithWithState gate loop        :1067    NnClGlob.LstmHidGates(x, w, u, bias, hPrev,
+                                                                   hOut, workspace, t)
   Python NnClGlob (compiler/nncl_glob.py)
   bmm(A, B)                           :110     NnClGlob.bmm(A, B)
   permute(x, axes)                    :148     NnClGlob.permute(x, axes)
@@ -210,6 +212,35 @@ class NnClGlob:
         _launch("migemm_lstm_recurrent_gates", (xw, hOut, u), _ptr(xw), _ptr(hOut), _ptr(u), b,
                 s_, h, int(t))
         return xw
+
+    def LstmHidGates(self, x, w, u, bias, hPrev, hOut, workspace, t):
+        """The gate product of step t of lstm_hid_forward (lstm.cl:788-870, gate loop
+        :832-844), enqueued by NnClGlob.LstmWithWithState (NnClGlob.cs:1067-1100), in place
+        on workspace [S, B, 4H]: workspace[t] = bias + x[:, t] @ w + h_{t-1} @ u, with
+        h_{t-1} = hPrev [B, H] at t = 0 and hOut[:, t-1] ([B, S, H]) after. x is [B, S, F],
+        w [F, 4H], u [H, 4H], bias [4H]. One launch over the four separate buffers; the
+        activations and cell update that follow in the reference kernel are the caller's."""
+        for name, v in (("x", x), ("w", w), ("u", u), ("bias", bias), ("hPrev", hPrev),
+                        ("hOut", hOut), ("workspace", workspace)):
+            _check_tensor(name, v)
+        _require(x.dim() == 3, f"x must be [Batch, Seq, In] (got {list(x.shape)})")
+        b, s_, f = x.shape
+        _require(u.dim() == 2 and u.shape[1] == 4 * u.shape[0],
+                 f"u must be [hidden, 4*hidden] (got {list(u.shape)})")
+        h = u.shape[0]
+        g = 4 * h
+        _require(list(w.shape) == [f, g], f"w must be [{f}, {g}] (got {list(w.shape)})")
+        _require(bias.numel() == g, f"bias must have {g} elements (got {bias.numel()})")
+        _require(list(hPrev.shape) == [b, h], f"hPrev must be [{b}, {h}] (got {list(hPrev.shape)})")
+        _require(list(hOut.shape) == [b, s_, h],
+                 f"hOut must be [{b}, {s_}, {h}] (got {list(hOut.shape)})")
+        _require(list(workspace.shape) == [s_, b, g],
+                 f"workspace must be [{s_}, {b}, {g}] (got {list(workspace.shape)})")
+        _require(0 <= t < s_, f"step {t} is outside [0, {s_})")
+        _launch("migemm_lstm_hid_gates", (x, w, u, bias, hPrev, hOut, workspace), _ptr(x),
+                _ptr(w), _ptr(u), _ptr(bias), _ptr(hPrev), _ptr(hOut), _ptr(workspace), b, s_,
+                f, h, int(t))
+        return workspace
 
     def LstmGemmGradX(self, allGradGates, w, xShape):
         """grad_X (shape xShape) = allGradGates[T, 4H] @ w[F, 4H]^T: stage 2 of

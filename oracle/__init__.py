@@ -52,6 +52,7 @@ def lib():
         L.oracle_lstm_gemm_grad_x.argtypes = [f, f, f, i32, i32, i32]
         L.oracle_lstm_gemm_grad_weights.argtypes = [f] * 6 + [i32] * 4
         L.oracle_lstm_recurrent_gates.argtypes = [f, f, f, f, i32, i32, i32, i32]
+        L.oracle_lstm_hid_gates.argtypes = [f] * 7 + [i32] * 5
         L.oracle_tensor_permute.argtypes = [f, f, i, i, i32]
         L.oracle_reduce_sum_axis.argtypes = [f, f, i32, i32, i32]
         L.oracle_linear_bias_backward.argtypes = [f, f, i32, i32]
@@ -224,6 +225,21 @@ def lstm_recurrent_gates(XW, H_out, U, t):
     H = U.shape[0]
     gates = np.empty((B, Gt), dtype=np.float32)
     lib().oracle_lstm_recurrent_gates(_fp(XW), _fp(H_out), _fp(U), _fp(gates), B, S, H, t)
+    return gates
+
+
+def lstm_hid_gates(X, W, U, bias, H_prev, H_out, t):
+    """lstm.cl:826-844: the raw gates [B, 4H] of step t of lstm_hid_forward with the
+    reference's fp32 arithmetic: bias[g] as the accumulator's start, then one fma chain over
+    X[b, t, :] against W and over h_{t-1} against U; h_{t-1} = H_prev [B, H] at t = 0, else
+    H_out[:, t-1] ([B, S, H])."""
+    B, S, F = X.shape
+    H = U.shape[0]
+    gates = np.empty((B, 4 * H), dtype=np.float32)
+    Hp = np.ascontiguousarray(H_prev, dtype=np.float32)
+    Ho = np.ascontiguousarray(H_out, dtype=np.float32)
+    lib().oracle_lstm_hid_gates(_fp(X), _fp(W), _fp(U), _fp(bias), _fp(Hp), _fp(Ho),
+                                _fp(gates), B, S, F, H, t)
     return gates
 
 

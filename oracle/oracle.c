@@ -36,6 +36,15 @@
  *    the committed fixture tests/golden/reference_outputs.npz), by exact small-integer
  *    products against an independent numpy construction, and by a planted mistake (the
  *    hidden state of step t instead of t-1) that the known answers reject.
+ *  - oracle_lstm_hid_gates follows the gate loop of lstm_hid_forward,
+ *    cs/cl_kernels/lstm.cl:826-844: the accumulator starts at bias[g], then one fma chain
+ *    over the step's input row against W (i ascending) continued over h_{t-1} against U (h
+ *    ascending); h_{t-1} is H_prev at t == 0, else the kernel's own previous output. Pinned
+ *    by the reference kernel's stored gates (its workspace, tests/test_reference_gpu.py and
+ *    the committed fixture tests/golden/reference_outputs.npz), by exact small-integer
+ *    answers against an independent numpy construction, and by planted mistakes (bias
+ *    added last, h_t instead of h_{t-1}, the U chain before the W chain) that the fixture
+ *    rejects.
  *  - oracle_tensor_permute follows cl_kernels/permute.cl:11-50. Pinned by numpy.transpose.
  *  - oracle_reduce_sum_axis / oracle_linear_bias_backward follow
  *    cs/cl_kernels/reduce_sum_axis.cl:3-24 and cs/cl_kernels/linear.cl:149-168: sequential
@@ -254,6 +263,40 @@ void oracle_lstm_recurrent_gates(const float *XW, const float *Hout, const float
             }
             gates[(int64_t)b * Gt + g] = acc;
         }
+}
+
+/* The gate loop of lstm_hid_forward, cs/cl_kernels/lstm.cl:826-844, for one step t:
+ *   x_offset  = b*(seq_len*in_features) + t*in_features                          :827
+ *   ws_offset = t*(batch*4H) + b*4H                                               :828
+ *   val = bias[g]                                                                 :833
+ *   val = fma(X[x_offset + i], W[i*4H + g], val) for i = 0..in_features-1          :835-837
+ *   val = fma(h_curr[h], U[h*4H + g], val)        for h = 0..hidden-1              :839-841
+ *   workspace[ws_offset + g] = val                                                :843
+ * (OpenCL C contracts `val += a*b` to an fma by default). h_curr is H_prev[b*H + h] at t == 0
+ * (:819-822) and afterwards the previous step's hidden state, which the kernel also stores
+ * as H_out[b*(seq_len*H) + (t-1)*H + h] (:861). gates[b*4H + g] receives val. */
+void oracle_lstm_hid_gates(const float *X, const float *W, const float *U, const float *bias,
+                           const float *Hprev, const float *Hout, float *gates, int batch_size,
+                           int seq_len, int in_features, int hidden, int t) {
+    const int Gt = 4 * hidden;
+    /* Each gate's chain is the kernel's, in its order; the loops run g innermost so W and U
+     * are read by rows (the chains of different g are independent). */
+#pragma omp parallel for schedule(static)
+    for (int b = 0; b < batch_size; ++b) {
+        const float *x = X + (int64_t)b * seq_len * in_features + (int64_t)t * in_features;
+        const float *hp = t == 0 ? Hprev + (int64_t)b * hidden
+                                 : Hout + (int64_t)b * seq_len * hidden + (int64_t)(t - 1) * hidden;
+        float *val = gates + (int64_t)b * Gt;
+        for (int g = 0; g < Gt; ++g) val[g] = bias[g];
+        for (int i = 0; i < in_features; ++i) {
+            const float *w = W + (int64_t)i * Gt;
+            for (int g = 0; g < Gt; ++g) val[g] = fmaf(x[i], w[g], val[g]);
+        }
+        for (int h = 0; h < hidden; ++h) {
+            const float *u = U + (int64_t)h * Gt;
+            for (int g = 0; g < Gt; ++g) val[g] = fmaf(hp[h], u[g], val[g]);
+        }
+    }
 }
 
 /* permute.cl:11-50: dst[tid] = src[src_index(permuted coords)], up to 10 dimensions. */

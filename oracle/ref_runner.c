@@ -22,6 +22,7 @@
  *                      NnClGlob.cs:1017-1024
  *   lstm_recurrent_forward  global (wg, 1, batch) local (wg, 1, 1) with
  *                      wg = min(max work-group size, ceil(H/32)*32)  NnClGlob.cs:920-928
+ *   lstm_hid_forward   global (batch) local chosen by the driver     NnClGlob.cs:1080-1097
  *
  * Usage: ref_runner <code_object> <kernel> <M> <K> <N> <batch> <sA> <sB> <sC> <transA>
  *                   <transB> <A.f32> <B.f32|-> <bias.f32|-> <out.f32> [reps]
@@ -33,7 +34,10 @@
  *  grad_bias, which are re-uploaded before every repetition (the kernel accumulates), and
  *  <out> receives the three concatenated.
  *  lstm_recurrent_forward: M = batch_size, K = seq_len, N = hidden; A = XW_in [B, S, 4H],
- *  B = U [H, 4H]; <out> receives H_out [B, S, H] followed by workspace [S, B, 5H].)
+ *  B = U [H, 4H]; <out> receives H_out [B, S, H] followed by workspace [S, B, 5H].
+ *  lstm_hid_forward: M = batch_size, K = seq_len, N = hidden, batch = in_features; A = X
+ *  [B, S, F] then H_prev [B, H] then C_prev [B, H]; B = W [F, 4H] then U [H, 4H]; bias [4H];
+ *  <out> receives H_out [B, S, H], workspace [S, B, 4H], final_H [B, H], final_C [B, H].)
  * Inputs are raw little-endian float32 files; the output file receives the kernel's output
  * buffer. One JSON line on stdout reports the median kernel time from OpenCL profiling
  * events. Exit status 3 means no OpenCL GPU device or the binary was refused (the caller
@@ -145,6 +149,11 @@ int main(int argc, char **argv) {
     const int is_permute = strcmp(kname, "tensor_permute") == 0;
     const int is_gw = strcmp(kname, "lstm_gemm_grad_weights") == 0;
     const int is_rec = strcmp(kname, "lstm_recurrent_forward") == 0;
+    const int is_hid = strcmp(kname, "lstm_hid_forward") == 0;
+    /* lstm_hid_forward (M = batch, K = seq, N = hidden, batch = in_features): H_out,
+     * workspace, final_H, final_C */
+    const size_t hid_n[4] = {(size_t)M * K * N, (size_t)K * M * 4 * (size_t)N, (size_t)M * N,
+                             (size_t)M * N};
     /* lstm_recurrent_forward: H_out [B, S, H] then workspace [S, B, 5H] */
     const size_t rec_n[2] = {(size_t)M * K * N, (size_t)K * M * 5 * (size_t)N};
     size_t out_elems;
@@ -156,6 +165,15 @@ int main(int argc, char **argv) {
         out_elems = a_size / sizeof(float);
     } else if (is_rec) {
         out_elems = rec_n[0] + rec_n[1];
+    } else if (is_hid) {
+        out_elems = hid_n[0] + hid_n[1] + hid_n[2] + hid_n[3];
+        const size_t F = (size_t)batch, H = (size_t)N, Bn = (size_t)M, S = (size_t)K;
+        if (a_size != (Bn * S * F + 2 * Bn * H) * sizeof(float) || !hb ||
+            b_size != (F + H) * 4 * H * sizeof(float) || !hbias ||
+            bias_size != 4 * H * sizeof(float)) {
+            fprintf(stderr, "ref_runner: lstm_hid_forward input sizes do not match\n");
+            return 1;
+        }
     } else if (is_gw) {
         out_elems = gw_n[0] + gw_n[1] + gw_n[2];
         char init_path[4096];
@@ -186,6 +204,7 @@ int main(int argc, char **argv) {
 
     cl_mem gw_bufs[3] = {NULL, NULL, NULL};
     cl_mem rec_ws = NULL;
+    cl_mem hid_bufs[4] = {NULL, NULL, NULL, NULL}; /* H_out (= C), workspace, final_H, final_C */
     size_t gsz[3], lsz[3];
     cl_uint dims = 3;
     size_t *lptr = lsz;
@@ -319,6 +338,41 @@ int main(int argc, char **argv) {
         gsz[2] = (size_t)M;
         lsz[0] = wg;
         lsz[1] = lsz[2] = 1;
+    } else if (is_hid) {
+        /* (X, W, U, bias, H_prev, C_prev, H_out, workspace, final_H, final_C, batch, seq,
+         * in, hidden); the inputs are slices of the A and B files */
+        const int F = batch, H = N;
+        const float *fa = (const float *)ha, *fb = (const float *)hb;
+        const size_t nx = (size_t)M * K * F, nh = (size_t)M * H, nw = (size_t)F * 4 * H,
+                     nu = (size_t)H * 4 * H;
+        cl_mem in_bufs[5];
+        const float *in_src[5] = {fa, fb, fb + nw, fa + nx, fa + nx + nh};
+        const size_t in_n[5] = {nx, nw, nu, nh, nh};
+        for (int i = 0; i < 5; ++i) {
+            in_bufs[i] = clCreateBuffer(ctx, CL_MEM_READ_ONLY | CL_MEM_COPY_HOST_PTR,
+                                        in_n[i] * sizeof(float), (void *)in_src[i], &err);
+            CHECK(err, "lstm_hid_forward input");
+        }
+        hid_bufs[0] = dc;
+        for (int i = 1; i < 4; ++i) {
+            hid_bufs[i] = clCreateBuffer(ctx, CL_MEM_READ_WRITE, hid_n[i] * sizeof(float), NULL,
+                                         &err);
+            CHECK(err, "lstm_hid_forward output");
+        }
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &in_bufs[0]); /* X */
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &in_bufs[1]); /* W */
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &in_bufs[2]); /* U */
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &dbias);      /* bias */
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &in_bufs[3]); /* H_prev */
+        clSetKernelArg(kern, t++, sizeof(cl_mem), &in_bufs[4]); /* C_prev */
+        for (int i = 0; i < 4; ++i) clSetKernelArg(kern, t++, sizeof(cl_mem), &hid_bufs[i]);
+        clSetKernelArg(kern, t++, sizeof(int), &M);
+        clSetKernelArg(kern, t++, sizeof(int), &K);
+        clSetKernelArg(kern, t++, sizeof(int), &F);
+        clSetKernelArg(kern, t++, sizeof(int), &H);
+        dims = 1;
+        gsz[0] = (size_t)M;
+        lptr = NULL;
     } else if (is_permute) {
         /* B file holds int32 dims[M] then axes[M]; M = num_dims */
         const int nd = M;
@@ -386,6 +440,14 @@ int main(int argc, char **argv) {
                                       hc + off, 0, NULL, NULL),
                   "read grads");
             off += gw_n[i];
+        }
+    } else if (is_hid) {
+        size_t off = 0;
+        for (int i = 0; i < 4; ++i) {
+            CHECK(clEnqueueReadBuffer(q, hid_bufs[i], CL_TRUE, 0, hid_n[i] * sizeof(float),
+                                      hc + off, 0, NULL, NULL),
+                  "read lstm_hid_forward outputs");
+            off += hid_n[i];
         }
     } else if (is_rec) {
         CHECK(clEnqueueReadBuffer(q, dc, CL_TRUE, 0, rec_n[0] * sizeof(float), hc, 0, NULL,

@@ -28,6 +28,7 @@ CODE_OBJECT = {
     "lstm_gemm_grad_x": "lstm.co",
     "lstm_gemm_grad_weights": "lstm.co",
     "lstm_recurrent_forward": "lstm.co",
+    "lstm_hid_forward": "lstm.co",
 }
 
 
@@ -98,3 +99,18 @@ def lstm_recurrent_forward(XW, U, reps=1):
     n_h = B * S * H
     ws = res[n_h:].reshape(S, B, 5 * H)
     return res[:n_h].reshape(B, S, H), ws[:, :, :4 * H], ws[:, :, 4 * H:], info
+
+
+def lstm_hid_forward(X, W, U, bias, H_prev, C_prev, reps=1):
+    """Runs the reference lstm_hid_forward (cs/cl_kernels/lstm.cl:788-870, one work-item per
+    sequence over all steps of X [B, S, F]); returns (H_out [B, S, H], raw gates [S, B, 4H]
+    -- the kernel's workspace --, final_H [B, H], final_C [B, H], info)."""
+    B, S, F = X.shape
+    H = U.shape[0]
+    A = np.concatenate([np.ravel(X), np.ravel(H_prev), np.ravel(C_prev)]).astype(np.float32)
+    Bm = np.concatenate([np.ravel(W), np.ravel(U)]).astype(np.float32)
+    res, info = run("lstm_hid_forward", A, Bm, bias, M=B, K=S, N=H, batch=F, reps=reps)
+    n = [B * S * H, S * B * 4 * H, B * H, B * H]
+    o = np.cumsum([0] + n)
+    return (res[o[0]:o[1]].reshape(B, S, H), res[o[1]:o[2]].reshape(S, B, 4 * H),
+            res[o[2]:o[3]].reshape(B, H), res[o[3]:o[4]].reshape(B, H), info)

@@ -72,6 +72,7 @@ def cases():
 
 
 def main(path=OUT):
+    print("writing", path, flush=True)
     data, meta = {}, {}
     for name, kernel, inputs, args in cases():
         res, info = ref.run(kernel, inputs["A"], inputs.get("B"), inputs.get("bias"), reps=1,
@@ -101,6 +102,22 @@ def main(path=OUT):
     for k, v in {"XW": XW, "U": U, "H_out": Ho, "gates": gates, "cells": cells}.items():
         data[f"{name}.{k}"] = v
     meta[name] = {"kernel": "lstm_recurrent_forward", "args": {"B": B, "S": S, "H": H}}
+    # lstm_hid_forward: the stored raw gates of every step (bias-first chains over x_t W and
+    # h_{t-1} U), with a non-zero incoming state, at two ragged sizes
+    for (B, S, F, H, seed) in [(3, 4, 10, 12, 67), (2, 3, 33, 20, 68)]:
+        X = oracle.normal((B, S, F), seed, 0)
+        W = oracle.uniform((F, 4 * H), seed, 1, -0.3, 0.3)
+        U = oracle.uniform((H, 4 * H), seed, 2, -0.3, 0.3)
+        bias = oracle.uniform((4 * H,), seed, 3, -0.3, 0.3)
+        Hp = oracle.uniform((B, H), seed, 4, -0.5, 0.5)
+        Cp = oracle.uniform((B, H), seed, 5, -0.5, 0.5)
+        Ho, gates, fH, fC, info = ref.lstm_hid_forward(X, W, U, bias, Hp, Cp)
+        name = f"lstm_hid_forward_b{B}_s{S}_f{F}_h{H}"
+        for k, v in {"X": X, "W": W, "U": U, "bias": bias, "H_prev": Hp, "C_prev": Cp,
+                     "H_out": Ho, "gates": gates, "final_H": fH, "final_C": fC}.items():
+            data[f"{name}.{k}"] = v
+        meta[name] = {"kernel": "lstm_hid_forward", "args": {"B": B, "S": S, "F": F, "H": H}}
+        print(name, info["device"], flush=True)
     data["_meta"] = np.frombuffer(json.dumps({"device": info["device"], "cases": meta},
                                              sort_keys=True).encode(), dtype=np.uint8)
     np.savez_compressed(path, **data)

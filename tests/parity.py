@@ -92,3 +92,33 @@ class Tuner:
         for k, v in self.saved.items():
             _native.set_tuning(k, v)
         self.saved = {}
+
+
+def check_full(C, A, B, transA, transB, bias=None, ref=None):
+    """Whole-output check of a single 2-D GEMM C = op(A) op(B) (+ bias) against fp64: C64
+    and |op(A)| |op(B)| (+ |bias|) by numpy's float64 matmul over every element, both error
+    bounds of oracle.errors, and (if given) the componentwise distance of every element to
+    the reference kernel's output `ref`. Returns (normwise, componentwise, vs_ref)."""
+    a = np.asarray(A, np.float64)
+    b = np.asarray(B, np.float64)
+    a = a.T if transA else a
+    b = b.T if transB else b
+    K = a.shape[1]
+    c64 = a @ b
+    ap = np.abs(a) @ np.abs(b)
+    if bias is not None:
+        c64 += np.asarray(bias, np.float64)
+        ap += np.abs(np.asarray(bias, np.float64))
+    C = np.asarray(C).reshape(c64.shape)
+    assert np.all(np.isfinite(C)), "non-finite output"
+    tol = oracle.tolerance(K)
+    nw, cw = oracle.errors(C, c64, ap)
+    assert nw <= tol, f"normwise error {nw:.3e} > {tol:.3e}"
+    assert cw <= tol, f"componentwise error {cw:.3e} > {tol:.3e}"
+    vs_ref = 0.0
+    if ref is not None:
+        d = np.abs(C.astype(np.float64) - np.asarray(ref, np.float64).reshape(c64.shape))
+        with np.errstate(divide="ignore", invalid="ignore"):
+            vs_ref = float(np.max(np.where(ap > 0, d / ap, np.where(d > 0, np.inf, 0.0))))
+        assert vs_ref <= 2 * tol, f"distance to the reference kernel {vs_ref:.3e}"
+    return nw, cw, vs_ref

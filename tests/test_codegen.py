@@ -1,8 +1,9 @@
-"""Checks on the generated gfx950 code of the direct-to-LDS GEMM kernel (CPU only: hipcc
+"""Checks on the generated gfx950 code of the direct-to-LDS GEMM kernels (CPU only: hipcc
 cross-compiles the device code to assembly text).
 
-gemm_direct.hip issues global_load_lds_dwordx4 / global_load_lds_dword through inline
-assembly that sets M0 itself and declares it clobbered. M0 is a register the compiler
+gemm_direct_kernel (gemm_direct.h) and gemm_panel_kernel (gemm_panel.hip) issue
+global_load_lds_dwordx4 / global_load_lds_dword through inline assembly that sets M0 itself
+and declares it clobbered. M0 is a register the compiler
 reserves, so the kernels may only be correct if no compiler-generated code relies on M0
 across those statements. This test pins that: in the device assembly, M0 is written only by
 `s_mov_b32 m0, s<n>` immediately followed by one of those loads, and nothing reads it
@@ -16,8 +17,10 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "my_pytchon_opencl_lib_amd", "csrc")
-# the translation units that instantiate gemm_direct_kernel (one per tile shape)
-SRCS = [os.path.join(CSRC, f"gemm_direct_{t}.hip") for t in ("256", "128x256", "128", "64")]
+# the translation units that instantiate gemm_direct_kernel (one per tile shape) and the
+# panel kernel (every operand layout, one or two operand pairs)
+SRCS = [os.path.join(CSRC, f"gemm_direct_{t}.hip") for t in ("256", "128x256", "128", "64")] + \
+    [os.path.join(CSRC, "gemm_panel.hip")]
 
 
 def _hipcc():

@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import oracle
-from parity import Tuner, check_gemm, dev, host, sample_rows
+from parity import Tuner, check_full, check_gemm, dev, host, sample_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -208,7 +208,7 @@ def test_config3_lstm_gate_gemm(nncl):
 
 def test_config3_all_100_timesteps_and_graph_replay(nncl):
     """BASELINE config 3 as the bench runs it: 100 timestep inputs x[t] (64 x 1536) through
-    gemm + bias with one W [1536, 4096]. Every step is checked against fp64 (sampled rows of
+    gemm + bias with one W [1536, 4096]. Every step is checked against fp64 (every element of
     the stacked 6400 x 4096 output, tolerance 1e-5 sqrt(K)); then the 100 calls are captured
     in a HIP graph and each of three replays must reproduce the eager outputs bit for bit
     (the kernels are deterministic, and the graph path must not change the plan)."""
@@ -222,8 +222,7 @@ def test_config3_all_100_timesteps_and_graph_replay(nncl):
     for t in range(steps):
         nncl.gemm(x[t], w, bias=b, out=eager[t])
     Y = host(eager).reshape(steps * 64, 4096)
-    check_gemm(Y, X, W, 0, 0, bias=bias, M=steps * 64, N=4096, K=1536, lda=1536, ldb=4096,
-               rows=sample_rows(steps * 64, 96))
+    check_full(Y, X, W, 0, 0, bias=bias)
     out = torch.full((steps, 64, 4096), float("nan"), device="cuda:0")
     cap = torch.cuda.Stream()
     with torch.cuda.stream(cap):
@@ -250,7 +249,9 @@ def test_config4_4096_cube(nncl, form):
     ta, tb = {"NN": (0, 0), "NT": (0, 1), "TN": (1, 0)}[form]
     say("config4", form)
     C = gemm_gpu(nncl, A, B, bool(ta), bool(tb))
-    check_gemm(C, A, B, ta, tb, M=n, N=n, K=n, lda=n, ldb=n, rows=sample_rows(n, 16))
+    # every one of the 4096^2 outputs against fp64 (numpy float64 matmul, a few seconds)
+    nw, cw, _ = check_full(C, A, B, ta, tb)
+    say("config4", form, "whole output: normwise", nw, "componentwise", cw)
 
 
 def test_config5a_ragged(nncl):
@@ -258,9 +259,8 @@ def test_config5a_ragged(nncl):
     B = oracle.uniform((777, 3000), 4, 1)
     say("config5a ragged")
     C = gemm_gpu(nncl, A, B)
-    rows = sample_rows(1000, 40)
     ref = oracle.matmul_rows(A, B, 0, 1000, threads=8)
-    check_gemm(C, A, B, 0, 0, M=1000, N=3000, K=777, lda=777, ldb=3000, rows=rows, ref=ref)
+    check_full(C, A, B, 0, 0, ref=ref)
 
 
 def test_config5b_gemv(nncl):
@@ -270,7 +270,7 @@ def test_config5b_gemv(nncl):
     C = gemm_gpu(nncl, A, B)
     check_gemm(C, A, B, 0, 0, M=1, N=11008, K=4096, lda=4096, ldb=11008,
                ref=oracle.matmul_rows(A, B, 0, 1, threads=8))
-    # repeated calls reuse the arrival counters: the result must not change
+    # a repeated call (same plan, same workspace) gives the same bits
     C2 = gemm_gpu(nncl, A, B)
     assert np.array_equal(C, C2)
 

@@ -389,7 +389,8 @@ def test_restatement_equals_reference_fixture():
     (its OpenCL sources compiled for gfx950, run on the GPU by
     tests/golden/make_reference_golden.py): matmul_tiled, bmm_tiled (with a broadcast B),
     bmm_permute_tiled in all four layouts, linear_forward_tiled, tensor_permute, the three
-    lstm.cl GEMMs and lstm_recurrent_forward's stored gates. The restatement reproduces every
+    lstm.cl GEMMs, lstm_recurrent_forward's and lstm_hid_forward's stored gates. The
+    restatement reproduces every
     one of them bit for bit, here on the CPU."""
     import json
     d = np.load(REF_FIXTURE, allow_pickle=False)
@@ -411,6 +412,12 @@ def test_restatement_equals_reference_fixture():
             for t in range(a["S"]):
                 assert np.array_equal(oracle.lstm_recurrent_gates(XW, Ho, U, t), gates[t]), \
                     (name, t)
+        elif kernel == "lstm_hid_forward":
+            X, W, U, bias, Hp, Ho, gates = (d[f"{name}.{k}"] for k in (
+                "X", "W", "U", "bias", "H_prev", "H_out", "gates"))
+            for t in range(a["S"]):
+                assert np.array_equal(oracle.lstm_hid_gates(X, W, U, bias, Hp, Ho, t),
+                                      gates[t]), (name, t)
         else:
             inp = {k: d[f"{name}.{k}"] for k in ("A", "B", "bias") if f"{name}.{k}" in d}
             out = d[f"{name}.out"]
@@ -418,7 +425,7 @@ def test_restatement_equals_reference_fixture():
             assert ours.shape == out.shape and np.array_equal(ours, out), name
     assert kernels == {"matmul_tiled", "bmm_tiled", "bmm_permute_tiled", "linear_forward_tiled",
                        "tensor_permute", "lstm_gemm_xw", "lstm_gemm_grad_x",
-                       "lstm_gemm_grad_weights", "lstm_recurrent_forward"}
+                       "lstm_gemm_grad_weights", "lstm_recurrent_forward", "lstm_hid_forward"}
 
 
 def test_reference_fixture_catches_planted_mistakes():
@@ -440,3 +447,74 @@ def test_reference_fixture_catches_planted_mistakes():
     A, B, out = d[f"{name}.A"], d[f"{name}.B"], d[f"{name}.out"]
     wrong = oracle.bmm_permute(A, np.ascontiguousarray(B.reshape(2, 47, 29)), False, False)
     assert not np.array_equal(np.ravel(wrong), out)
+
+
+def _hid_case(name):
+    d = np.load(REF_FIXTURE, allow_pickle=False)
+    return {k: d[f"{name}.{k}"] for k in ("X", "W", "U", "bias", "H_prev", "H_out", "gates")}
+
+
+def test_hid_gates_small_integer_answers():
+    """oracle_lstm_hid_gates with small-integer operands (every partial sum exact) equals
+    the integer answer bias + x_t W + h_{t-1} U, built here with int64 numpy, at every step:
+    h_{t-1} is the incoming state at t = 0 and the previous step's output after. A mistake
+    of index (the step's own output h_t, x of another step, a transposed weight) changes
+    the answer."""
+    rng = np.random.default_rng(5)
+    B, S, F, H = 3, 4, 7, 5
+    G = 4 * H
+    ints = lambda *s: rng.integers(-3, 4, size=s).astype(np.float32)
+    X, W, U, bias, Hp, Ho = ints(B, S, F), ints(F, G), ints(H, G), ints(G), ints(B, H), ints(B, S, H)
+    i64 = lambda a: a.astype(np.int64)
+    for t in range(S):
+        prev = Hp if t == 0 else Ho[:, t - 1]
+        expect = i64(bias) + i64(X[:, t]) @ i64(W) + i64(prev) @ i64(U)
+        got = oracle.lstm_hid_gates(X, W, U, bias, Hp, Ho, t)
+        assert np.array_equal(got, expect.astype(np.float32)), t
+        wrong = i64(bias) + i64(X[:, t]) @ i64(W) + i64(Ho[:, t]) @ i64(U)
+        assert not np.array_equal(got, wrong.astype(np.float32)), t
+
+
+def test_hid_fixture_catches_planted_mistakes():
+    """The reference's stored lstm_hid_forward gates reject plausible restatement mistakes:
+    the bias added after the products (as linear.cl / lstm_gemm_xw do, not lstm.cl:833),
+    the U chain before the W chain, a chain without fused multiply-adds, and h_t in place
+    of h_{t-1}. Each would be a single plausible slip in the restatement."""
+    c = _hid_case("lstm_hid_forward_b2_s3_f33_h20")
+    X, W, U, bias, Hp, Ho, gates = (c[k] for k in ("X", "W", "U", "bias", "H_prev", "H_out",
+                                                   "gates"))
+    B, S, F = X.shape
+    H = U.shape[0]
+    z = np.zeros_like(bias)
+    for t in range(S):
+        prev = Hp if t == 0 else Ho[:, t - 1]
+        assert np.array_equal(oracle.lstm_hid_gates(X, W, U, bias, Hp, Ho, t), gates[t])
+        # bias last: the chain from 0, then one add
+        bias_last = oracle.lstm_hid_gates(X, W, U, z, Hp, Ho, t) + bias
+        assert not np.array_equal(bias_last, gates[t]), t
+        # U chain first: one chain over [h_{t-1} || x_t] against [U; W] (the h part of the
+        # restatement fed zeros, whose fmas leave the accumulator unchanged)
+        xh = np.concatenate([prev, X[:, t]], axis=1)[:, None, :].copy()
+        UW = np.concatenate([U, W])
+        zU, zH = np.zeros_like(U), np.zeros((B, H), np.float32)
+        swapped = oracle.lstm_hid_gates(xh, UW, zU, bias, zH, zH[:, None, :].copy(), 0)
+        assert not np.array_equal(swapped, gates[t]), t
+        same_order = np.concatenate([X[:, t], prev], axis=1)[:, None, :].copy()
+        kept = oracle.lstm_hid_gates(same_order, np.concatenate([W, U]), zU, bias, zH,
+                                     zH[:, None, :].copy(), 0)
+        assert np.array_equal(kept, gates[t]), t  # the construction itself is faithful
+        # unfused chain in the kernel's own order
+        unfused = np.empty_like(gates[t])
+        for b in range(B):
+            acc = bias.copy()
+            for i in range(F):
+                acc = (acc + X[b, t, i] * W[i]).astype(np.float32)
+            for h in range(H):
+                acc = (acc + prev[b, h] * U[h]).astype(np.float32)
+            unfused[b] = acc
+        assert not np.array_equal(unfused, gates[t]), t
+        if t > 0:
+            own = np.ascontiguousarray(Ho[:, 1:])  # h_t in place of h_{t-1}: shift by one
+            Ho_shift = np.concatenate([own, Ho[:, -1:]], axis=1)
+            assert not np.array_equal(oracle.lstm_hid_gates(X, W, U, bias, Hp, Ho_shift, t),
+                                      gates[t]), t
