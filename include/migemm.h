@@ -254,8 +254,10 @@ int migemm_memcpy_h2d(void *stream, void *dst, const void *src, size_t bytes);
 int migemm_memcpy_d2h(void *stream, void *dst, const void *src, size_t bytes);
 int migemm_memset(void *stream, void *dst, int value, size_t bytes);
 int migemm_stream_create(void **stream);
-/* Waits for the stream's queued work, frees the library workspace held for it (see
- * migemm_workspace_release) and destroys it. */
+/* Frees the library workspace held for the stream (see migemm_workspace_release), stops
+ * treating it as a registered queue (migemm_queue_register_current; a thread that still
+ * names it as its current queue must not compute on it), waits for its queued work and
+ * destroys it. */
 int migemm_stream_destroy(void *stream);
 int migemm_stream_synchronize(void *stream);
 
@@ -263,17 +265,21 @@ int migemm_stream_synchronize(void *stream);
  * sums in device memory that the library owns: one growing buffer per (device, stream),
  * plus one for operands an entry point stages (lstm_gemm_grad_weights' H_prev), so calls
  * on different streams never share partial sums. The reference host has no counterpart
- * (its kernels never split K).
+ * (its kernels never split K). The buffers come from a device memory pool of the library
+ * in the stream's order, and an outgrown or released buffer is freed in the stream's order
+ * (after the queued work that uses it): neither waits on the host.
  * Nothing is allocated while a stream is being captured into a HIP graph, and a capturing
  * stream uses only its own buffers: size them before the capture, with this call or by
  * running the same calls once on that stream. A call that needs more during a capture
- * fails with MIGEMM_ERR_WORKSPACE. */
-/* Grows each of `stream`'s two workspace buffers (current device) to >= bytes. */
+ * fails with MIGEMM_ERR_WORKSPACE. A buffer that a graph captured lives until the process
+ * ends and is no longer used by eager calls after the capture (the next eager call on the
+ * stream gets a new one), so replaying the graph on another stream cannot race with them. */
+/* Grows each of `stream`'s two workspace buffers (the stream's device) to >= bytes. */
 int migemm_workspace_reserve(void *stream, size_t bytes);
-/* Waits for the stream's queued work and frees its workspace buffers (current device),
- * except those a HIP graph captured, which live until the process ends. */
+/* Frees the stream's workspace buffers in the stream's order (the work queued so far still
+ * uses them), except those a HIP graph captured. */
 int migemm_workspace_release(void *stream);
-/* Current size of `stream`'s partial-sum buffer on the current device (0 if none). */
+/* Current size of `stream`'s partial-sum buffer (0 if none). */
 int migemm_workspace_size(void *stream, size_t *bytes);
 /* Message of the last failing call on this host thread ("" if none). */
 const char *migemm_last_error(void);
@@ -304,10 +310,14 @@ int migemm_context_info(void *ctx, int *device, char *arch_name, size_t arch_nam
                         int *work_group_x, int *work_group_y, size_t *global_mem_bytes);
 
 /* Replaces OpenCLBufferManager.GetOrCreateBuffer (cs/compiler/OpenCLBufferManager.cs:22-61):
- * the device buffer called `name` if it belongs to `ctx` and holds >= bytes; otherwise the
- * old one (if any) is freed -- after its device has finished the work queued so far, since
- * kernels may still use it -- and a buffer of exactly `bytes` is allocated on the context's
- * device. Errors as the reference's: null context, empty name, zero size (:24-26). */
+ * the device buffer called `name` if it belongs to `ctx` and holds >= bytes; otherwise a
+ * buffer of exactly `bytes` is allocated on the context's device and the old one (if any)
+ * is released. A released buffer is freed once the work queued before the release on every
+ * registered queue of its device (and on the null stream) has run, as an OpenCL buffer
+ * outlives its release until the kernels using it finish; the caller never waits for that.
+ * Lookups that find their buffer run in parallel across threads. Errors as the reference's:
+ * null context, empty name, zero size (:24-26); a handle of a destroyed context is rejected
+ * on every thread. */
 int migemm_buffer_get_or_create(void *ctx, const char *name, size_t bytes, void **ptr);
 /* Replaces OpenCLBufferManager.ReleaseBuffer (:66-75); an unknown name is not an error. */
 int migemm_buffer_release(const char *name);
@@ -317,10 +327,12 @@ int migemm_buffer_release_all(void);
 int migemm_buffer_count(size_t *count, size_t *total_bytes);
 
 /* Replaces DeviceQueueRegistry.RegisterCurrent (cs/core/DeviceQueueRegistry.cs:19-22): the
- * calling thread's current queue is `stream` of `ctx`; a null stream is rejected (:21). */
+ * calling thread's current queue is `stream` of `ctx`; a null stream is rejected (:21), and
+ * so is a stream of another device than the context's. */
 int migemm_queue_register_current(void *ctx, void *stream);
 /* Replaces DeviceQueueRegistry.GetCurrent (:28-38): MIGEMM_ERR_NO_QUEUE when this thread has
- * registered none. Either output may be NULL. */
+ * registered none, MIGEMM_ERR_INVALID_ARG when its context has been destroyed (by any
+ * thread). Either output may be NULL. */
 int migemm_queue_get_current(void **ctx, void **stream);
 /* Replaces DeviceQueueRegistry.Clear (:43-46). */
 int migemm_queue_clear_current(void);

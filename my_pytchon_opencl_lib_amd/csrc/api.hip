@@ -13,6 +13,7 @@
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <vector>
 
 #include "migemm_internal.h"
 
@@ -51,12 +52,15 @@ struct DeviceWorkspace {
     void *ptr = nullptr;
     size_t bytes = 0;
     // Handed out to work captured into a HIP graph: the graph keeps the address, so the
-    // buffer is never freed (a replay may run at any later time).
+    // buffer is never freed (a replay may run at any later time) and, once the capture has
+    // ended, no longer lent to eager work (a replay on another stream could overlap it).
     bool captured = false;
 };
 std::mutex g_ws_mutex;
 // keyed by (device, stream, slot)
 std::map<std::tuple<int, uintptr_t, int>, DeviceWorkspace> g_ws;
+// buffers that captured graphs refer to: kept until the process ends
+std::vector<void *> g_graph_owned;
 }  // namespace
 
 int set_error(int code, const char *fmt, ...) {
@@ -76,13 +80,23 @@ int hip_check(hipError_t e, const char *what) {
     return set_error(MIGEMM_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+int stream_device(hipStream_t stream, int *device) {
+    if (stream == nullptr) {
+        MIGEMM_HIP(hipGetDevice(device));
+    } else {
+        MIGEMM_HIP(hipStreamGetDevice(stream, device));
+    }
+    return MIGEMM_OK;
+}
+
 // One growing buffer per device, stream and slot: calls on one stream run in order, so
 // they can share a buffer, and calls on different streams (the reference host keeps one
-// queue per thread) never share one. A buffer that is outgrown is retired, not freed:
-// work already queued, or a HIP graph captured earlier, may still refer to it, so retired
-// buffers live until the process ends (the doubling growth keeps them below the live
-// buffer's size). migemm_workspace_release / migemm_stream_destroy free a stream's live
-// buffers once its queued work is done, unless a graph captured them.
+// queue per thread) never share one. Buffers come from the library's device memory pool
+// (runtime.hip) in the stream's order, and an outgrown buffer is freed in the stream's
+// order too (after the work already queued that uses it), so growing never waits on the
+// host. A buffer a HIP graph captured is never freed and, once the capture has ended, is
+// retired from eager use: the next eager call on the stream gets a buffer of its own.
+// migemm_workspace_release / migemm_stream_destroy free a stream's live buffers.
 // Nothing is allocated while the stream is being captured into a HIP graph (an allocation
 // would invalidate the capture), and a capturing stream only uses its own buffer: work on
 // another stream may run at the same time as a replay, so a borrowed buffer could race.
@@ -90,30 +104,28 @@ int hip_check(hipError_t e, const char *what) {
 // by running the same call once on that stream outside the capture.
 void *workspace(hipStream_t stream, size_t bytes, int *status, int slot) {
     int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) {
-        *status = hip_check(e, "hipGetDevice");
-        return nullptr;
-    }
+    *status = stream_device(stream, &dev);
+    if (*status != MIGEMM_OK) return nullptr;
     if (slot < 0 || slot >= kWorkspaceSlots) {
         *status = set_error(MIGEMM_ERR_WORKSPACE, "workspace slot %d", slot);
         return nullptr;
     }
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-    e = hipStreamIsCapturing(stream, &capture);
+    hipError_t e = hipStreamIsCapturing(stream, &capture);
     if (e != hipSuccess) {
         *status = hip_check(e, "hipStreamIsCapturing");
         return nullptr;
     }
+    const bool capturing = capture != hipStreamCaptureStatusNone;
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     const auto key = std::make_tuple(dev, reinterpret_cast<uintptr_t>(stream), slot);
     auto it = g_ws.find(key);
-    if (it != g_ws.end() && it->second.bytes >= bytes) {
-        if (capture != hipStreamCaptureStatusNone) it->second.captured = true;
+    if (it != g_ws.end() && it->second.bytes >= bytes && (capturing || !it->second.captured)) {
+        if (capturing) it->second.captured = true;
         *status = MIGEMM_OK;
         return it->second.ptr;
     }
-    if (capture != hipStreamCaptureStatusNone) {
+    if (capturing) {
         *status = set_error(MIGEMM_ERR_WORKSPACE,
                             "%zu bytes of workspace are needed during HIP graph capture but "
                             "the capturing stream holds %zu: call migemm_workspace_reserve on "
@@ -123,15 +135,22 @@ void *workspace(hipStream_t stream, size_t bytes, int *status, int slot) {
     }
     DeviceWorkspace &w = g_ws[key];
     size_t want = bytes < ((size_t)8 << 20) ? ((size_t)8 << 20) : bytes;
-    if (want < 2 * w.bytes) want = 2 * w.bytes;
+    if (!w.captured && want < 2 * w.bytes) want = 2 * w.bytes;
     void *p = nullptr;
-    e = hipMalloc(&p, want);
-    if (e != hipSuccess) {
-        *status = set_error(MIGEMM_ERR_WORKSPACE, "workspace of %zu bytes: %s", want,
-                            hipGetErrorString(e));
-        return nullptr;
+    *status = devmem_alloc_on(stream, dev, want, &p);
+    if (*status != MIGEMM_OK) return nullptr;
+    if (w.ptr != nullptr) {
+        if (w.captured) {
+            g_graph_owned.push_back(w.ptr);  // the graph keeps using it
+        } else {
+            *status = devmem_free_on(stream, w.ptr);  // after the queued work that uses it
+            if (*status != MIGEMM_OK) {
+                (void)devmem_free_on(stream, p);
+                return nullptr;
+            }
+        }
     }
-    w.ptr = p;  // the previous buffer (if any) is retired, never freed
+    w.ptr = p;
     w.bytes = want;
     w.captured = false;
     *status = MIGEMM_OK;
@@ -151,18 +170,24 @@ float *partial_buffer(hipStream_t stream, const GemmDesc &d, size_t bytes, int *
     return d.scratch;
 }
 
-// Frees the live workspace buffers of `stream` on the current device (the caller has
-// waited for the stream's work). Buffers a graph captured are kept.
+// Frees the live workspace buffers of `stream` (on the stream's device) in the stream's
+// order. Buffers a graph captured are kept.
 static int release_workspace(hipStream_t stream) {
     int dev = 0;
-    MIGEMM_HIP(hipGetDevice(&dev));
+    int rc = stream_device(stream, &dev);
+    if (rc != MIGEMM_OK) return rc;
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     for (int slot = 0; slot < kWorkspaceSlots; ++slot) {
         auto it = g_ws.find(std::make_tuple(dev, reinterpret_cast<uintptr_t>(stream), slot));
         if (it == g_ws.end()) continue;
         const DeviceWorkspace w = it->second;
         g_ws.erase(it);
-        if (!w.captured) MIGEMM_HIP(hipFree(w.ptr));
+        if (w.captured) {
+            g_graph_owned.push_back(w.ptr);
+        } else {
+            rc = devmem_free_on(stream, w.ptr);
+            if (rc != MIGEMM_OK) return rc;
+        }
     }
     return MIGEMM_OK;
 }
@@ -180,10 +205,12 @@ constexpr int kMaxDevices = 64;
 static std::atomic<float *> g_scratch_ptr[kMaxDevices];
 static std::mutex g_scratch_mutex;
 
-// Device address of `scratch` on the current device (looked up on the first call there).
-static int scratch_address(float **out) {
+// Device address of `scratch` on the device of `stream` (looked up on the first call there,
+// with that device current).
+static int scratch_address(hipStream_t stream, float **out) {
     int dev = 0;
-    MIGEMM_HIP(hipGetDevice(&dev));
+    int rc = stream_device(stream, &dev);
+    if (rc != MIGEMM_OK) return rc;
     if (dev < 0 || dev >= kMaxDevices)
         return set_error(MIGEMM_ERR_UNSUPPORTED, "device %d: the no-allocation entry point "
                          "supports devices 0..%d", dev, kMaxDevices - 1);
@@ -192,8 +219,13 @@ static int scratch_address(float **out) {
         std::lock_guard<std::mutex> lock(g_scratch_mutex);
         p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
         if (p == nullptr) {
+            int cur = 0;
+            MIGEMM_HIP(hipGetDevice(&cur));
+            if (cur != dev) MIGEMM_HIP(hipSetDevice(dev));
             void *addr = nullptr;
-            MIGEMM_HIP(hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)));
+            const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+            if (cur != dev) MIGEMM_HIP(hipSetDevice(cur));
+            MIGEMM_HIP(e);
             p = static_cast<float *>(addr);
             g_scratch_ptr[dev].store(p, std::memory_order_release);
         }
@@ -387,7 +419,7 @@ int migemm_gemm_strided_batched_noalloc(void *stream, int transA, int transB, in
                            ldc, strideC, batch, &d);
     if (rc != MIGEMM_OK) return rc;
     d.accumulate = (flags & MIGEMM_GEMM_ACCUMULATE) != 0;
-    rc = scratch_address(&d.scratch);
+    rc = scratch_address(static_cast<hipStream_t>(stream), &d.scratch);
     if (rc != MIGEMM_OK) return rc;
     d.scratch_bytes = MIGEMM_NOALLOC_SCRATCH_BYTES;
     return run_gemm(static_cast<hipStream_t>(stream), d);
@@ -771,10 +803,11 @@ int migemm_stream_destroy(void *stream) {
     clear_error();
     if (stream == nullptr) return MIGEMM_OK;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // the stream's queued work may still use its workspace: wait for it, then free both
-    MIGEMM_HIP(hipStreamSynchronize(s));
-    int rc = release_workspace(s);
+    // deferred frees must not record events on it any more
+    forget_stream(stream);
+    int rc = release_workspace(s);  // in the stream's order
     if (rc != MIGEMM_OK) return rc;
+    MIGEMM_HIP(hipStreamSynchronize(s));
     MIGEMM_HIP(hipStreamDestroy(s));
     return MIGEMM_OK;
 }
@@ -802,18 +835,19 @@ int migemm_workspace_release(void *stream) {
     if (capture != hipStreamCaptureStatusNone)
         return set_error(MIGEMM_ERR_INVALID_ARG,
                          "workspace_release: the stream is being captured into a HIP graph");
-    MIGEMM_HIP(hipStreamSynchronize(s));
     return release_workspace(s);
 }
 
 int migemm_workspace_size(void *stream, size_t *bytes) {
     clear_error();
     if (bytes == nullptr) return set_error(MIGEMM_ERR_INVALID_ARG, "workspace_size: null pointer");
-    int dev = 0;
-    MIGEMM_HIP(hipGetDevice(&dev));
+    // no HIP call: the stream may already have been destroyed (then it holds nothing)
     std::lock_guard<std::mutex> lock(g_ws_mutex);
-    auto it = g_ws.find(std::make_tuple(dev, reinterpret_cast<uintptr_t>(stream), 0));
-    *bytes = it != g_ws.end() ? it->second.bytes : 0;
+    *bytes = 0;
+    for (const auto &kv : g_ws)
+        if (std::get<1>(kv.first) == reinterpret_cast<uintptr_t>(stream) &&
+            std::get<2>(kv.first) == 0)
+            *bytes = kv.second.bytes;
     return MIGEMM_OK;
 }
 

@@ -126,6 +126,25 @@ bool small_preferred(const GemmDesc &d);
 // 5-16 rows of C over a B (not transposed) of 256 MB or more: the tiled kernel's 32x32 tiles.
 bool narrow_rows_streaming(const GemmDesc &d);
 
+// Device memory owned by the library (runtime.hip): a memory pool per device whose frees
+// are stream-ordered, so releasing memory never waits on the host (hipFree would
+// synchronize the whole device).
+// devmem_alloc: `bytes` usable on any stream of `device` when it returns.
+int devmem_alloc(int device, size_t bytes, void **ptr);
+// devmem_alloc_on: `bytes` usable by work queued on `stream` (of `device`) after the call.
+int devmem_alloc_on(hipStream_t stream, int device, size_t bytes, void **ptr);
+// devmem_free_on: frees pool memory once the work queued on `stream` so far has run.
+int devmem_free_on(hipStream_t stream, void *ptr);
+// devmem_free_after: frees pool memory of `device` once the work queued so far on each of
+// the n streams has run (a null entry is the null stream).
+int devmem_free_after(int device, void *ptr, void *const *streams, int n);
+// devmem_trim: waits for pending frees of `device` and returns unused pool memory.
+int devmem_trim(int device);
+// A stream that is about to be destroyed stops being a registered queue.
+void forget_stream(void *stream);
+// The device a stream belongs to (the current device for the null stream).
+int stream_device(hipStream_t stream, int *device);
+
 // Device workspace owned by the library: one growing buffer per device, stream and slot.
 // Slot 0 holds split-K partial sums (GEMM, column sums); slot 1 holds operands staged by
 // an entry point for the GEMMs it then runs (which may use slot 0). Returns nullptr and

@@ -218,11 +218,21 @@ def test_runtime_services_validate_without_gpu(lib):
         results["get"] = lib.migemm_queue_get_current(None, None)
         results["get_msg"] = _native.last_error()
         results["buf"] = lib.migemm_tensor_buffer(b"t0", 64, ctypes.byref(ctypes.c_void_p()))
+    def other_thread():  # handles that are not live contexts fail on any thread
+        results["other"] = lib.migemm_buffer_get_or_create(P[0], b"x", 16,
+                                                           ctypes.byref(ctypes.c_void_p()))
+        results["other_msg"] = _native.last_error()
+        results["other_reg"] = lib.migemm_queue_register_current(ctypes.c_void_p(1), P[1])
     th = threading.Thread(target=fresh_thread)
+    th.start()
+    th.join()
+    th = threading.Thread(target=other_thread)
     th.start()
     th.join()
     assert results["get"] == NO_QUEUE and "no queue is registered" in results["get_msg"]
     assert results["buf"] == NO_QUEUE
+    assert results["other"] == INVALID and "unknown context" in results["other_msg"]
+    assert results["other_reg"] == INVALID
     assert lib.migemm_queue_clear_current() == 0
     n, b = ctypes.c_size_t(9), ctypes.c_size_t(9)
     assert lib.migemm_buffer_count(ctypes.byref(n), ctypes.byref(b)) == 0 and n.value == 0

@@ -408,6 +408,42 @@ def test_graph_replay_overlaps_eager_split_k(nncl):
             assert np.array_equal(host(ys[i]), expect[1 + i]), f"eager {rep}/{i} differs"
 
 
+def test_graph_replay_elsewhere_while_eager_runs_on_the_capture_stream(nncl):
+    """A graph captured on stream S is replayed on another stream while eager split-K GEMMs
+    run on S itself, with no synchronisation between them. The captured partial-sum buffer
+    belongs to the graph once the capture has ended: the eager calls on S get a buffer of
+    their own, so neither result is corrupted."""
+    say("graph replay on another stream, eager split-K on the capture stream")
+    W = dev(small_ints((8192, 1536), 97, -2, 2))
+    xs = [dev(small_ints((64, 8192), 98 + i, -2, 2)) for i in range(4)]
+    expect = [(host(x).astype(np.float64) @ host(W).astype(np.float64)).astype(np.float32)
+              for x in xs]
+    cap, other = torch.cuda.Stream(), torch.cuda.Stream()
+    y_graph = torch.empty(64, 1536, device="cuda:0")
+    with torch.cuda.stream(cap):
+        nncl.gemm(xs[0], W, out=y_graph)  # sizes cap's workspace before the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap):
+        for _ in range(8):
+            nncl.gemm(xs[0], W, out=y_graph)
+    ys = [torch.empty(64, 1536, device="cuda:0") for _ in range(3)]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        y_graph.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(other):
+            g.replay()
+        with torch.cuda.stream(cap):
+            for i in range(3):
+                for _ in range(4):
+                    nncl.gemm(xs[1 + i], W, out=ys[i])
+        torch.cuda.synchronize()
+        assert np.array_equal(host(y_graph), expect[0]), f"replay {rep} differs"
+        for i in range(3):
+            assert np.array_equal(host(ys[i]), expect[1 + i]), f"eager {rep}/{i} differs"
+
+
 def test_stream_destroy_frees_its_workspace(nncl):
     """migemm_stream_destroy waits for the stream's work and frees the workspace the
     library held for it; migemm_workspace_release does the same for a caller's stream."""

@@ -211,3 +211,142 @@ def test_c_caller_runtime_on_the_gpu():
     r = c_abi.run("runtime")
     assert r.returncode == 0, r.stdout + r.stderr
     assert "c_abi_check runtime: ok" in r.stdout
+
+
+def _fill_ints(t, seed, lo=-2, hi=2):
+    g = torch.Generator(device=t.device)
+    g.manual_seed(seed)
+    t.copy_(torch.randint(lo, hi + 1, t.shape, device=t.device, generator=g).float())
+
+
+def test_pool_release_never_waits_for_other_queues(rt, nncl):
+    """Thread B queues ~30 ms of GEMMs on its queue over pooled operands; meanwhile thread A
+    grows a buffer of its own (the pool replaces and frees the old one) and releases it. A
+    returns while B's GEMMs are still running (the free is ordered after them on the device,
+    not waited for on the host), B's buffer lookups run meanwhile, and B's product is exact.
+    Then B's own operand is replaced while its GEMM still reads it, and the memory of the
+    old operand is not handed out (and overwritten) before that GEMM has finished."""
+    import time
+    say("runtime pool: release without waiting")
+    n = 8192
+    M = rt.OpenCLBufferManager
+    with rt.ComputeContext() as ctx:
+        qa, qb = ctx.CreateCommandQueue(), ctx.CreateCommandQueue()
+        sb = qb.torch_stream()
+        bufs = {k: M.GetOrCreateBuffer(ctx, f"b_{k}", 4 * n * n) for k in "ABC"}
+        with torch.cuda.stream(sb):
+            _fill_ints(bufs["A"].as_tensor((n, n)), 1)
+            _fill_ints(bufs["B"].as_tensor((n, n)), 2)
+        qb.Finish()
+        with torch.cuda.stream(sb):
+            expect = torch.mm(bufs["A"].as_tensor((n, n)), bufs["B"].as_tensor((n, n)))
+        qb.Finish()
+        res, errors = {}, []
+        queued = threading.Event()
+
+        def thread_b():
+            try:
+                rt.DeviceQueueRegistry.RegisterCurrent(qb)
+                with torch.cuda.stream(sb):
+                    a, b, c = (bufs[k].as_tensor((n, n)) for k in "ABC")
+                    for _ in range(4):
+                        nncl.gemm(a, b, out=c)
+                queued.set()
+                t0 = time.perf_counter()
+                for _ in range(200):
+                    rt.tensor_buffer("b_C", (n, n))
+                res["lookups_s"] = time.perf_counter() - t0
+                res["b_busy_after_lookups"] = not sb.query()
+                rt.DeviceQueueRegistry.Clear()
+            except Exception as e:  # noqa: BLE001
+                errors.append(repr(e))
+                queued.set()
+
+        def thread_a():
+            try:
+                rt.DeviceQueueRegistry.RegisterCurrent(qa)
+                M.GetOrCreateBuffer(ctx, "a_grow", 1 << 20)
+                queued.wait(60)
+                t0 = time.perf_counter()
+                M.GetOrCreateBuffer(ctx, "a_grow", 64 << 20)  # replaces (frees) the 1 MB one
+                M.ReleaseBuffer("a_grow")
+                res["grow_s"] = time.perf_counter() - t0
+                res["b_busy_after_grow"] = not sb.query()
+                rt.DeviceQueueRegistry.Clear()
+            except Exception as e:  # noqa: BLE001
+                errors.append(repr(e))
+
+        ta, tb = threading.Thread(target=thread_a), threading.Thread(target=thread_b)
+        tb.start()
+        ta.start()
+        ta.join()
+        tb.join()
+        assert not errors, errors
+        say("grow", res["grow_s"], "lookups", res["lookups_s"])
+        assert res["b_busy_after_grow"], "A's grow and release waited for B's GEMMs"
+        assert res["grow_s"] < 0.01
+        qb.Finish()
+        assert torch.equal(bufs["C"].as_tensor((n, n)), expect)
+        # B's operand replaced while its GEMM reads it; the old memory must outlive the GEMM
+        rt.DeviceQueueRegistry.RegisterCurrent(qb)
+        with torch.cuda.stream(sb):
+            a, b, c = (bufs[k].as_tensor((n, n)) for k in "ABC")
+            c.zero_()
+            nncl.gemm(a, b, out=c)
+            nncl.gemm(a, b, out=c)
+        M.GetOrCreateBuffer(ctx, "b_A", 8 * n * n)  # a larger "b_A": the old one is released
+        junk = M.GetOrCreateBuffer(ctx, "junk", 4 * n * n)
+        with torch.cuda.stream(qa.torch_stream()):
+            junk.as_tensor((n, n)).fill_(float("nan"))
+        assert not sb.query(), "B's GEMMs finished before the replacement: test too short"
+        qb.Finish()
+        qa.Finish()
+        assert torch.equal(bufs["C"].as_tensor((n, n)), expect)
+        rt.DeviceQueueRegistry.Clear()
+        del a, b, c, expect
+        for q in (qa, qb):
+            q.Dispose()
+
+
+def test_destroyed_context_is_rejected_on_every_thread(rt):
+    """A context destroyed on one thread is rejected on another whose current queue names it
+    (its handle is an id that is never reused): buffer lookups, Tensor.DataBuffer and
+    GetCurrent fail instead of using freed state, and a new context gets another handle."""
+    from my_pytchon_opencl_lib_amd import _native
+    say("runtime: destroyed context")
+    ctx = rt.ComputeContext()
+    q = ctx.CreateCommandQueue()
+    stage, out = threading.Barrier(2, timeout=60), {}
+
+    def other():
+        try:
+            rt.DeviceQueueRegistry.RegisterCurrent(q)
+            out["before"] = rt.tensor_buffer("x", (4,)).numel()
+            stage.wait()   # main destroys the context now
+            stage.wait()
+            p = ctypes.c_void_p()
+            out["tensor_buffer"] = _native.load().migemm_tensor_buffer(b"x", 16, ctypes.byref(p))
+            out["get_current"] = _native.load().migemm_queue_get_current(None, None)
+            out["get_or_create"] = _native.load().migemm_buffer_get_or_create(
+                ctx.handle, b"y", 16, ctypes.byref(p))
+            rt.DeviceQueueRegistry.Clear()
+        except Exception as e:  # noqa: BLE001
+            out["error"] = repr(e)
+            stage.abort()
+
+    th = threading.Thread(target=other)
+    th.start()
+    stage.wait()
+    old = ctx.handle.value
+    ctx.Dispose()
+    fresh = rt.ComputeContext()
+    stage.wait()
+    th.join()
+    assert "error" not in out, out
+    assert out["before"] == 4
+    assert out["tensor_buffer"] == _native.MIGEMM_ERR_INVALID_ARG
+    assert out["get_current"] == _native.MIGEMM_ERR_INVALID_ARG
+    assert out["get_or_create"] == _native.MIGEMM_ERR_INVALID_ARG
+    assert fresh.handle.value != old
+    fresh.Dispose()
+    q.Dispose()

@@ -138,3 +138,48 @@ def test_noalloc_rejects_more_than_its_scratch():
     assert L.migemm_gemm_strided_batched_noalloc(None, 0, 0, 0, 4, 4, None, 4, 0, None, 4, 0,
                                                  None, None, 4, 0, 1, 0) == \
         _native.MIGEMM_ERR_INVALID_ARG
+
+
+def test_noalloc_under_graph_capture():
+    """Callers that cannot allocate include code under HIP graph capture: the no-allocation
+    entry point's split-K GEMM and sliced GEMV are captured on a stream that was never used
+    before, the graph is replayed three times with eager work between the replays, and each
+    replay's outputs equal the existing entry point's eager outputs bit for bit."""
+    from my_pytchon_opencl_lib_amd import _native
+    _native.load()
+    cases = [case(**PAIRS[0][0]), case(**PAIRS[1][0])]
+    s = ctypes.c_void_p()
+    _native.call("migemm_stream_create", ctypes.byref(s))
+    try:
+        eager = []
+        for c in cases:
+            (ref, _), _ = both(s, c)
+            eager.append(ref)
+        say("noalloc under capture")
+        cap = torch.cuda.Stream()
+        outs = [c["C0"].clone() for c in cases]
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            st = ctypes.c_void_p(cap.cuda_stream)
+            for c, C in zip(cases, outs):
+                rc = run("migemm_gemm_strided_batched_noalloc", st, c["ta"], c["tb"], c["M"],
+                         c["N"], c["K"], c["A"], c["B"], c["bias"], C, c["batch"], c["sA"],
+                         c["sB"], c["sC"], c["flags"])
+                assert rc == 0, _native.last_error()
+        size = ctypes.c_size_t(1)
+        _native.call("migemm_workspace_size", ctypes.c_void_p(cap.cuda_stream),
+                     ctypes.byref(size))
+        assert size.value == 0, "the capture allocated a workspace"
+        for rep in range(3):
+            for c, C in zip(cases, outs):
+                C.copy_(c["C0"])
+            noise = torch.mm(cases[0]["A"][0], cases[0]["B"][0])  # eager work between replays
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            for i, C in enumerate(outs):
+                assert np.array_equal(host(C), eager[i]), f"replay {rep}, case {i}"
+            del noise
+    finally:
+        _native.call("migemm_stream_destroy", s)
