@@ -19,30 +19,134 @@
 #include "migemm.h"
 
 static int failures = 0;
+static pthread_mutex_t failures_lock = PTHREAD_MUTEX_INITIALIZER;
 
 #define CHECK(cond, ...)                              \
     do {                                              \
         if (!(cond)) {                                \
+            pthread_mutex_lock(&failures_lock);       \
             fprintf(stderr, "FAIL %s:%d: ", __FILE__, __LINE__); \
             fprintf(stderr, __VA_ARGS__);             \
             fprintf(stderr, "\n");                    \
             ++failures;                               \
+            pthread_mutex_unlock(&failures_lock);     \
         }                                             \
     } while (0)
 
-static int validate(void) {
+/* Argument checks of every entry point; all of them fail before any HIP call, so no GPU is
+ * needed. Run from several threads at once (each thread has its own last-error message). */
+static void *validate_thread(void *arg) {
     float *fake = (float *)(uintptr_t)0x100000;
+    (void)arg;
     CHECK(strlen(migemm_version()) > 0, "empty version");
     int rc = migemm_gemm_strided_batched(NULL, 0, 0, 0, 4, 4, fake, 4, 0, fake + 64, 4, 0, NULL,
                                          fake + 128, 4, 0, 1);
     CHECK(rc == MIGEMM_ERR_INVALID_ARG, "M = 0 gave %d", rc);
-    CHECK(strlen(migemm_last_error()) > 0, "no message for M = 0");
+    CHECK(strstr(migemm_last_error(), "sizes must be >= 1") != NULL, "message for M = 0: %s",
+          migemm_last_error());
     rc = migemm_gemm_strided_batched(NULL, 0, 0, 4, 4, 4, fake, 4, 0, fake, 4, 0, NULL, fake, 4,
                                      0, 1);
     CHECK(rc == MIGEMM_ERR_ALIAS, "aliased output gave %d", rc);
+    rc = migemm_gemm_strided_batched(NULL, 2, 0, 4, 4, 4, fake, 4, 0, fake + 64, 4, 0, NULL,
+                                     fake + 128, 4, 0, 1);
+    CHECK(rc == MIGEMM_ERR_INVALID_ARG, "transA = 2 gave %d", rc);
+    rc = migemm_gemm_strided_batched(NULL, 0, 0, 4, 4, 4, fake, 3, 0, fake + 64, 4, 0, NULL,
+                                     fake + 128, 4, 0, 1);
+    CHECK(rc == MIGEMM_ERR_INVALID_ARG, "lda < K gave %d", rc);
+    rc = migemm_gemm_strided_batched(NULL, 0, 0, 4, 4, 4, fake, 4, 16, fake + 64, 4, 16, NULL,
+                                     fake + 256, 4, 4, 2);
+    CHECK(rc == MIGEMM_ERR_INVALID_ARG, "overlapping batch entries of C gave %d", rc);
+    rc = migemm_gemm_strided_batched(NULL, 0, 0, 1 << 30, 1 << 30, 4, fake, 4, 0, fake, 1 << 30,
+                                     0, NULL, fake, (int64_t)1 << 40, 0, 1);
+    CHECK(rc == MIGEMM_ERR_INVALID_ARG, "overflowing extent gave %d", rc);
+    rc = migemm_gemm_strided_batched_ex(NULL, 0, 0, 4, 4, 4, fake, 4, 0, fake + 64, 4, 0, NULL,
+                                        fake + 128, 4, 0, 1, 4);
+    CHECK(rc == MIGEMM_ERR_INVALID_ARG, "unknown flag gave %d", rc);
+    rc = migemm_gemm_strided_batched_noalloc(NULL, 0, 0, 4, 4, 0, fake, 4, 0, fake + 64, 4, 0,
+                                             NULL, fake + 128, 4, 0, 1, 0);
+    CHECK(rc == MIGEMM_ERR_INVALID_ARG, "noalloc K = 0 gave %d", rc);
     rc = migemm_bmm_tiled(NULL, fake, fake + 64, fake + 128, 4, 4, 4, -1, 0, 16, 2);
     CHECK(rc == MIGEMM_ERR_INVALID_ARG, "negative stride gave %d", rc);
+    rc = migemm_bmm_permute_tiled(NULL, fake, fake + 64, fake + 128, 4, 4, 4, 16, 16, -16, 1, 0, 2);
+    CHECK(rc == MIGEMM_ERR_INVALID_ARG, "negative C stride gave %d", rc);
+    rc = migemm_linear_forward(NULL, fake, fake + 64, NULL, fake + 128, 4, 4, 4, 16, 16, 1);
+    CHECK(rc == MIGEMM_ERR_INVALID_ARG, "linear_forward without bias gave %d", rc);
+    rc = migemm_lstm_gemm_xw(NULL, fake, fake + 64, NULL, fake + 128, 4, 4, 4);
+    CHECK(rc == MIGEMM_ERR_INVALID_ARG, "lstm_gemm_xw without bias gave %d", rc);
+    rc = migemm_lstm_gemm_grad_weights(NULL, fake, fake + 64, fake + 128, fake + 256, fake + 256,
+                                       fake + 512, 2, 3, 4, 5);
+    CHECK(rc == MIGEMM_ERR_ALIAS, "grad_weights with overlapping outputs gave %d", rc);
+    rc = migemm_lstm_recurrent_gates(NULL, fake, fake + 4096, fake + 8192, 2, 3, 4, 3);
+    CHECK(rc == MIGEMM_ERR_INVALID_ARG, "recurrent step 3 of 3 gave %d", rc);
+    rc = migemm_lstm_hid_gates(NULL, fake, fake + 4096, fake + 8192, fake + 12288, NULL,
+                               fake + 16384, fake + 20480, 2, 3, 4, 5, 0);
+    CHECK(rc == MIGEMM_ERR_INVALID_ARG, "hid gates with no H_prev at step 0 gave %d", rc);
+    /* step 1's gates (batch 2 x 20 gates, from workspace + 40) start where H_out starts */
+    rc = migemm_lstm_hid_gates(NULL, fake, fake + 4096, fake + 8192, fake + 12288, fake + 16384,
+                               fake + 20480, fake + 20440, 2, 3, 4, 5, 1);
+    CHECK(rc == MIGEMM_ERR_ALIAS, "hid gates over H_out gave %d", rc);
+    rc = migemm_lstm_hid_gates(NULL, fake, fake + 4096, fake + 8192, fake + 12288, fake + 16384,
+                               fake + 20480, fake + 40960, 2, 3, 4, 5, -1);
+    CHECK(rc == MIGEMM_ERR_INVALID_ARG, "hid gates step -1 gave %d", rc);
+    {
+        int dims[3] = {2, 3, 4}, axes[3] = {0, 2, 2};
+        rc = migemm_tensor_permute(NULL, fake, fake + 64, dims, axes, 3);
+        CHECK(rc == MIGEMM_ERR_INVALID_ARG, "axes with a repeat gave %d", rc);
+        axes[2] = 1;
+        rc = migemm_tensor_permute(NULL, fake, fake + 8, dims, axes, 3);
+        CHECK(rc == MIGEMM_ERR_ALIAS, "permute into its source gave %d", rc);
+        rc = migemm_tensor_permute(NULL, fake, fake + 64, dims, axes, 11);
+        CHECK(rc == MIGEMM_ERR_INVALID_ARG, "11 dimensions gave %d", rc);
+    }
+    rc = migemm_reduce_sum_axis(NULL, fake, fake + 2, 1, 4, 4);
+    CHECK(rc == MIGEMM_ERR_ALIAS, "reduce into its input gave %d", rc);
+    rc = migemm_linear_bias_backward(NULL, fake, fake + 1024, 0, 4);
+    CHECK(rc == MIGEMM_ERR_INVALID_ARG, "no rows gave %d", rc);
+    rc = migemm_linear_weight_grad(NULL, fake, fake + 64, fake + 128, 4, 0, 4, 1);
+    CHECK(rc == MIGEMM_ERR_INVALID_ARG, "K = 0 gave %d", rc);
+    /* runtime services */
+    void *p = NULL, *ctx = NULL, *st = NULL;
+    CHECK(migemm_buffer_get_or_create(NULL, "x", 16, &p) == MIGEMM_ERR_INVALID_ARG, "null ctx");
+    CHECK(migemm_buffer_get_or_create((void *)(uintptr_t)12345, "x", 16, &p) ==
+              MIGEMM_ERR_INVALID_ARG && strstr(migemm_last_error(), "unknown context"),
+          "unknown context accepted");
+    CHECK(migemm_buffer_get_or_create((void *)(uintptr_t)12345, "", 16, &p) ==
+              MIGEMM_ERR_INVALID_ARG, "empty name accepted");
+    CHECK(migemm_queue_register_current((void *)(uintptr_t)12345, NULL) ==
+              MIGEMM_ERR_INVALID_ARG, "null queue accepted");
+    CHECK(migemm_queue_get_current(&ctx, &st) == MIGEMM_ERR_NO_QUEUE, "a queue without register");
+    CHECK(migemm_tensor_buffer("t", 16, &p) == MIGEMM_ERR_NO_QUEUE, "tensor_buffer without queue");
+    CHECK(migemm_queue_clear_current() == MIGEMM_OK, "clear");
+    CHECK(migemm_buffer_release("never-created") == MIGEMM_OK, "release of an unknown name");
+    CHECK(migemm_context_destroy((void *)(uintptr_t)12345) == MIGEMM_ERR_INVALID_ARG,
+          "destroy of an unknown context");
+    CHECK(migemm_context_create(-2, &ctx) == MIGEMM_ERR_INVALID_ARG, "device -2 accepted");
+    {
+        size_t n = 1, b = 1;
+        CHECK(migemm_buffer_count(&n, &b) == MIGEMM_OK && n == 0 && b == 0, "empty pool");
+        CHECK(migemm_workspace_size(NULL, &b) == MIGEMM_OK && b == 0, "workspace of no stream");
+        CHECK(migemm_workspace_size(NULL, NULL) == MIGEMM_ERR_INVALID_ARG, "null size pointer");
+    }
+    /* policy, tuning and the plan record */
+    int prev = -1;
     CHECK(migemm_set_gemm_policy(9, NULL) == MIGEMM_ERR_INVALID_ARG, "policy 9 accepted");
+    CHECK(migemm_set_tuning(MIGEMM_TUNE_TILE, 48, &prev) == MIGEMM_ERR_INVALID_ARG, "tile 48");
+    CHECK(migemm_set_tuning(99, 0, &prev) == MIGEMM_ERR_INVALID_ARG, "tuning key 99");
+    {
+        char plan[8];
+        CHECK(migemm_last_plan(plan, sizeof(plan)) == MIGEMM_OK && strlen(plan) < sizeof(plan),
+              "plan truncation");
+        CHECK(migemm_last_plan(NULL, 4) == MIGEMM_ERR_INVALID_ARG, "null plan buffer");
+    }
+    return NULL;
+}
+
+static int validate(void) {
+    enum { T = 4 };
+    pthread_t th[T];
+    for (int i = 0; i < T; ++i) pthread_create(&th[i], NULL, validate_thread, NULL);
+    for (int i = 0; i < T; ++i) pthread_join(th[i], NULL);
+    validate_thread(NULL);
     return failures;
 }
 
