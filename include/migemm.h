@@ -384,6 +384,18 @@ int migemm_set_tuning(int key, int value, int *previous);
  * buf (NUL-terminated, truncated to len). For tests and tuning; the reference has none. */
 int migemm_last_plan(char *buf, size_t len);
 
+/* The plan migemm_gemm_strided_batched_ex would run for these arguments, written into
+ * plan as by migemm_last_plan, without running it: the arguments are validated the same way
+ * and the dispatcher makes every choice, but nothing is launched, no memory is touched or
+ * allocated and no HIP call is made, so it works without a GPU. The pointers only take
+ * part through their alignment and overlap checks. No counterpart in the reference: for
+ * tests that pin the dispatcher's choices on the CPU. */
+int migemm_gemm_plan(int transA, int transB, int M, int N, int K,
+                     const float *A, int64_t lda, int64_t strideA,
+                     const float *B, int64_t ldb, int64_t strideB,
+                     const float *bias, float *C, int64_t ldc, int64_t strideC,
+                     int batch, int flags, char *plan, size_t plan_len);
+
 #ifdef __cplusplus
 }
 #endif

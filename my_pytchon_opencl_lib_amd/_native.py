@@ -131,6 +131,8 @@ SIGNATURES = {
     "migemm_set_gemm_policy": ([_i32, _ip], _i32),
     "migemm_set_tuning": ([_i32, _i32, _ip], _i32),
     "migemm_last_plan": ([ctypes.c_char_p, _sz], _i32),
+    "migemm_gemm_plan": ([_i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _i64, _i64, _vp,
+                          _vp, _i64, _i64, _i32, _i32, ctypes.c_char_p, _sz], _i32),
 }
 
 _lib = None
@@ -221,4 +223,14 @@ def last_plan():
     """What the last GEMM / permute / column-sum call of this thread ran."""
     buf = ctypes.create_string_buffer(256)
     call("migemm_last_plan", buf, len(buf))
+    return buf.value.decode()
+
+
+def gemm_plan(transA, transB, M, N, K, A, lda, strideA, B, ldb, strideB, bias, C, ldc, strideC,
+              batch=1, flags=0):
+    """The plan string migemm_gemm_strided_batched_ex would run for these arguments, without
+    running it (no GPU needed). A, B, bias and C are integer addresses (None for no bias)."""
+    buf = ctypes.create_string_buffer(256)
+    call("migemm_gemm_plan", int(transA), int(transB), M, N, K, A, lda, strideA, B, ldb,
+         strideB, bias, C, ldc, strideC, batch, flags, buf, len(buf))
     return buf.value.decode()

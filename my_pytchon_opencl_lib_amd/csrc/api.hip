@@ -80,6 +80,19 @@ int hip_check(hipError_t e, const char *what) {
     return set_error(MIGEMM_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+namespace {
+thread_local bool t_plan_only = false;
+// An address that is never dereferenced: the partial-sum buffer of a plan-only dispatch.
+float *const kPlanPlaceholder = reinterpret_cast<float *>(static_cast<uintptr_t>(1) << 12);
+}  // namespace
+
+bool plan_only() { return t_plan_only; }
+
+int launch_status(const char *what) {
+    if (t_plan_only) return MIGEMM_OK;
+    return hip_check(hipGetLastError(), what);
+}
+
 int stream_device(hipStream_t stream, int *device) {
     if (stream == nullptr) {
         MIGEMM_HIP(hipGetDevice(device));
@@ -103,6 +116,10 @@ int stream_device(hipStream_t stream, int *device) {
 // A caller sizes the capturing stream's buffer beforehand with migemm_workspace_reserve or
 // by running the same call once on that stream outside the capture.
 void *workspace(hipStream_t stream, size_t bytes, int *status, int slot) {
+    if (t_plan_only) {
+        *status = MIGEMM_OK;
+        return kPlanPlaceholder;
+    }
     int dev = 0;
     *status = stream_device(stream, &dev);
     if (*status != MIGEMM_OK) return nullptr;
@@ -423,6 +440,27 @@ int migemm_gemm_strided_batched_noalloc(void *stream, int transA, int transB, in
     if (rc != MIGEMM_OK) return rc;
     d.scratch_bytes = MIGEMM_NOALLOC_SCRATCH_BYTES;
     return run_gemm(static_cast<hipStream_t>(stream), d);
+}
+
+int migemm_gemm_plan(int transA, int transB, int M, int N, int K, const float *A, int64_t lda,
+                     int64_t strideA, const float *B, int64_t ldb, int64_t strideB,
+                     const float *bias, float *C, int64_t ldc, int64_t strideC, int batch,
+                     int flags, char *plan, size_t plan_len) {
+    clear_error();
+    if (plan == nullptr || plan_len == 0)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "gemm_plan: null or empty plan buffer");
+    if ((flags & ~MIGEMM_GEMM_ACCUMULATE) != 0)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "gemm_plan: unknown flags 0x%x", flags);
+    GemmDesc d;
+    int rc = validate_gemm(transA, transB, M, N, K, A, lda, strideA, B, ldb, strideB, bias, C,
+                           ldc, strideC, batch, &d);
+    if (rc != MIGEMM_OK) return rc;
+    d.accumulate = (flags & MIGEMM_GEMM_ACCUMULATE) != 0;
+    t_plan_only = true;
+    rc = run_gemm(nullptr, d);
+    t_plan_only = false;
+    if (rc != MIGEMM_OK) return rc;
+    return migemm_last_plan(plan, plan_len);
 }
 
 int migemm_matmul_tiled(void *stream, const float *A, const float *B, float *C, int M, int K,

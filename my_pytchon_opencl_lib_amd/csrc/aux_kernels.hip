@@ -216,12 +216,12 @@ int launch_permute(hipStream_t stream, const float *src, float *dst, const int *
         const int64_t tiles_c = (Cc + 31) / 32;
         if (batch <= 65535 && R <= INT32_MAX && Cc <= INT32_MAX &&
             tiles_r * tiles_c <= INT32_MAX) {
-            hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)(tiles_r * tiles_c),
+            MIGEMM_LAUNCH(transpose_kernel, dim3((unsigned)(tiles_r * tiles_c),
                                                       (unsigned)batch),
                                dim3(256), 0, stream, src, dst, (int)R, (int)Cc, (int)tiles_c);
             record_plan(PlanRecord{"transpose", 32, 32, 1, 0, (int)R, (int)Cc, 0, (int)batch,
                                    false, false});
-            return hip_check(hipGetLastError(), "transpose_kernel launch");
+            return launch_status("transpose_kernel launch");
         }
     }
     // 16-byte elements when the innermost destination axis is the source's contiguous one
@@ -245,13 +245,13 @@ int launch_permute(hipStream_t stream, const float *src, float *dst, const int *
     int64_t blocks = (a.total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     if (vw == 4)
-        hipLaunchKernelGGL(permute_gather_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream,
+        MIGEMM_LAUNCH(permute_gather_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream,
                            a);
     else
-        hipLaunchKernelGGL(permute_gather_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream,
+        MIGEMM_LAUNCH(permute_gather_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream,
                            a);
     record_plan(PlanRecord{"permute_gather", 0, 0, 1, 4 * vw, 0, 0, 0, nd, false, false});
-    return hip_check(hipGetLastError(), "permute_gather_kernel launch");
+    return launch_status("permute_gather_kernel launch");
 }
 
 int launch_column_sum(hipStream_t stream, const float *X, float *Y, int outer, int axis,
@@ -272,12 +272,12 @@ int launch_column_sum(hipStream_t stream, const float *X, float *Y, int outer, i
     const int64_t threads = (int64_t)outer * (vec ? inner / 4 : inner);
     const dim3 grid((unsigned)((threads + 255) / 256), (unsigned)chunks);
     if (vec)
-        hipLaunchKernelGGL(column_sum_kernel<4>, grid, dim3(256), 0, stream, X, dst, outer,
+        MIGEMM_LAUNCH(column_sum_kernel<4>, grid, dim3(256), 0, stream, X, dst, outer,
                            axis, inner, rows, (int)(accumulate && chunks == 1));
     else
-        hipLaunchKernelGGL(column_sum_kernel<1>, grid, dim3(256), 0, stream, X, dst, outer,
+        MIGEMM_LAUNCH(column_sum_kernel<1>, grid, dim3(256), 0, stream, X, dst, outer,
                            axis, inner, rows, (int)(accumulate && chunks == 1));
-    const int rc = hip_check(hipGetLastError(), "column_sum_kernel launch");
+    const int rc = launch_status("column_sum_kernel launch");
     record_plan(PlanRecord{"column_sum", rows, vec ? 4 : 1, chunks, 0, outer, inner, axis, 1,
                            false, false});
     if (rc != MIGEMM_OK || chunks == 1) return rc;
@@ -292,12 +292,12 @@ int launch_shift_rows(hipStream_t stream, const float *H, float *Hp, int total_t
     int64_t blocks = ((vec ? total / 4 : total) + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     if (vec)
-        hipLaunchKernelGGL(shift_rows_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream, H,
+        MIGEMM_LAUNCH(shift_rows_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream, H,
                            Hp, total, seq_len, hidden);
     else
-        hipLaunchKernelGGL(shift_rows_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream, H,
+        MIGEMM_LAUNCH(shift_rows_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream, H,
                            Hp, total, seq_len, hidden);
-    return hip_check(hipGetLastError(), "shift_rows_kernel launch");
+    return launch_status("shift_rows_kernel launch");
 }
 
 }  // namespace migemm

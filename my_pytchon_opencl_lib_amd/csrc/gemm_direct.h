@@ -388,10 +388,10 @@ int launch_direct(hipStream_t s, TiledArgs &a) {
                          (long long)total);
     a.total = (int)total;
     set_tile_divisors(a);
-    hipLaunchKernelGGL((gemm_direct_kernel<BM, BN, WM, WN, AKC, BKC, BK, S, D, OCC, WA, WB>),
+    MIGEMM_LAUNCH((gemm_direct_kernel<BM, BN, WM, WN, AKC, BKC, BK, S, D, OCC, WA, WB>),
                        dim3(a.total),
                        dim3(WM * WN * 64), 0, s, a);
-    return hip_check(hipGetLastError(), "gemm_direct_kernel launch");
+    return launch_status("gemm_direct_kernel launch");
 }
 
 // Every operand layout (NN, NT, TN, TT) with wavefronts of 32x128 (64x64 tiles: 2 x 2

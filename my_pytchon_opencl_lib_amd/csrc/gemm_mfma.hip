@@ -433,9 +433,9 @@ struct TileCfg {
 
 template <int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, bool AV, bool BV>
 int launch_one(hipStream_t s, const TiledArgs &a) {
-    hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, BK, WM, WN, AKC, BKC, AV, BV>),
+    MIGEMM_LAUNCH((gemm_mfma_kernel<BM, BN, BK, WM, WN, AKC, BKC, AV, BV>),
                        dim3(a.total), dim3(WM * WN * 64), 0, s, a);
-    return hip_check(hipGetLastError(), "gemm_mfma_kernel launch");
+    return launch_status("gemm_mfma_kernel launch");
 }
 
 template <int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC>
@@ -498,7 +498,7 @@ int launch_reduce_slices(hipStream_t stream, const float *partial, int slices, i
                        (batch == 1 || strideC == (int64_t)M * N) &&
                        (!wide || ((uintptr_t)C & 15) == 0);
 #define MIGEMM_REDUCE(VW, PLAIN)                                                              \
-    hipLaunchKernelGGL((reduce_slices_kernel<VW, PLAIN>), dim3((unsigned)blocks), dim3(256), 0, \
+    MIGEMM_LAUNCH((reduce_slices_kernel<VW, PLAIN>), dim3((unsigned)blocks), dim3(256), 0, \
                        stream, partial, slices, total, M, N, bias, C, ldc, strideC,            \
                        (int)accumulate)
     if (wide) {
@@ -509,7 +509,7 @@ int launch_reduce_slices(hipStream_t stream, const float *partial, int slices, i
         else MIGEMM_REDUCE(1, false);
     }
 #undef MIGEMM_REDUCE
-    return hip_check(hipGetLastError(), "reduce_slices_kernel launch");
+    return launch_status("reduce_slices_kernel launch");
 }
 
 namespace {

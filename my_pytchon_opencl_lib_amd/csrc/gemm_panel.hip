@@ -364,12 +364,12 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
 template <bool AKC, bool BKC, bool TWO>
 int launch_nw(hipStream_t stream, const PanelArgs &a, int nw) {
     switch (nw) {
-        case 8: hipLaunchKernelGGL((gemm_panel_kernel<8, 1, AKC, BKC, TWO>), dim3(a.total), dim3(8 * 64), 0, stream, a); break;
-        case 4: hipLaunchKernelGGL((gemm_panel_kernel<4, 1, AKC, BKC, TWO>), dim3(a.total), dim3(4 * 64), 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((gemm_panel_kernel<2, 1, AKC, BKC, TWO>), dim3(a.total), dim3(2 * 64), 0, stream, a); break;
-        default: hipLaunchKernelGGL((gemm_panel_kernel<1, 1, AKC, BKC, TWO>), dim3(a.total), dim3(64), 0, stream, a); break;
+        case 8: MIGEMM_LAUNCH((gemm_panel_kernel<8, 1, AKC, BKC, TWO>), dim3(a.total), dim3(8 * 64), 0, stream, a); break;
+        case 4: MIGEMM_LAUNCH((gemm_panel_kernel<4, 1, AKC, BKC, TWO>), dim3(a.total), dim3(4 * 64), 0, stream, a); break;
+        case 2: MIGEMM_LAUNCH((gemm_panel_kernel<2, 1, AKC, BKC, TWO>), dim3(a.total), dim3(2 * 64), 0, stream, a); break;
+        default: MIGEMM_LAUNCH((gemm_panel_kernel<1, 1, AKC, BKC, TWO>), dim3(a.total), dim3(64), 0, stream, a); break;
     }
-    return hip_check(hipGetLastError(), "gemm_panel_kernel launch");
+    return launch_status("gemm_panel_kernel launch");
 }
 
 template <bool TWO>

@@ -331,12 +331,12 @@ int launch_rows(hipStream_t st, const SkinnyArgs &a, int am, int batch) {
     constexpr int per_wg = RW_WAVES * RowsPlan<MR>::RW;
     dim3 grid((a.N + per_wg - 1) / per_wg, batch);
     if (am == 0)
-        hipLaunchKernelGGL((gemv_rows_kernel<MR, 0>), grid, dim3(RW_WAVES * 64), 0, st, a);
+        MIGEMM_LAUNCH((gemv_rows_kernel<MR, 0>), grid, dim3(RW_WAVES * 64), 0, st, a);
     else if (am == 2)
-        hipLaunchKernelGGL((gemv_rows_kernel<MR, 2>), grid, dim3(RW_WAVES * 64), 0, st, a);
+        MIGEMM_LAUNCH((gemv_rows_kernel<MR, 2>), grid, dim3(RW_WAVES * 64), 0, st, a);
     else
-        hipLaunchKernelGGL((gemv_rows_kernel<MR, 1>), grid, dim3(RW_WAVES * 64), 0, st, a);
-    return hip_check(hipGetLastError(), "gemv_rows_kernel launch");
+        MIGEMM_LAUNCH((gemv_rows_kernel<MR, 1>), grid, dim3(RW_WAVES * 64), 0, st, a);
+    return launch_status("gemv_rows_kernel launch");
 }
 
 template <int MR>
@@ -345,10 +345,10 @@ int launch_mr(hipStream_t st, const SkinnyArgs &a, bool vec, int batch) {
     // B is streamed once: non-temporal loads (measured 1x11008x4096: 32.0 us against 36.6 us
     // with ordinary loads, 3 rotating copies of B).
     if (vec)
-        hipLaunchKernelGGL((gemm_skinny_kernel<MR, true, true>), grid, dim3(SK_THREADS), 0, st, a);
+        MIGEMM_LAUNCH((gemm_skinny_kernel<MR, true, true>), grid, dim3(SK_THREADS), 0, st, a);
     else
-        hipLaunchKernelGGL((gemm_skinny_kernel<MR, false, true>), grid, dim3(SK_THREADS), 0, st, a);
-    return hip_check(hipGetLastError(), "gemm_skinny_kernel launch");
+        MIGEMM_LAUNCH((gemm_skinny_kernel<MR, false, true>), grid, dim3(SK_THREADS), 0, st, a);
+    return launch_status("gemm_skinny_kernel launch");
 }
 
 }  // namespace

@@ -314,14 +314,14 @@ template <int MB, int NB, int NW>
 int launch_layout(hipStream_t st, const SmallArgs &a, bool akc, bool bkc) {
     const dim3 grid(a.total), block(NW * 64);
     if (akc && bkc)
-        hipLaunchKernelGGL((gemm_small_kernel<MB, NB, NW, true, true>), grid, block, 0, st, a);
+        MIGEMM_LAUNCH((gemm_small_kernel<MB, NB, NW, true, true>), grid, block, 0, st, a);
     else if (akc)
-        hipLaunchKernelGGL((gemm_small_kernel<MB, NB, NW, true, false>), grid, block, 0, st, a);
+        MIGEMM_LAUNCH((gemm_small_kernel<MB, NB, NW, true, false>), grid, block, 0, st, a);
     else if (bkc)
-        hipLaunchKernelGGL((gemm_small_kernel<MB, NB, NW, false, true>), grid, block, 0, st, a);
+        MIGEMM_LAUNCH((gemm_small_kernel<MB, NB, NW, false, true>), grid, block, 0, st, a);
     else
-        hipLaunchKernelGGL((gemm_small_kernel<MB, NB, NW, false, false>), grid, block, 0, st, a);
-    return hip_check(hipGetLastError(), "gemm_small_kernel launch");
+        MIGEMM_LAUNCH((gemm_small_kernel<MB, NB, NW, false, false>), grid, block, 0, st, a);
+    return launch_status("gemm_small_kernel launch");
 }
 
 template <int MB, int NB = 1>

@@ -188,14 +188,14 @@ int launch_g(hipStream_t st, const TinyArgs &a, bool akc, bool bkc) {
     constexpr int TPW = TWG / KS;  // tiles per work-group
     const dim3 grid((unsigned)((a.total + TPW - 1) / TPW)), block(TWG * 64);
     if (akc && bkc)
-        hipLaunchKernelGGL((gemm_tiny_kernel<true, true, G, KS>), grid, block, 0, st, a);
+        MIGEMM_LAUNCH((gemm_tiny_kernel<true, true, G, KS>), grid, block, 0, st, a);
     else if (akc)
-        hipLaunchKernelGGL((gemm_tiny_kernel<true, false, G, KS>), grid, block, 0, st, a);
+        MIGEMM_LAUNCH((gemm_tiny_kernel<true, false, G, KS>), grid, block, 0, st, a);
     else if (bkc)
-        hipLaunchKernelGGL((gemm_tiny_kernel<false, true, G, KS>), grid, block, 0, st, a);
+        MIGEMM_LAUNCH((gemm_tiny_kernel<false, true, G, KS>), grid, block, 0, st, a);
     else
-        hipLaunchKernelGGL((gemm_tiny_kernel<false, false, G, KS>), grid, block, 0, st, a);
-    return hip_check(hipGetLastError(), "gemm_tiny_kernel launch");
+        MIGEMM_LAUNCH((gemm_tiny_kernel<false, false, G, KS>), grid, block, 0, st, a);
+    return launch_status("gemm_tiny_kernel launch");
 }
 
 int64_t tiles16(const GemmDesc &d) {

@@ -97,6 +97,18 @@ void record_plan(const PlanRecord &p);
 void record_plan(const char *kernel, const GemmDesc &d, int bm, int bn, int splits,
                  int load_bytes);
 
+// Plan-only dispatch (migemm_gemm_plan): on this host thread the launchers make every
+// choice and record the plan exactly as for a real call, but enqueue nothing and make no HIP
+// call: kernel launches go through MIGEMM_LAUNCH, their status through launch_status, and
+// partial-sum / workspace requests return a placeholder address that nothing dereferences.
+bool plan_only();
+#define MIGEMM_LAUNCH(...)                                          \
+    do {                                                            \
+        if (!::migemm::plan_only()) hipLaunchKernelGGL(__VA_ARGS__); \
+    } while (0)
+// hip_check(hipGetLastError(), what) after a launch; MIGEMM_OK when planning only.
+int launch_status(const char *what);
+
 // Launchers. They assume a validated descriptor and only enqueue work.
 int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d);
 int launch_gemm_skinny(hipStream_t stream, const GemmDesc &d);

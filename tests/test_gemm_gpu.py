@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 import torch
 
+import dispatch_cases
 import oracle
 from parity import Tuner, check_full, check_gemm, dev, host, sample_rows
 
@@ -763,43 +764,7 @@ def test_nonfinite_inputs_propagate(nncl, policy, M, K, N, ta, tb):
 
 # Shapes the dispatcher sends to particular kernels under AUTO (the regimes a random-shape audit
 # of the dispatcher found): each is checked against fp64 with the kernel it must run.
-AUTO_REGIMES = [
-    # 5-16 rows over >= 256 MB of B: 32x32 tiles, k split to ~1536 work-groups
-    (dict(batch=16, M=8, K=6000, N=1024, ta=0, tb=0), "tiled-staged tile=32x32 splits=3"),
-    # operands not loadable 16 bytes per lane, short K, large output: 64x64 tiles
-    (dict(batch=1, M=2047, K=61, N=2051, ta=1, tb=1), "tiled-direct tile=64x64"),
-    # 16 or fewer rows: the small kernel, or the short-K kernel for K <= 80
-    (dict(batch=32, M=8, K=195, N=1000, ta=0, tb=0), "small"),
-    (dict(batch=8, M=10, K=75, N=2166, ta=0, tb=0), "tiny"),
-    (dict(batch=32, M=2, K=35, N=7626, ta=1, tb=0), "tiny"),
-    # few 64x64 tiles and K < 256: the small kernel
-    (dict(batch=1, M=1000, K=100, N=700, ta=0, tb=0), "small"),
-    # a weight stored [N, K] at M = 1: rows streamed whole
-    (dict(batch=1, M=1, K=4096, N=2048, ta=0, tb=1), "skinny-rows"),
-    # a tiny output over a huge K (dot products): the small kernel in 256 k ranges
-    (dict(batch=1, M=1, K=1000000, N=1, ta=0, tb=0), "small tile=16x16 splits=256"),
-    (dict(batch=1, M=7, K=300000, N=9, ta=0, tb=1), "small tile=16x16 splits=254"),
-    # outputs of >= 64 MB over K <= 16 with C rows on 128-byte lines: 128x128 tiles
-    (dict(batch=1, M=8192, K=4, N=8192, ta=0, tb=0), "tiled-direct tile=128x128"),
-    # the same with rows off the lines: the short-K kernel
-    (dict(batch=1, M=7008, K=6, N=6220, ta=0, tb=0), "tiny"),
-    # short K, C rows off 64-byte boundaries: 64x64 tiles; on them (operands loaded 4 bytes
-    # per lane, >= 6 rounds of tiles): 128x128
-    (dict(batch=1, M=8192, K=64, N=8180, ta=0, tb=0), "tiled-direct tile=64x64"),
-    (dict(batch=1, M=12592, K=47, N=2304, ta=0, tb=0), "tiled-direct tile=128x128"),
-    # long K over few tiles: 64x64 tiles in k ranges (the LSTM gate gradient)
-    (dict(batch=1, M=6400, K=4096, N=512, ta=0, tb=1), "tiled-direct tile=64x64 splits=3"),
-    # one row of C, B stored [N, K], few rows: the rows GEMV; 3 rows over a batch whose
-    # entries hold small B: the small kernel
-    (dict(batch=1, M=1, K=1301, N=440, ta=0, tb=1), "skinny-rows"),
-    (dict(batch=8, M=3, K=6278, N=362, ta=0, tb=0), "small"),
-    # 3-4 rows over a batch with N % 4 != 0: from 96 MB of B over the batch, the skinny
-    # kernel (below it, the small kernel)
-    (dict(batch=4, M=4, K=11887, N=529, ta=0, tb=0), "skinny tile=0x256"),
-    (dict(batch=8, M=3, K=3350, N=866, ta=0, tb=0), "small"),
-    # a narrow output over long K with 16 MB or more of operands: 1.5x the k ranges
-    (dict(batch=1, M=1846, K=4713, N=17, ta=0, tb=0), "small tile=32x32 splits=8"),
-]
+AUTO_REGIMES = dispatch_cases.AUTO_REGIMES  # shared with the CPU plan test
 
 
 @pytest.mark.parametrize("spec,plan", AUTO_REGIMES)
@@ -818,3 +783,50 @@ def test_auto_regimes(nncl, spec, plan):
         _native.set_gemm_policy(prev)
     check_gemm(C.reshape(b, M, N), A, B, ta, tb, M=M, N=N, K=K, lda=M if ta else K,
                ldb=K if tb else N, sA=M * K, sB=K * N, batch=b, rows=sample_rows(M, 32))
+
+
+def _extent(batch, stride, rows, ld, cols):
+    return (batch - 1) * stride + (rows - 1) * ld + cols
+
+
+PINNED = [(n, s, p, False) for n, s, p in dispatch_cases.BASELINE + dispatch_cases.CALLERS] + \
+    [(str(s), s, p, True) for s, p in AUTO_REGIMES]
+
+
+@pytest.mark.parametrize("name,spec,plan,regime", PINNED, ids=[c[0] for c in PINNED])
+def test_dry_run_plans_match_real_calls(nncl, name, spec, plan, regime):
+    """The plan the dry-run entry point migemm_gemm_plan reports for a call (the CPU test
+    tests/test_plans.py pins those) is the plan the real call runs, for every pinned shape."""
+    dc = dispatch_cases
+    from my_pytchon_opencl_lib_amd import _native
+    a = list(dc.regime_args(spec) if regime else dc.args(**spec))
+    ta, tb, M, N, K, _, lda, sA, _, ldb, sB, _, _, ldc, sC, batch, flags = a
+    offA = (a[5] - dc.BASES["A"]) // 4
+    offC = (a[12] - dc.BASES["C"]) // 4
+    say("dry run vs real call", name)
+    bufs = {
+        "A": torch.zeros(offA + _extent(batch, sA, K if ta else M, lda, M if ta else K),
+                         device="cuda:0"),
+        "B": torch.zeros(_extent(batch, sB, N if tb else K, ldb, K if tb else N),
+                         device="cuda:0"),
+        "C": torch.zeros(offC + _extent(batch, sC, M, ldc, N), device="cuda:0"),
+        "bias": torch.zeros(N, device="cuda:0"),
+    }
+    real = list(a)
+    real[5] = bufs["A"].data_ptr() + 4 * offA
+    real[8] = bufs["B"].data_ptr()
+    real[11] = bufs["bias"].data_ptr() if a[11] is not None else None
+    real[12] = bufs["C"].data_ptr() + 4 * offC
+    prev = _native.set_gemm_policy(_native.MIGEMM_POLICY_AUTO)
+    try:
+        dry = _native.gemm_plan(*real)
+        _native.call("migemm_gemm_strided_batched_ex",
+                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream),
+                     *[ctypes.c_void_p(v) if i in (5, 8, 11, 12) and v is not None else v
+                       for i, v in enumerate(real)])
+        ran = _native.last_plan()
+        torch.cuda.synchronize()
+    finally:
+        _native.set_gemm_policy(prev)
+    assert dry == ran, (dry, ran)
+    assert ran.startswith(plan) if regime else ran == plan, (ran, plan)
