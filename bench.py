@@ -568,8 +568,10 @@ def measure_all_configs(torch, nncl, _native, calls=100):
     copies = [r(4096, 11008) for _ in range(3)]  # 541 MB > the 256 MB MALL
     y = torch.empty(1, 11008, device=dev)
     f5b = [lambda c=c: nncl.gemm(x, c, out=y) for c in copies]
-    # (no torch data floor here: torch's column sum may record a memset node into the graph)
+    # (no graph-replayed torch data floor here: torch's reductions may record a memset node
+    # into a graph; the read floor below is timed eagerly instead)
     rec("5b_gemv", timed(f5b), f5b, vendor=[lambda c=c: torch.mm(x, c, out=y) for c in copies])
+    out["5b_gemv"]["read_floor"] = read_floor(torch, copies, out["5b_gemv"]["us"])
     del copies
 
     def permute_into(src, dst, axes):
@@ -594,6 +596,37 @@ def measure_all_configs(torch, nncl, _native, calls=100):
     out["copy_floor"] = {"us": round(timed([lambda: c1.copy_(c0)]) * 1e3, 2),
                          "kernel": "torch copy of 256 KB, graph-replayed back to back"}
     return out
+
+
+def read_floor(torch, copies, gemv_us, calls=60):
+    """The streaming-read floor of config 5b: torch's own reductions that read each of the
+    same rotating 180 MB copies of B once and write almost nothing (a full sum, a column sum,
+    a full max), timed eagerly (HIP events around `calls` back-to-back calls after a warm-up;
+    each call is ~25 us, longer than its launch, so launches overlap the kernels). The
+    fastest is the floor; x_read_floor = the GEMV's time / the floor."""
+    cands = {"torch.sum(B)": lambda c: torch.sum(c),
+             "B.sum(dim=0)": lambda c: c.sum(dim=0),
+             "torch.amax(B)": lambda c: torch.amax(c)}
+    nbytes = copies[0].numel() * 4
+    res = {}
+    for name, f in cands.items():
+        for c in copies:
+            f(c)
+        torch.cuda.synchronize()
+        t = Timer(torch)
+
+        def run():
+            for i in range(calls):
+                f(copies[i % len(copies)])
+        t.around(run)
+        res[name] = t.mean_ms() * 1e3 / calls
+    best = min(res, key=res.get)
+    us = res[best]
+    return {"us": round(us, 2), "kernel": best, "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "pct_hbm_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 2),
+            "x_read_floor": round(gemv_us / us, 3),
+            "candidates_us": {k: round(v, 2) for k, v in res.items()},
+            "timing": "eager, HIP events around back-to-back calls over the 3 rotating copies"}
 
 
 def measure_callers(torch, nncl, _native):

@@ -342,6 +342,15 @@ class NnClGlob:
                 _ptr(dw), m, k, n, batch)
         return dw
 
+    @staticmethod
+    def reserve_workspace(stream, nbytes):
+        """Sizes the library workspace of `stream` (a torch.cuda.Stream) to at least nbytes
+        per buffer before it is captured into a HIP graph: a capture allocates nothing, and a
+        split GEMM captured on a stream whose workspace is too small fails with
+        MIGEMM_ERR_WORKSPACE (migemm_workspace_reserve)."""
+        _native.call("migemm_workspace_reserve", ctypes.c_void_p(stream.cuda_stream),
+                     int(nbytes))
+
     def gemm(self, a, b, transA=False, transB=False, bias=None, out=None):
         """General 2-D / batched entry point: out = op(a) @ op(b) (+ bias)."""
         _check_tensor("a", a)

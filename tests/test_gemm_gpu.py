@@ -364,7 +364,7 @@ def test_graph_capture_needs_its_own_workspace(nncl):
         with torch.cuda.graph(g, stream=cap):
             nncl.gemm(X, W, out=Y)
     torch.cuda.synchronize()
-    _native.call("migemm_workspace_reserve", ctypes.c_void_p(cap.cuda_stream), 64 << 20)
+    nncl.reserve_workspace(cap, 64 << 20)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=cap):
         nncl.gemm(X, W, out=Y)
