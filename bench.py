@@ -568,10 +568,11 @@ def measure_all_configs(torch, nncl, _native, calls=100):
     copies = [r(4096, 11008) for _ in range(3)]  # 541 MB > the 256 MB MALL
     y = torch.empty(1, 11008, device=dev)
     f5b = [lambda c=c: nncl.gemm(x, c, out=y) for c in copies]
-    # (no graph-replayed torch data floor here: torch's reductions may record a memset node
-    # into a graph; the read floor below is timed eagerly instead)
+    # (no torch data floor here: torch's reductions may record a memset node into a graph,
+    # and they read at ~3.4 TB/s; the read floor below is the library's streaming kernel)
     rec("5b_gemv", timed(f5b), f5b, vendor=[lambda c=c: torch.mm(x, c, out=y) for c in copies])
-    out["5b_gemv"]["read_floor"] = read_floor(torch, copies, out["5b_gemv"]["us"])
+    out["5b_gemv"]["read_floor"] = read_floor(torch, _native, timed, copies,
+                                              out["5b_gemv"]["us"])
     del copies
 
     def permute_into(src, dst, axes):
@@ -598,35 +599,29 @@ def measure_all_configs(torch, nncl, _native, calls=100):
     return out
 
 
-def read_floor(torch, copies, gemv_us, calls=60):
-    """The streaming-read floor of config 5b: torch's own reductions that read each of the
-    same rotating 180 MB copies of B once and write almost nothing (a full sum, a column sum,
-    a full max), timed eagerly (HIP events around `calls` back-to-back calls after a warm-up;
-    each call is ~25 us, longer than its launch, so launches overlap the kernels). The
-    fastest is the floor; x_read_floor = the GEMV's time / the floor."""
-    cands = {"torch.sum(B)": lambda c: torch.sum(c),
-             "B.sum(dim=0)": lambda c: c.sum(dim=0),
-             "torch.amax(B)": lambda c: torch.amax(c)}
+def read_floor(torch, _native, timed, copies, gemv_us):
+    """The streaming-read ceiling of config 5b: the library's read-only streaming kernel
+    (migemm_stream_read: contiguous ranges per work-group, 16-byte non-temporal loads, one
+    sum per work-group written) over the same three rotating 180 MB copies of B, timed the
+    same way as the GEMV (graph replay, 100 calls), at several work-group counts; the
+    fastest is the floor, and x_read_floor = the GEMV's time / the floor."""
     nbytes = copies[0].numel() * 4
-    res = {}
-    for name, f in cands.items():
-        for c in copies:
-            f(c)
-        torch.cuda.synchronize()
-        t = Timer(torch)
+    sums = torch.empty(4096, device=copies[0].device)
+    st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
-        def run():
-            for i in range(calls):
-                f(copies[i % len(copies)])
-        t.around(run)
-        res[name] = t.mean_ms() * 1e3 / calls
+    def call(c, blocks):
+        _native.call("migemm_stream_read", st(), ctypes.c_void_p(c.data_ptr()), c.numel(),
+                     ctypes.c_void_p(sums.data_ptr()), blocks)
+    res = {}
+    for blocks in (344, 688, 1376, 2752, 4096):
+        res[blocks] = timed([lambda c=c, b=blocks: call(c, b) for c in copies]) * 1e3
     best = min(res, key=res.get)
     us = res[best]
-    return {"us": round(us, 2), "kernel": best, "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+    return {"us": round(us, 2), "kernel": f"stream_read_kernel, {best} work-groups",
+            "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
             "pct_hbm_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 2),
             "x_read_floor": round(gemv_us / us, 3),
-            "candidates_us": {k: round(v, 2) for k, v in res.items()},
-            "timing": "eager, HIP events around back-to-back calls over the 3 rotating copies"}
+            "by_work_groups_us": {str(k): round(v, 2) for k, v in res.items()}}
 
 
 def measure_callers(torch, nncl, _native):

@@ -384,6 +384,13 @@ int migemm_set_tuning(int key, int value, int *previous);
  * buf (NUL-terminated, truncated to len). For tests and tuning; the reference has none. */
 int migemm_last_plan(char *buf, size_t len);
 
+/* (5) Measurement. Streams src[0 .. n) once -- `blocks` work-groups, each a contiguous
+ * range, 16-byte non-temporal loads -- and writes the sum of the b-th range to sums[b]. It
+ * has no counterpart in the reference: it measures the read rate a kernel that only
+ * streams reaches on the device, the ceiling the HBM-bound GEMV (M <= 4) is compared with.
+ * n a positive multiple of 4, src 16-byte aligned, 1 <= blocks <= min(65535, n / 4). */
+int migemm_stream_read(void *stream, const float *src, size_t n, float *sums, int blocks);
+
 /* The plan migemm_gemm_strided_batched_ex would run for these arguments, written into
  * plan as by migemm_last_plan, without running it: the arguments are validated the same way
  * and the dispatcher makes every choice, but nothing is launched, no memory is touched or

@@ -131,6 +131,7 @@ SIGNATURES = {
     "migemm_set_gemm_policy": ([_i32, _ip], _i32),
     "migemm_set_tuning": ([_i32, _i32, _ip], _i32),
     "migemm_last_plan": ([ctypes.c_char_p, _sz], _i32),
+    "migemm_stream_read": ([_vp, _vp, _sz, _vp, _i32], _i32),
     "migemm_gemm_plan": ([_i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _i64, _i64, _vp,
                           _vp, _i64, _i64, _i32, _i32, ctypes.c_char_p, _sz], _i32),
 }

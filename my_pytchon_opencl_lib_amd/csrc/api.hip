@@ -733,6 +733,25 @@ int migemm_reduce_sum_axis(void *stream, const float *X, float *Y, int outer_siz
                              inner_size);
 }
 
+int migemm_stream_read(void *stream, const float *src, size_t n, float *sums, int blocks) {
+    clear_error();
+    if (src == nullptr || sums == nullptr)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "stream_read: null pointer argument");
+    if (n == 0 || n % 4 != 0 || (reinterpret_cast<uintptr_t>(src) & 15) != 0)
+        return set_error(MIGEMM_ERR_INVALID_ARG,
+                         "stream_read: n must be a positive multiple of 4 and src 16-byte "
+                         "aligned (n=%zu)", n);
+    if (blocks < 1 || blocks > 65535 || (int64_t)(n / 4) < blocks)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "stream_read: blocks=%d not in [1, min(65535, "
+                         "n/4)]", blocks);
+    if (n > (size_t)kMaxElems)
+        return set_error(MIGEMM_ERR_INVALID_ARG, "stream_read: n=%zu too large", n);
+    if (ranges_overlap(sums, blocks, src, (int64_t)n))
+        return set_error(MIGEMM_ERR_ALIAS, "stream_read: sums overlap src");
+    return launch_stream_read(static_cast<hipStream_t>(stream), src, (int64_t)(n / 4), sums,
+                              blocks);
+}
+
 int migemm_linear_bias_backward(void *stream, const float *grad_output, float *grad_bias,
                                 int total_rows, int N) {
     clear_error();

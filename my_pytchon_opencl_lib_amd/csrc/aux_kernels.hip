@@ -171,7 +171,48 @@ __global__ void __launch_bounds__(256) shift_rows_kernel(const float *__restrict
     }
 }
 
+// The streaming-read reference of the HBM-bound kernels (the GEMV of BASELINE config 5b):
+// reads n4 float4 once, each work-group a contiguous range, every lane RS_U 16-byte
+// non-temporal loads in flight, and writes one sum per work-group so the loads stay live.
+// What it reaches is the read rate a kernel that only streams can get on the box.
+constexpr int RS_U = 16;
+__global__ void __launch_bounds__(256) stream_read_kernel(const float4 *__restrict__ src,
+                                                          int64_t n4, int64_t per,
+                                                          float *__restrict__ sums) {
+    typedef float vec __attribute__((ext_vector_type(4)));
+    const int64_t lo = (int64_t)blockIdx.x * per;
+    const int64_t hi = lo + per < n4 ? lo + per : n4;
+    const vec *s = reinterpret_cast<const vec *>(src);
+    vec acc = vec{0.f, 0.f, 0.f, 0.f};
+    for (int64_t i = lo + threadIdx.x; i < hi; i += 256 * RS_U) {
+        vec v[RS_U];
+#pragma unroll
+        for (int u = 0; u < RS_U; ++u) {
+            const int64_t j = i + (int64_t)u * 256;
+            v[u] = j < hi ? __builtin_nontemporal_load(s + j) : vec{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int u = 0; u < RS_U; ++u) acc += v[u];
+    }
+    __shared__ float part[256];
+    part[threadIdx.x] = acc[0] + acc[1] + acc[2] + acc[3];
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) sums[blockIdx.x] = part[0];
+}
+
 }  // namespace
+
+int launch_stream_read(hipStream_t stream, const float *src, int64_t n4, float *sums,
+                       int blocks) {
+    const int64_t per = (n4 + blocks - 1) / blocks;
+    MIGEMM_LAUNCH(stream_read_kernel, dim3(blocks), dim3(256), 0, stream,
+                  reinterpret_cast<const float4 *>(src), n4, per, sums);
+    return launch_status("stream_read_kernel launch");
+}
 
 int launch_permute(hipStream_t stream, const float *src, float *dst, const int *src_dims,
                    const int *axes, int num_dims, int64_t total) {

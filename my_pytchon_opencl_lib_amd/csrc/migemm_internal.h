@@ -176,6 +176,10 @@ int launch_permute(hipStream_t stream, const float *src, float *dst,
 int launch_column_sum(hipStream_t stream, const float *X, float *Y,
                       int outer, int axis, int inner, bool accumulate = false);
 
+// sums[b] = sum of the b-th of `blocks` contiguous ranges of src[0 .. 4 n4), streamed once.
+int launch_stream_read(hipStream_t stream, const float *src, int64_t n4, float *sums,
+                       int blocks);
+
 // Hp[t] = H[t - 1] when t % seq_len > 0, else 0 (rows of `hidden` floats).
 int launch_shift_rows(hipStream_t stream, const float *H, float *Hp, int total_tokens,
                       int seq_len, int hidden);

@@ -276,6 +276,24 @@ def test_config5b_gemv(nncl):
     assert np.array_equal(C, C2)
 
 
+@pytest.mark.parametrize("n,blocks", [(4, 1), (4096, 7), (1 << 20, 688), (180 * 256, 4096)])
+def test_stream_read_sums_its_ranges(nncl, n, blocks):
+    """migemm_stream_read (the streaming-read reference of the GEMV's roofline) reads every
+    element once: each work-group's sum is the sum of its contiguous range."""
+    from my_pytchon_opencl_lib_amd import _native
+    rng = np.random.default_rng(n + blocks)
+    x = rng.integers(-3, 4, size=n).astype(np.float32)
+    sums = torch.full((blocks,), float("nan"), device="cuda:0")
+    xd = dev(x)
+    _native.call("migemm_stream_read", ctypes.c_void_p(torch.cuda.current_stream().cuda_stream),
+                 ctypes.c_void_p(xd.data_ptr()), n, ctypes.c_void_p(sums.data_ptr()), blocks)
+    n4 = n // 4
+    per = -(-n4 // blocks)
+    expect = [x[4 * b * per:4 * min(n4, (b + 1) * per)].astype(np.int64).sum()
+              for b in range(blocks)]
+    assert np.array_equal(host(sums), np.array(expect, dtype=np.float32))
+
+
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
 def test_skinny_rows_and_bias(nncl, policy, M):
     K, N = 1000, 1030  # N not a multiple of 4 -> scalar loads; K not a slice multiple
