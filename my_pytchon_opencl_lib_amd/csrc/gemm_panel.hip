@@ -184,32 +184,9 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
         // operands are issued first and k-row operands interleaved by instruction, so those
         // loads are the oldest PEEL of the 8.
         constexpr int PEEL = 4 * ((int)AKC + (int)BKC) + ((int)!AKC + (int)!BKC);
-        auto issue = [&](int j, int slot) {
-            const int g = j < ng ? j : ng - 1;
-            const char *ag, *bg;
-            uint32_t ao[4], bo[4];
-            if constexpr (TWO) {
-                // wave-uniform choice of the pair that holds absolute k-group g0 + g
-                const int ga = g0 + g;
-                const bool second = ga >= p.G1;
-                const int gl = second ? ga - p.G1 : ga;
-                ag = second ? abase2 + (int64_t)gl * astep2 : abase + (int64_t)gl * astep;
-                bg = second ? bbase2 + (int64_t)gl * bstep2 : bbase + (int64_t)gl * bstep;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    ao[q] = second ? aoffs2[q] : aoffs[q];
-                    bo[q] = second ? boffs2[q] : boffs[q];
-                }
-            } else {
-                ag = abase + (int64_t)g * astep;
-                bg = bbase + (int64_t)g * bstep;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    ao[q] = aoffs[q];
-                    bo[q] = boffs[q];
-                }
-            }
-            float *st = my + slot * PSTAGE;
+        // the 8 loads of one k-group from operand bases ag / bg with lane offsets ao / bo
+        auto issue_from = [&](const char *ag, const char *bg, const uint32_t(&ao)[4],
+                              const uint32_t(&bo)[4], float *st) {
             if constexpr (AKC) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) dma16(ag, ao[q], st + 1024 + 256 * q);
@@ -222,6 +199,24 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
             for (int q = 0; q < 4; ++q) {
                 if constexpr (!AKC) dma16(ag, ao[q], st + 1024 + 256 * q);
                 if constexpr (!BKC) dma16(bg, bo[q], st + 256 * q);
+            }
+        };
+        auto issue = [&](int j, int slot) {
+            const int g = j < ng ? j : ng - 1;
+            float *st = my + slot * PSTAGE;
+            if constexpr (TWO) {
+                // absolute k-group g0 + g: a wave-uniform branch to the pair that holds it
+                // (per-lane selects of the 8 offsets cost ~35 instructions per k-group)
+                const int ga = g0 + g;
+                if (ga >= p.G1)
+                    issue_from(abase2 + (int64_t)(ga - p.G1) * astep2,
+                               bbase2 + (int64_t)(ga - p.G1) * bstep2, aoffs2, boffs2, st);
+                else
+                    issue_from(abase + (int64_t)ga * astep, bbase + (int64_t)ga * bstep, aoffs,
+                               boffs, st);
+            } else {
+                issue_from(abase + (int64_t)g * astep, bbase + (int64_t)g * bstep, aoffs, boffs,
+                           st);
             }
         };
         // Fragments of sub-group j (k = 8j .. 8j+7 of the k-group), step s: B lane l holds
