@@ -91,7 +91,8 @@ def parse():
     p.add_argument("--pmc-target", nargs="?", const="4096",
                    choices=["4096", "1", "2a", "2b", "3", "3h", "5a", "5b", "a5t", "a5h",
                             "floor"],
-                   help="run only one workload for rocprofv3 --pmc passes, each 3 times: '4096' "
+                   help="run only one workload for rocprofv3 --pmc passes (3 launches, 21 "
+                        "for the short configs): '4096' "
                         "the three 4096^3 forms, '1' / '2a' / '2b' / '3' / '5a' / '5b' that "
                         "BASELINE config, '3h' config 3 in the stateful x_t W + h_{t-1} U "
                         "form, 'a5t' / 'a5h' the 4096^2 [1,0] and the [0,2,1,3] "
@@ -321,32 +322,36 @@ def main():
 
 
 def pmc_target(torch, nncl, which="4096"):
-    """One workload, 3 launches, for rocprofv3 --pmc passes; then the copy reference."""
+    """One workload for rocprofv3 --pmc passes, then the copy reference: 3 launches of each
+    4096^3 form, of 5a, 5b (one per copy of B) and the 4096^2 permute; 21 of the short configs
+    (1, 2a, 2b, 3, 3h, the head permute and the launch floor), whose per-dispatch counters
+    vary more (the summary takes each counter's median over the launches)."""
     g = torch.Generator(device="cuda:0")
     g.manual_seed(0)
     dev = torch.device("cuda:0")
     r = lambda *s: torch.rand(*s, device=dev, generator=g) * 2 - 1
     if which == "1":
         A, B, C = r(256, 256), r(256, 256), torch.empty(256, 256, device=dev)
-        calls = [lambda: nncl.gemm(A, B, out=C)] * 3
+        calls = [lambda: nncl.gemm(A, B, out=C)] * 21
     elif which in ("2a", "2b"):
         if which == "2a":
             X, Y, Z = r(32, 128, 64), r(32, 64, 128), torch.empty(32, 128, 128, device=dev)
         else:
             X, Y, Z = r(32, 128, 128), r(32, 128, 64), torch.empty(32, 128, 64, device=dev)
-        calls = [lambda: nncl.gemm(X, Y, out=Z)] * 3
+        calls = [lambda: nncl.gemm(X, Y, out=Z)] * 21
     elif which == "3":
         X = torch.randn(3, 64, 1536, device=dev, generator=g)
         W = r(1536, 4096) / 32
         bias = r(4096) / 32
         Y = torch.empty(64, 4096, device=dev)
-        calls = [lambda i=i: nncl.gemm(X[i], W, bias=bias, out=Y) for i in range(3)]
+        calls = [lambda i=i: nncl.gemm(X[i], W, bias=bias, out=Y) for i in range(3)] * 7
     elif which == "3h":
         Xs = torch.randn(64, 3, 512, device=dev, generator=g)
         Wx, Uh, bias = r(512, 4096) / 32, r(1024, 4096) / 32, r(4096) / 32
         Hp, Ho = r(64, 1024), r(64, 3, 1024)
         ws = torch.empty(3, 64, 4096, device=dev)
-        calls = [lambda t=t: nncl.LstmHidGates(Xs, Wx, Uh, bias, Hp, Ho, ws, t) for t in range(3)]
+        calls = [lambda t=t: nncl.LstmHidGates(Xs, Wx, Uh, bias, Hp, Ho, ws, t)
+                 for t in range(3)] * 7
     elif which == "5a":
         A, B, C = r(1000, 777), r(777, 3000), torch.empty(1000, 3000, device=dev)
         calls = [lambda: nncl.gemm(A, B, out=C)] * 3
@@ -360,10 +365,10 @@ def pmc_target(torch, nncl, which="4096"):
         calls = [lambda: nncl.Permute(T, [1, 0])] * 3
     elif which == "a5h":
         H = r(32, 128, 16, 64)
-        calls = [lambda: nncl.Permute(H, [0, 2, 1, 3])] * 3
+        calls = [lambda: nncl.Permute(H, [0, 2, 1, 3])] * 21
     elif which == "floor":
         z = torch.empty(1, device=dev)
-        calls = [lambda: z.fill_(1.0)] * 3
+        calls = [lambda: z.fill_(1.0)] * 21
     else:
         n = N4096
         A = torch.randn(n, n, device=dev, generator=g) / 64
@@ -472,7 +477,12 @@ def graph_timed(torch, cap, fns, per):
         for _ in range(per):
             for f in fns:
                 f()
-    graph.replay()
+    # Warm replays for at least ~20 ms of device time first, so every config is timed at the
+    # clocks of sustained load rather than partly during the ramp after shorter work.
+    w = Timer(torch)
+    w.around(graph.replay)
+    for _ in range(min(200, int(20.0 / max(w.mean_ms(), 1e-3)))):
+        graph.replay()
     torch.cuda.synchronize()
     t = Timer(torch)
     for _ in range(5):

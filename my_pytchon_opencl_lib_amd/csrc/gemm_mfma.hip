@@ -519,6 +519,36 @@ namespace {
 bool rows16(const float *p, int64_t ld, int64_t stride) {
     return ((uintptr_t)p & 15) == 0 && ld % 4 == 0 && stride % 4 == 0;
 }
+
+// The tile cost model. A macro-tile shape runs at a fitted rate with a fixed per-tile
+// overhead of `over` k-steps: time = rounds of 256 work-groups (one round as long as one
+// tile) x 2 x tile area x (K + over) / rate. Fitted to NN at 4096 x K x 4096, K = 256 ..
+// 4096, in one process on one box; every dispatcher rule below that weighs tile shapes
+// takes its constants from these tables.
+struct TileFit {
+    double rate;  // TFLOP/s (kElementFit: relative to 256x256)
+    double over;  // k-steps per tile
+};
+enum TileShape { T64 = 0, T128 = 1, T128x256 = 2, T256 = 3 };
+// operands loaded straight into LDS (gemm_direct_kernel, 16-byte aligned rows)
+constexpr TileFit kDirectFit[4] = {{135.2, 95}, {147.6, 90}, {152.1, 98}, {152.6, 75}};
+// register-staged kernels (other 128-bit operands)
+constexpr TileFit kStagedFit[4] = {{134.2, 75}, {138.9, 78}, {140.6, 99}, {147.2, 73}};
+// element-wise loads (M, N or K not a multiple of 4): the earlier three-shape model, rates
+// relative to 256x256; 256x256 work-groups fill a CU alone, their prologue and C store not
+// overlapped (about 32 k-steps per tile, 16 for 128x256). 64x64 at 0.91: fitted first to
+// five shapes (graph replay, us, 64x64 / 128x128: 1231 x 4246 x 7348 NT 598 / 745, batch-8
+// 701 x 1107 x 1602 TT 166 / 209, 12000 x 500 x 6565 702 / 633, 6000 x 1000 x 6001 595 /
+// 542, 4096 x 4095 x 4095 980 / 951 with 256x256 at 941), then raised from 0.88 on 49
+// audited outputs of 256-16384 per side (picks' time above the per-shape best 1.13 -> 0.84
+// %) and checked on 40 others: 5 picks changed, each 2-12 % faster (8948 x 1088 x 3283
+// 558.0 -> 489.6), 0.5 % less in total.
+constexpr TileFit kElementFit[4] = {{0.91, 0}, {0.966, 0}, {0.981, 16}, {1.0, 32}};
+// Operands loaded 4 bytes per lane (not 16-byte aligned rows) lower the rates of split
+// 64x64 and 128x128 tiles to these fractions (long-K regime below).
+constexpr double kUnalignedRate64 = 0.85, kUnalignedRate128 = 0.95;
+// Split-K partial sums cost (2S + 1) M N 4 bytes of HBM traffic at this rate (bytes / us).
+constexpr double kPartialBytesPerUs = 6e6;
 }  // namespace
 
 int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
@@ -574,19 +604,20 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     const int direct_mode = tuning(MIGEMM_TUNE_DIRECT);
     const bool fits = direct_mode != 1 && d.lda <= (1 << 21) && d.ldb <= (1 << 21);
     const bool direct = fits && wa == 4 && wb == 4;
-    // Estimated time (us) of `t` tiles of `area` outputs over k at a fitted rate (TFLOP/s)
-    // with a per-tile overhead of o k-steps: the work-groups are dealt over the 256 CUs in
-    // rounds, each round as long as one tile.
-    auto est = [](int64_t t, double area, double k, double o, double rate) {
-        return (double)((t + 255) / 256) * 256.0 * 2.0 * area * (k + o) / (rate * 1e6);
+    // Estimated time (us) of `t` tiles of `area` outputs over k at a fitted rate (TFLOP/s,
+    // scaled by `scale`) with its per-tile overhead: the work-groups are dealt over the 256
+    // CUs in rounds, each round as long as one tile.
+    auto est = [](int64_t t, double area, double k, TileFit f, double scale = 1.0) {
+        return (double)((t + 255) / 256) * 256.0 * 2.0 * area * (k + f.over) /
+               (f.rate * scale * 1e6);
     };
     // Whole 128x256 or 256x256 tiles (loaded straight into LDS) instead of 64x64 ones for
     // outputs with few 128x128 tiles, when the estimate says so: 8000 x 4096 x 1000 runs
     // 476.1 us in 128x256 tiles against 538.9 in 64x64, 1000 x 4096 x 8000 TN 485.6 / 519.0,
     // 8000 x 1024 x 1000 131.6 / 147.0.
     auto wider = [&](double c64, int &cfg_out, int &big_out) {
-        const double c1 = est(tiles(128, 256), 32768, d.K, 98, 152.1);
-        const double c2 = est(tiles(256, 256), 65536, d.K, 75, 152.6);
+        const double c1 = est(tiles(128, 256), 32768, d.K, kDirectFit[T128x256]);
+        const double c2 = est(tiles(256, 256), 65536, d.K, kDirectFit[T256]);
         if (c1 < c64 && c1 <= c2) {
             cfg_out = 128;
             big_out = 1;
@@ -623,25 +654,28 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         // 128-split 249.7, 64x64 198.4 (chosen); 500 x 12000 x 6565 TN 128-split 685.0
         // (chosen), 64x64 722.4; 12000 x 6565 x 500 NT 128-split 669.8, 64x64 633.1 (chosen).
         // 64x64 tiles are also weighed in 2-4 ranges, and operands loaded 4 bytes per lane
-        // (not `direct`) lower the rates of 64x64 and 128x128 tiles to 0.85 and 0.95: on 30
+        // (not `direct`) lower the rates of 64x64 and 128x128 tiles (kUnalignedRate*): on 30
         // shapes of this regime (K 4096-16384, every tile and range count timed) the picks'
         // time above the per-shape best fell from 7.1 % to 2.7 % (800 x 5000 x 2500 NT 213.4
         // -> 184.0 us in four 64x64 ranges, 160 x 10116 x 11952 490.6 -> 418.7, the LSTM
         // gate gradient 6400 x 4096 x 512 NT 230.9 -> 220.3 in three).
-        const double e64 = direct ? 1.0 : 0.85, e128 = direct ? 1.0 : 0.95;
-        auto traffic = [&](int s) { return (2.0 * s + 1) * d.M * d.N * 4.0 * d.batch / 6e6; };
+        const double e64 = direct ? 1.0 : kUnalignedRate64;
+        const double e128 = direct ? 1.0 : kUnalignedRate128;
+        auto traffic = [&](int s) {
+            return (2.0 * s + 1) * d.M * d.N * 4.0 * d.batch / kPartialBytesPerUs;
+        };
         const int64_t t128 = tiles(128, 128), t256 = tiles(256, 256), t64 = tiles(64, 64);
         int64_t want = (1024 + t128 - 1) / t128;
         want += want & 1;
         const int s128 = (int)(want < 8 ? want : 8);
         double best =
-            est(t128 * s128, 16384, (double)d.K / s128, 78, 138.9 * e128) + traffic(s128);
+            est(t128 * s128, 16384, (double)d.K / s128, kStagedFit[T128], e128) + traffic(s128);
         cfg = 128;
         splits = s128;
         if (av && bv && (t256 == 32 || t256 == 64)) {
             const int s256 = (int)(256 / t256);
-            const double c = est(256, 65536, (double)d.K / s256, direct ? 75 : 73,
-                                 direct ? 152.6 : 147.2) + traffic(s256);
+            const double c = est(256, 65536, (double)d.K / s256,
+                                 direct ? kDirectFit[T256] : kStagedFit[T256]) + traffic(s256);
             if (c < best) {
                 best = c;
                 big = 2;
@@ -649,7 +683,7 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
             }
         }
         for (int s = 1; s <= 4 && fits; ++s) {
-            const double c = est(t64 * s, 4096, (double)d.K / s, 95, 135.2 * e64) +
+            const double c = est(t64 * s, 4096, (double)d.K / s, kDirectFit[T64], e64) +
                              (s > 1 ? traffic(s) : 0.0);
             if (c < best) {
                 best = c;
@@ -676,7 +710,8 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         if (t64 >= 256 && t64 < 320 && nk32 >= 24 &&
             (d.K >= 2048 || (t64 % 256 != 0 && d.K >= 768)))
             splits = 3;
-        if (direct && splits == 1 && cfg == 64) wider(est(t64, 4096, d.K, 95, 135.2), cfg, big);
+        if (direct && splits == 1 && cfg == 64)
+            wider(est(t64, 4096, d.K, kDirectFit[T64]), cfg, big);
     } else {
         cfg = 64;
         const int64_t t64 = tiles(64, 64);
@@ -691,23 +726,15 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
     }
     // Large outputs: pick the macro-tile by the busiest CU's share of the work. The work-
     // groups are dealt over the 256 CUs, so a CU carries ceil(tiles / 256) tiles of area x
-    // (K + a per-tile overhead), at each tile's own rate. The rates and overheads are fitted
-    // to NN at 4096 x K x 4096, K = 256 .. 4096 (time = tiles per CU x area x (K + o) /
-    // rate), in one process on one box:
-    //   operands loaded straight into LDS (gemm_direct_kernel; 16-byte aligned rows):
-    //     256x256 152.6 TFLOP/s, o = 75; 128x256 152.1, o = 98; 128x128 147.6, o = 90;
-    //     64x64 135.2, o = 95;
-    //   register-staged kernels (other 128-bit operands): 256x256 147.2, o = 73; 128x256
-    //     140.6, o = 99; 128x128 138.9, o = 78; 64x64 134.2, o = 75.
-    // The tile count's quantization then decides: 3072 x 1024 x 3072 runs 168.7 us in 64x64
+    // (K + a per-tile overhead), at each tile's own rate (kDirectFit, kStagedFit,
+    // kElementFit). The tile count's quantization then decides: 3072 x 1024 x 3072 runs 168.7 us in 64x64
     // tiles (9 per CU) against 190.1 in 128x128 (2.25 per CU); 4096 x 256 x 4096 74.4 in
     // 256x256 against 82.1 in 128x128. (Outputs of 256-511 tiles of 128x128 stay on 64x64
     // tiles: one 4-wavefront work-group per CU hides latency poorly, 2048 x 1024 x 2048 TN
     // 81.0 us in direct 64x64 tiles against 86.3 in 128x128.)
-    // Element-wise loads (M, N or K not a multiple of 4) keep the earlier three-shape model:
-    // 256x256 work-groups fill a CU alone, their prologue and C store not overlapped (about
-    // 32 k-steps per tile, 16 for 128x256), which decides short K: 12000 x 6565 x 500 runs
-    // 729 us at 128x128, 747 at 256x256.
+    // Element-wise loads (M, N or K not a multiple of 4) keep the earlier three-shape model
+    // (kElementFit), whose 256x256 overhead decides short K: 12000 x 6565 x 500 runs 729 us
+    // at 128x128, 747 at 256x256.
     // C's rows start on 64-byte boundaries (every batch entry's too)
     const bool rows64 = d.ldc % 16 == 0 && ((uintptr_t)d.C & 63) == 0 &&
                         (d.batch == 1 || d.sC % 16 == 0);
@@ -719,9 +746,10 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
         big = 0;
     } else if (cfg == 128 && splits == 1 && tiles(128, 128) >= 512) {
         const double k = d.K;
-        auto cost = [&](int bm, int bn, double rate, double over) {
-            return (double)((tiles(bm, bn) + 255) / 256) * bm * bn * (k + over) / rate;
+        auto cost = [&](int bm, int bn, TileFit f, double over) {
+            return (double)((tiles(bm, bn) + 255) / 256) * bm * bn * (k + over) / f.rate;
         };
+        const TileFit *fit = direct ? kDirectFit : av && bv ? kStagedFit : kElementFit;
         if (av && bv) {
             double c64, c0, c1, c2;
             if (direct) {
@@ -756,15 +784,16 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
                 // other work-groups' k loops hide it (12000 x 500 x 6565 NT 728 in 128x256
                 // tiles, 787 in 64x64).
                 const double om = !rows64 && d.K <= 256 ? 110.0 : 0.0;
-                c64 = cost(64, 64, 135.2, 95);
-                c0 = cost(128, 128, 147.6, 90 * s + om);
-                c1 = cost(128, 256, 152.1, 98 * s + om);
-                c2 = cost(256, 256, 152.6, 75 * s + (om > 0 ? om : cmis ? 75 * s : 0.0));
+                c64 = cost(64, 64, fit[T64], fit[T64].over);
+                c0 = cost(128, 128, fit[T128], fit[T128].over * s + om);
+                c1 = cost(128, 256, fit[T128x256], fit[T128x256].over * s + om);
+                const double o256 = fit[T256].over * s;
+                c2 = cost(256, 256, fit[T256], o256 + (om > 0 ? om : cmis ? o256 : 0.0));
             } else {
-                c64 = cost(64, 64, 134.2, 75);
-                c0 = cost(128, 128, 138.9, 78);
-                c1 = cost(128, 256, 140.6, 99);
-                c2 = cost(256, 256, 147.2, 73);
+                c64 = cost(64, 64, fit[T64], fit[T64].over);
+                c0 = cost(128, 128, fit[T128], fit[T128].over);
+                c1 = cost(128, 256, fit[T128x256], fit[T128x256].over);
+                c2 = cost(256, 256, fit[T256], fit[T256].over);
             }
             const double best = std::min(std::min(c64, c0), std::min(c1, c2));
             cfg = best == c64 ? 64 : 128;
@@ -782,17 +811,11 @@ int launch_gemm_tiled(hipStream_t stream, const GemmDesc &d) {
             cfg = rows64 && tiles(128, 128) >= 1536 ? 128 : 64;
             big = 0;
         } else {
-            // 64x64 tiles weigh in at 0.91 of the 256x256 rate. Fitted first to five shapes
-            // (graph replay, us, 64x64 / 128x128: 1231 x 4246 x 7348 NT 598 / 745, batch-8
-            // 701 x 1107 x 1602 TT 166 / 209, 12000 x 500 x 6565 702 / 633, 6000 x 1000 x
-            // 6001 595 / 542, 4096 x 4095 x 4095 980 / 951 with 256x256 at 941; the estimate
-            // picks the faster in all five), then raised from 0.88 on 49 audited outputs of
-            // 256-16384 per side (picks' time above the per-shape best 1.13 -> 0.84 %) and
-            // checked on 40 others: 5 picks changed, each 2-12 % faster (8948 x 1088 x 3283
-            // 558.0 -> 489.6), 0.5 % less in total.
-            const double c64 = fits ? cost(64, 64, 0.91, 0) : 1e300;
-            const double c0 = cost(128, 128, 0.966, 0), c1 = cost(128, 256, 0.981, 16);
-            const double c2 = cost(256, 256, 1.0, 32);
+            // element-wise loads: kElementFit (64x64 only where gemm_direct_kernel applies)
+            const double c64 = fits ? cost(64, 64, fit[T64], fit[T64].over) : 1e300;
+            const double c0 = cost(128, 128, fit[T128], fit[T128].over);
+            const double c1 = cost(128, 256, fit[T128x256], fit[T128x256].over);
+            const double c2 = cost(256, 256, fit[T256], fit[T256].over);
             const double best = std::min(std::min(c64, c0), std::min(c1, c2));
             cfg = best == c64 ? 64 : 128;
             big = best == c2 ? 2 : (best == c1 ? 1 : 0);
