@@ -7,7 +7,8 @@ One step = the three GEMMs of BASELINE config 4 on synthetic N(0, 1/64) data res
   TN  dB = A^T * dC    (autograd gradient of B)
 each M = N = K = 4096, 2*4096^3 FLOP. `value` is the whole step's FLOP / wall time.
 
-Prints ONE JSON line on stdout. Besides the step it carries, by default:
+Prints ONE JSON line on stdout. Besides the step (and, in config.torch_blas_forms, torch's
+own fp32 GEMM of the three forms on the same tensors) it carries, by default:
   configs            every other BASELINE config timed on this GPU (HIP events around HIP-graph
                      replays of back-to-back calls), with its roofline fraction, the launch
                      floor (a one-element fill kernel replayed the same way), for the small
@@ -271,6 +272,23 @@ def main():
     achieved = FLOP_4096 / (dom_ms * 1e-3) / 1e12
     value = 3 * FLOP_4096 / (ms_per_step * 1e-3) / 1e12
 
+    # torch's own fp32 GEMM (hipBLASLt) on the same tensors and forms, for comparison only
+    vendor_forms = {
+        "NN": lambda: torch.mm(A, B, out=C),
+        "NT": lambda: torch.mm(dC, B.t(), out=dA),
+        "TN": lambda: torch.mm(A.t(), dC, out=dB),
+    }
+    torch_blas = {}
+    for k, f in vendor_forms.items():
+        for _ in range(5):
+            f()
+        vt = Timer(torch)
+        for _ in range(10):
+            vt.around(f)
+        ms = vt.mean_ms()
+        torch_blas[k] = {"ms": round(ms, 4),
+                         "tflops": round(FLOP_4096 / (ms * 1e-3) / 1e12, 2)}
+
     configs = measure_all_configs(torch, nncl, _native) if args.configs == "all" else None
     callers = measure_callers(torch, nncl, _native) if args.configs == "all" else None
     ref = None if args.no_reference else reference_same_gpu(per_form["NN"]["ms"])
@@ -310,6 +328,7 @@ def main():
         "config": {"workload": "BASELINE config 4: fp32 4096x4096x4096 NN forward + NT "
                                "(dA = dC*B^T) + TN (dB = A^T*dC), one step = all three",
                    "M": n, "N": n, "K": n, "forms": per_form,
+                   "torch_blas_forms": torch_blas,
                    "pct_of_fp32_matrix_peak": round(100 * value / PEAK_FP32_MFMA_TFLOPS, 2),
                    "parallelism": "single GPU"},
         "roofline": roofline,
