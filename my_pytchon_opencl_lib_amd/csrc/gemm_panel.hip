@@ -116,6 +116,19 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
         const int nb = n0 + (threadIdx.x & 7) * 4;
         if (p.bias != nullptr && nb < p.N) bias4 = *reinterpret_cast<const f4u *>(p.bias + nb);
     }
+    // Likewise the C group a thread adds onto (accumulate) when each thread stores one group
+    // (NW >= 4): in the epilogue its latency was ~0.15 us of the 64 x 1024 x 4096 recurrent
+    // step. C overlaps no operand (the entry points reject aliasing) and only this thread
+    // writes it, after the k loop.
+    constexpr bool CPRE = NW * 64 >= PT * PT / 4;
+    f4 c4 = f4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (CPRE) {
+        const int mi = threadIdx.x >> 3;
+        const int nq = (threadIdx.x & 7) * 4;
+        if (p.accumulate && mi < PT && m0 + mi < p.M && n0 + nq < p.N)
+            c4 = *reinterpret_cast<const f4u *>(p.C + (int64_t)bb * p.sC +
+                                                (int64_t)(m0 + mi) * p.ldc + n0 + nq);
+    }
 
     float *my = ring + w * D * PSTAGE;
     f16 acc;
@@ -347,7 +360,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_panel_kernel(PanelArgs p) {
         if (m < p.M && n < p.N) {  // N % 4 == 0: the whole group is inside
             if (p.bias != nullptr) v = v + bias4;
             f4u *c = reinterpret_cast<f4u *>(Cb + (int64_t)m * p.ldc + n);
-            if (p.accumulate) v = *c + v;
+            if (p.accumulate) v = (CPRE ? c4 : f4(*c)) + v;
             *c = v;
         }
     }
