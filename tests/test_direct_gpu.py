@@ -216,8 +216,10 @@ def test_small_kernel_32x32_tiles_exact(ta, tb):
 # A is transposed), in every operand layout: ragged M (1, 17, 33, 63, 65; rounded up to a
 # multiple of 4 for a transposed A) and N (4, 36, 260), K with 1, 2, 4, 8 and more k-groups
 # (so 1, 2, 4 and 8 wavefronts, uneven shares), batches with bias and the accumulating
-# epilogue.
+# epilogue (whose C group is loaded at kernel start with 4 or more wavefronts, in the
+# epilogue with 1 or 2).
 PANEL_SHAPES = [(1, 32, 4, 1, False, False), (17, 64, 36, 2, True, False),
+                (5, 32, 8, 2, True, True), (20, 64, 68, 2, False, True),
                 (33, 128, 260, 3, False, True), (63, 256, 100, 1, True, True),
                 (65, 1536, 4096, 1, True, False), (64, 800, 516, 2, False, False),
                 (128, 2048, 260, 1, True, True), (40, 4096, 68, 1, False, False)]
