@@ -84,7 +84,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=25)
     p.add_argument("--configs", default="all", choices=["main", "all"],
                    help="'all' (default) also times every other BASELINE config")
-    p.add_argument("--cpu-seconds", type=float, default=12.0,
+    p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="target duration of the bounded CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-reference", action="store_true",
