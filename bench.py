@@ -515,7 +515,8 @@ def measure_all_configs(torch, nncl, _native, calls=100):
     launch, ~8 us, is spread over 100 calls as for the floor), 5 replays averaged. Inputs
     rotate where BASELINE repeats a config over many inputs (config 3: 100 timesteps) or the
     working set must exceed the 256 MB MALL (config 5b: three copies of B). The launch floor
-    is a one-element fill kernel replayed the same way."""
+    is a one-element fill kernel replayed the same way, right before and after each config
+    (x_launch_floor is taken to their mean)."""
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(0)
@@ -527,14 +528,24 @@ def measure_all_configs(torch, nncl, _native, calls=100):
         return graph_timed(torch, cap, fns, per or max(1, calls // len(fns)))
 
     z = torch.empty(1, device=dev)
-    floor_us = timed([lambda: z.fill_(1.0)]) * 1e3
-    out["launch_floor"] = {"us": round(floor_us, 2),
-                           "kernel": "torch fill of 1 element, graph-replayed back to back"}
+    fill = [lambda: z.fill_(1.0)]
+    floors = []
 
-    def rec(name, ms, fns, floor=None, vendor=None):
-        """floor = (torch op description, fns): a torch kernel that reads the config's input
-        bytes and writes its output bytes, timed the same way (the data-movement floor)."""
+    def local_floor():
+        us = timed(fill) * 1e3
+        floors.append(us)
+        return us
+
+    def rec(name, fns, floor=None, vendor=None, per=None):
+        """Times the config's calls `fns` with the launch floor right before and after it
+        (the clock state of a light load can change between minutes of one run, so the ratio
+        is taken to the floor of the same moment). floor = (torch op description, fns): a
+        torch kernel that reads the config's input bytes and writes its output bytes, timed
+        the same way (the data-movement floor)."""
         flop, byts, bound = CONFIGS[name]
+        f0 = local_floor()
+        ms = timed(fns, per)
+        floor_us = (f0 + local_floor()) / 2
         tf = flop / (ms * 1e-3) / 1e12
         gbs = byts / (ms * 1e-3) / 1e9
         fns[0]()
@@ -545,6 +556,7 @@ def measure_all_configs(torch, nncl, _native, calls=100):
                      "frac": round((tf / PEAK_FP32_MFMA_TFLOPS) if bound == "mfma"
                                    else (gbs / PEAK_HBM_GBS), 4),
                      "x_launch_floor": round(ms * 1e3 / floor_us, 2),
+                     "launch_floor_us": round(floor_us, 2),
                      "kernel": _native.last_plan()}
         if floor is not None:
             fl_ms = timed(floor[1])
@@ -559,18 +571,18 @@ def measure_all_configs(torch, nncl, _native, calls=100):
     f1 = [lambda: nncl.gemm(A, B, out=C)]
     # Data-movement floors of the small configs: one torch elementwise kernel that reads
     # the config's operands and writes its output (the same bytes, no arithmetic to speak of).
-    rec("1_nn_256", timed(f1), f1,
+    rec("1_nn_256", f1,
         ("torch.add(A, B, out=C): reads A and B, writes C", [lambda: torch.add(A, B, out=C)]),
         [lambda: torch.mm(A, B, out=C)])
     Q, Kt, P, V = r(32, 128, 64), r(32, 64, 128), r(32, 128, 128), r(32, 128, 64)
     S, O = torch.empty(32, 128, 128, device=dev), torch.empty(32, 128, 64, device=dev)
     f2a = [lambda: nncl.gemm(Q, Kt, out=S)]
-    rec("2a_bmm_qk", timed(f2a), f2a,
+    rec("2a_bmm_qk", f2a,
         ("torch.cat([Q, K^T], out=S): reads Q and K^T, writes S (2 MB each way)",
          [lambda: torch.cat([Q.view(-1), Kt.view(-1)], out=S.view(-1))]),
         [lambda: torch.bmm(Q, Kt, out=S)])
     f2b = [lambda: nncl.gemm(P, V, out=O)]
-    rec("2b_bmm_pv", timed(f2b), f2b,
+    rec("2b_bmm_pv", f2b,
         ("torch.addcmul(V, P[..., :64], P[..., 64:], out=O): reads P and V, writes O",
          [lambda: torch.addcmul(V, P[..., :64], P[..., 64:], out=O)]),
         [lambda: torch.bmm(P, V, out=O)])
@@ -579,7 +591,7 @@ def measure_all_configs(torch, nncl, _native, calls=100):
     bias = r(4096) / 32
     Y = torch.empty(64, 4096, device=dev)
     f3 = [lambda i=i: nncl.gemm(X[i], W, bias=bias, out=Y) for i in range(100)]
-    rec("3_lstm_gate_step", timed(f3, per=1), f3,
+    rec("3_lstm_gate_step", f3, per=1,
         vendor=[lambda i=i: torch.addmm(bias, X[i], W, out=Y) for i in range(100)])
     del X
     # the stateful form: 100 steps of one sequence chunk, step 0 from the incoming state
@@ -588,18 +600,18 @@ def measure_all_configs(torch, nncl, _native, calls=100):
     Hp, Ho = r(64, 1024), r(64, 100, 1024)
     ws = torch.empty(100, 64, 4096, device=dev)
     f3h = [lambda t=t: nncl.LstmHidGates(Xs, Wx, Uh, bias, Hp, Ho, ws, t) for t in range(100)]
-    rec("3h_lstm_hid_step", timed(f3h, per=1), f3h)
+    rec("3h_lstm_hid_step", f3h, per=1)
     del Xs, Ho, ws
     A5, B5, C5 = r(1000, 777), r(777, 3000), torch.empty(1000, 3000, device=dev)
     f5a = [lambda: nncl.gemm(A5, B5, out=C5)]
-    rec("5a_ragged", timed(f5a), f5a, vendor=[lambda: torch.mm(A5, B5, out=C5)])
+    rec("5a_ragged", f5a, vendor=[lambda: torch.mm(A5, B5, out=C5)])
     x = r(1, 4096)
     copies = [r(4096, 11008) for _ in range(3)]  # 541 MB > the 256 MB MALL
     y = torch.empty(1, 11008, device=dev)
     f5b = [lambda c=c: nncl.gemm(x, c, out=y) for c in copies]
     # (no torch data floor here: torch's reductions may record a memset node into a graph,
     # and they read at ~3.4 TB/s; the read floor below is the library's streaming kernel)
-    rec("5b_gemv", timed(f5b), f5b, vendor=[lambda c=c: torch.mm(x, c, out=y) for c in copies])
+    rec("5b_gemv", f5b, vendor=[lambda c=c: torch.mm(x, c, out=y) for c in copies])
     out["5b_gemv"]["read_floor"] = read_floor(torch, _native, timed, copies,
                                               out["5b_gemv"]["us"])
     del copies
@@ -614,17 +626,21 @@ def measure_all_configs(torch, nncl, _native, calls=100):
 
     T, Tt = r(4096, 4096), torch.empty(4096, 4096, device=dev)
     fpt = [lambda: permute_into(T, Tt, [1, 0])]
-    rec("a5_permute_4096_t", timed(fpt), fpt,
+    rec("a5_permute_4096_t", fpt,
         ("torch Tt.copy_(T.t()): torch's own transpose copy", [lambda: Tt.copy_(T.t())]))
     H, Hp = r(32, 128, 16, 64), torch.empty(32, 16, 128, 64, device=dev)
     fph = [lambda: permute_into(H, Hp, [0, 2, 1, 3])]
-    rec("a5_permute_heads_0213", timed(fph), fph,
+    rec("a5_permute_heads_0213", fph,
         ("torch Hp.copy_(H.permute(0, 2, 1, 3))", [lambda: Hp.copy_(H.permute(0, 2, 1, 3))]))
     # the floor of a kernel that must read its input before it writes: a torch device copy
     # of 256 KB (one 256^2 operand) replayed the same way
     c0, c1 = r(256, 256), torch.empty(256, 256, device=dev)
     out["copy_floor"] = {"us": round(timed([lambda: c1.copy_(c0)]) * 1e3, 2),
                          "kernel": "torch copy of 256 KB, graph-replayed back to back"}
+    out["launch_floor"] = {"us": round(float(np.median(floors)), 2),
+                           "min_us": round(min(floors), 2), "max_us": round(max(floors), 2),
+                           "kernel": "torch fill of 1 element, graph-replayed back to back, "
+                                     "timed before and after every config (median here)"}
     return out
 
 
