@@ -100,6 +100,10 @@ def parse():
                         "head-split permutes, 'floor' the one-element fill kernel; then a 256 MiB "
                         "device copy 3 times (the reference for scaling FETCH_SIZE / "
                         "WRITE_SIZE to bytes)")
+    p.add_argument("--decompose", action="store_true",
+                   help="only fit fixed cost + per-unit slope of the panel kernel (M = 64, "
+                        "N = 4096, K = 256 .. 2048) and of 64x64 tiles (1-4 work-groups per "
+                        "CU), from graph-timed sweeps; prints one JSON line")
     p.add_argument("--summarize-trace", metavar="DIR",
                    help="summarise the rocprofv3 --kernel-trace CSV under DIR, made from "
                         "'bench.py --steps S --warmup W' (pass the same --steps / --warmup)")
@@ -224,6 +228,10 @@ def main():
 
     if args.pmc_target:
         pmc_target(torch, NnClGlob("cuda:0"), args.pmc_target)
+        return
+    if args.decompose:
+        print(json.dumps({"decompose": decompose(torch, NnClGlob("cuda:0"), _native)}),
+              flush=True)
         return
     nncl = NnClGlob("cuda:0")
     dev = torch.device("cuda:0")
@@ -667,6 +675,90 @@ def read_floor(torch, _native, timed, copies, gemv_us):
             "pct_hbm_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 2),
             "x_read_floor": round(gemv_us / us, 3),
             "by_work_groups_us": {str(k): round(v, 2) for k, v in res.items()}}
+
+
+def decompose(torch, nncl, _native):
+    """Fixed cost and per-unit slope of the kernels behind configs 3 and 5a, from graph-timed
+    sweeps (HIP graphs of 100 calls as for the configs, the launch floor timed beside each
+    point), fitted by least squares:
+      panel: C = A B + bias with M = 64, N = 4096 and K = 256 .. 2048, A rotating over 100
+        inputs as in config 3 (K = 1536; the recurrent step has K = 1024): t(K) = fixed +
+        K x slope. Each SIMD runs 2 of the 8 wavefronts of its tile, 8 K MFMA cycles in all,
+        so 8 / slope is the clock the k loop runs at;
+      tiled: 64x64 tiles at K = 768 with 1, 2, 3 and 4 co-resident work-groups per CU
+        (config 5a has three): t(n) = fixed + n x slope; a work-group adds 24 576 MFMA cycles
+        per SIMD, so 24 576 / slope is again a clock.
+    The fixed part beside the launch floor is what a launch costs beyond the MFMA work: the
+    gap between kernels, the first loads, the reduction and the epilogue."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    cap = torch.cuda.Stream()
+    z = torch.empty(1, device=dev)
+
+    def timed_us(fns, per=None):
+        return graph_timed(torch, cap, fns, per or max(1, 100 // len(fns))) * 1e3
+
+    def point(fns, per=None):
+        f0 = timed_us([lambda: z.fill_(1.0)])
+        us = timed_us(fns, per)
+        f1 = timed_us([lambda: z.fill_(1.0)])
+        return us, (f0 + f1) / 2
+
+    def fit(xs, ys):
+        slope, fixed = np.polyfit(np.asarray(xs, float), np.asarray(ys, float), 1)
+        pred = fixed + slope * np.asarray(xs, float)
+        resid = float(np.max(np.abs(pred - np.asarray(ys, float))))
+        return float(fixed), float(slope), resid
+
+    out = {}
+    r = lambda *s: torch.rand(*s, device=dev, generator=g) * 2 - 1
+    ks, ts, floors, plans = (256, 512, 768, 1024, 1280, 1536, 2048), [], [], []
+    for K in ks:
+        X = torch.randn(100, 64, K, device=dev, generator=g)
+        W = r(K, 4096) / 32
+        bias = r(4096) / 32
+        Y = torch.empty(64, 4096, device=dev)
+        fns = [lambda i=i: nncl.gemm(X[i], W, bias=bias, out=Y) for i in range(100)]
+        fns[0]()
+        plans.append(_native.last_plan().split(" M=")[0])
+        us, fl = point(fns, per=1)
+        ts.append(us)
+        floors.append(fl)
+        del X, W
+    fixed, slope, resid = fit(ks, ts)
+    out["panel"] = {
+        "shape": "64 x K @ K x 4096 + bias, A rotating over 100 inputs",
+        "points_us": {str(k): round(t, 2) for k, t in zip(ks, ts)},
+        "launch_floor_us": round(float(np.mean(floors)), 2), "plans": sorted(set(plans)),
+        "fixed_us": round(fixed, 2), "slope_us_per_k": round(slope, 5),
+        "max_residual_us": round(resid, 3),
+        "k_loop_clock_ghz": round(8 / (slope * 1e3), 3),
+        "mfma_us_at_2_4_ghz": {"config3_K1536": round(8 * 1536 / 2400, 2),
+                               "recurrent_K1024": round(8 * 1024 / 2400, 2)}}
+    shapes = {1: (1024, 1024), 2: (1024, 2048), 3: (1536, 2048), 4: (2048, 2048)}
+    ns, ts, floors, plans = [], [], [], []
+    for n, (M, N) in shapes.items():
+        A, B, C = r(M, 768), r(768, N), torch.empty(M, N, device=dev)
+        fns = [lambda: nncl.gemm(A, B, out=C)]
+        with _native.tuned(tile=64, splitk=1):
+            fns[0]()
+            plans.append(_native.last_plan().split(" M=")[0])
+            us, fl = point(fns)
+        ns.append(n)
+        ts.append(us)
+        floors.append(fl)
+        del A, B, C
+    fixed, slope, resid = fit(ns, ts)
+    out["tiled64"] = {
+        "shape": "M x 768 @ 768 x N in 64x64 tiles, 256 n tiles (n per CU)",
+        "points_us": {str(n): round(t, 2) for n, t in zip(ns, ts)},
+        "launch_floor_us": round(float(np.mean(floors)), 2), "plans": sorted(set(plans)),
+        "fixed_us": round(fixed, 2), "slope_us_per_workgroup": round(slope, 3),
+        "max_residual_us": round(resid, 3),
+        "k_loop_clock_ghz": round(24576 / (slope * 1e3), 3),
+        "slope_tflops": round(256 * 2 * 64 * 64 * 768 / (slope * 1e-6) / 1e12, 1)}
+    return out
 
 
 def measure_callers(torch, nncl, _native):
