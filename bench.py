@@ -48,7 +48,7 @@ PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense FP32 matrix peak (AMD public speci
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 N4096 = 4096
 FLOP_4096 = 2.0 * N4096 ** 3
-EVENT_EVERY = 4  # timed steps per step whose launches carry HIP events
+EVENT_EVERY = 2  # timed steps per step whose launches carry HIP events
 TRACE_SUMMARY = os.path.join(ROOT, "profiles", "gemm_direct_4096_kernel_trace.md")
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemm_direct_4096_pmc.md")
 # GPU box: one GPU's share of the host is 16 threads (OMP_NUM_THREADS there)
@@ -263,8 +263,9 @@ def main():
             f()
     torch.cuda.synchronize()
 
-    # Per-launch HIP events on every EVENT_EVERY-th timed step only: an event pair around
-    # each launch added ~0.9 % to the step's wall time (2.759 against 2.735 ms per step).
+    # Per-launch HIP events on one timed step in EVENT_EVERY only: an event pair around every
+    # launch added ~0.9 % to the step's wall time (2.762 against 2.737 ms per step), on every
+    # 4th step ~0.2 %, but 5 samples per form at 20 steps left the mean noisy.
     t0 = time.perf_counter()
     for i in range(args.steps):
         for k, f in forms.items():
@@ -314,8 +315,8 @@ def main():
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
                 "traffic": load_traffic(dominant),
                 "algorithmic_per_launch": {"flop": FLOP_4096, "bytes": 4 * 3 * n * n},
-                "measured_by": f"HIP events around each launch of every {EVENT_EVERY}th timed "
-                               f"step, on the launch stream, this run"}
+                "measured_by": f"HIP events around each launch of one timed step in "
+                               f"{EVENT_EVERY}, on the launch stream, this run"}
     if dominant in prof:
         pus = prof[dominant]
         roofline["profiled_us"] = pus
